@@ -1,0 +1,175 @@
+/*
+ * tf_attn.h - C ABI of libtf_attn.so, the MI355X (gfx950) full-attention path.
+ *
+ * Drop-in boundary: the Python method
+ *   Qwen3_8FullAttention._slot_based_attention(q, layer_k_buffer,
+ *                                              layer_v_buffer, batch)
+ * (reference qwen3_8/full_attention.py:163-283) and the KV write just before it
+ * (qwen3_8/full_attention.py:146-149).  The reference has no FFI: its host
+ * side calls these entry points through ctypes (tokenfactory_amd/_native.py).
+ *
+ * Conventions
+ *  - Every pointer argument is a device pointer unless stated otherwise; the
+ *    library never allocates, frees or retains device memory.
+ *  - Index tensors keep the reference's dtype: int64 (req_to_token,
+ *    req_pool_indices, seq_lens, out_cache_loc; ForwardBatch,
+ *    qwen3_8/forward_batch.py:19-31).  Work lists made by the planners are int32.
+ *  - KV pools are one layer's [pool_slots, num_kv_heads, head_dim] block
+ *    (qwen3_8/hybrid_cache_pool.py:96-106, 151-154), row-major, in bf16 or in
+ *    OCP fp8-e4m3 with per-tensor fp32 scales (k_scale / v_scale, device
+ *    scalars; ignored for bf16).  Slot 0 is the padding slot
+ *    (token_to_kv_pool.py:20-23); req_to_token holds -1 for empty positions
+ *    (req_to_token_pool.py:13-16).  Slot ids read from req_to_token are clamped
+ *    into [0, pool_slots) so a bad id cannot fault the GPU.
+ *  - q / out are [T, num_q_heads, head_dim] bf16 with a free token stride
+ *    (q_row_stride / out_row_stride, in elements); heads and dims are dense.
+ *  - q head h reads kv head h / (num_q_heads / num_kv_heads)
+ *    (repeat_interleave semantics, qwen3_8/full_attention.py:191-193).
+ *  - Request b of the batch owns context positions [0, L_b) with
+ *    L_b = seq_lens[b] (or seq_len_override when > 0: the reference's bsz == 1
+ *    branch takes L from max_seq_len, full_attention.py:186), of which the last
+ *    ext_b are new; new token t attends to positions 0 .. L_b - ext_b + t
+ *    (full_attention.py:200-208, 234-238, 266-278).
+ *  - Work is enqueued on `stream` (NULL = the null stream); no call
+ *    synchronises the device.
+ *  - Return value: TF_OK (0) or a negative TF_ERR_* code; tf_attn_last_error()
+ *    then describes the failure (thread-local string).
+ */
+#ifndef TF_ATTN_H_
+#define TF_ATTN_H_
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct ihipStream_t* tf_stream_t; /* hipStream_t */
+
+enum {
+  TF_DTYPE_BF16 = 0,
+  TF_DTYPE_FP8_E4M3 = 1,
+  TF_DTYPE_FP32 = 2
+};
+
+enum {
+  TF_OK = 0,
+  TF_ERR_INVALID = -1,     /* bad shape, size, pointer or alignment */
+  TF_ERR_UNSUPPORTED = -2, /* valid but not implemented (head_dim, dtype, group) */
+  TF_ERR_HIP = -3          /* a HIP runtime call failed */
+};
+
+/* Integer ABI revision; bumped whenever a signature below changes. */
+int32_t tf_attn_abi_version(void);
+
+/* Message for the last non-zero return on the calling thread ("" if none). */
+const char* tf_attn_last_error(void);
+
+/* ------------------------------------------------------------------ decode
+ * Split-K decode attention: one new token per request (ext_b == 1).
+ * Replaces the pure-decode branch, full_attention.py:215-242, and the
+ * ext_len == 1 case of the bsz == 1 branch, full_attention.py:179-213.
+ *
+ * Processes n_items requests.  Item i is batch entry items[i] (or i when
+ * items is NULL) and reads / writes query row q_rows[i] (or items[i] / i when
+ * q_rows is NULL) of q and out.
+ *
+ * workspace: device scratch of tf_attn_decode_workspace_bytes(...) bytes that
+ * is zero-filled before its first use; every call leaves it zero-filled again
+ * (it holds split partials and arrival counters).  Calls that overlap in time
+ * must not share a workspace.
+ * chunk_tokens: context tokens per workgroup (multiple of 64), or 0 to let the
+ * library choose from max_seq_len and n_items.
+ * max_seq_len: an upper bound of every L_b processed (host int, as
+ * ForwardBatch.max_seq_len).
+ */
+int64_t tf_attn_decode_workspace_bytes(int32_t n_items, int32_t num_q_heads,
+                                       int32_t num_kv_heads, int32_t head_dim,
+                                       int32_t max_seq_len, int32_t chunk_tokens);
+
+int32_t tf_attn_decode(const void* q, int64_t q_row_stride,
+                       const void* k_pool, const void* v_pool, int64_t pool_slots,
+                       int32_t kv_dtype, const float* k_scale, const float* v_scale,
+                       const int64_t* req_to_token, int64_t rtt_rows,
+                       int64_t rtt_row_stride, int64_t rtt_cols,
+                       const int64_t* req_pool_indices, const int64_t* seq_lens,
+                       int32_t seq_len_override,
+                       const int32_t* items, const int32_t* q_rows, int32_t n_items,
+                       int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
+                       float scale, void* out, int64_t out_row_stride,
+                       void* workspace, int64_t workspace_bytes,
+                       int32_t max_seq_len, int32_t chunk_tokens, tf_stream_t stream);
+
+/* ------------------------------------------------------------------ extend
+ * Causal prefill / extend attention over cached prefix + new tokens, bf16
+ * MFMA, flash-style.  Replaces the extend / mixed branch,
+ * full_attention.py:244-283, and the ext_len > 1 case of the bsz == 1 branch,
+ * full_attention.py:179-213.
+ *
+ * work: device int32 [n_work][8] from tf_attn_plan_extend(); one entry per
+ * (request, kv head, tile of 128 (token, q-head) rows).
+ */
+int32_t tf_attn_extend(const void* q, int64_t q_row_stride,
+                       const void* k_pool, const void* v_pool, int64_t pool_slots,
+                       int32_t kv_dtype, const float* k_scale, const float* v_scale,
+                       const int64_t* req_to_token, int64_t rtt_rows,
+                       int64_t rtt_row_stride, int64_t rtt_cols,
+                       const int64_t* req_pool_indices, const int64_t* seq_lens,
+                       int32_t seq_len_override,
+                       const int32_t* work, int32_t n_work,
+                       int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
+                       float scale, void* out, int64_t out_row_stride,
+                       tf_stream_t stream);
+
+/* ------------------------------------------------------------------ planning
+ * Host-side work planning (all pointers are HOST pointers; no GPU needed).
+ *
+ * tf_attn_plan_extend: for the requests with extend_lens[b] > 1 (all of them
+ * when decode_to_decode_kernel == 0) writes extend work items
+ * {b, kv_head, row0, q_start_b, ext_b, 0, 0, 0} into work (capacity entries)
+ * and returns their count, or a negative error.  q_start_b is the first row of
+ * request b in the flattened q (exclusive prefix sum of extend_lens, as
+ * full_attention.py:250-256).  Items are ordered request by request, largest
+ * extend first, kv heads inner, later (heavier) row tiles first.
+ *
+ * tf_attn_plan_decode_items: lists the requests with extend_lens[b] == 1 in
+ * items (batch index) and q_rows (their row in q); returns the count.
+ */
+int32_t tf_attn_plan_extend(const int64_t* extend_lens, int32_t batch_size,
+                            int32_t num_q_heads, int32_t num_kv_heads,
+                            int32_t decode_to_decode_kernel,
+                            int32_t* work, int32_t capacity);
+
+int32_t tf_attn_plan_decode_items(const int64_t* extend_lens, int32_t batch_size,
+                                  int32_t* items, int32_t* q_rows, int32_t capacity);
+
+/* ------------------------------------------------------------------ KV write
+ * k_pool[out_cache_loc[t]] = k[t]; v_pool[out_cache_loc[t]] = v[t]
+ * (full_attention.py:146-149).  k / v: [n_tokens, num_kv_heads, head_dim] in
+ * src_dtype (bf16 or fp32) with token stride src_row_stride (elements).  For an
+ * fp8 pool each element is stored as e4m3(clamp(x / scale, -448, 448)), round
+ * to nearest even.  Slots outside [0, pool_slots) are skipped.
+ */
+int32_t tf_kv_write(const void* k, const void* v, int64_t src_row_stride,
+                    int32_t src_dtype, const int64_t* out_cache_loc, int64_t n_tokens,
+                    void* k_pool, void* v_pool, int64_t pool_slots, int32_t kv_dtype,
+                    const float* k_scale, const float* v_scale,
+                    int32_t num_kv_heads, int32_t head_dim, tf_stream_t stream);
+
+/* ------------------------------------------------------------------ gather
+ * Padded slot gather of the batched branches (full_attention.py:216-220):
+ * out[b, t] = pool[max(req_to_token[req_pool_indices[b], t], 0)] for
+ * t < max_len, bit-exact.  out: [batch, max_len, row_elems] in the pool dtype.
+ * Used to check the kernels' token-granular gather against PyTorch indexing.
+ */
+int32_t tf_gather_kv(const void* pool, int32_t kv_dtype, int64_t pool_slots,
+                     int64_t row_elems, const int64_t* req_to_token, int64_t rtt_rows,
+                     int64_t rtt_row_stride, int64_t rtt_cols,
+                     const int64_t* req_pool_indices, int32_t batch_size,
+                     int32_t max_len, void* out, tf_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* TF_ATTN_H_ */

@@ -1,0 +1,278 @@
+"""Pins the CPU oracle independently of its own formulas (CPU only).
+
+Two independent statements of the reference's attention semantics - the op-for-op
+PyTorch restatement (``oracle.slot_attention``) and the float64 loop oracle
+(``oracle.brute``) - are checked against each other and against facts that do
+not restate either: closed-form special cases, invariances of the slot
+indirection, the reference's own cache-equivalence property
+(``tests/test_hybrid_radix_cache.py:111-223`` of the reference), and planted
+mistakes that must each break at least one pin.
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle.brute import attention_brute, attention_dense
+from oracle.slot_attention import gather_kv_ref, slot_based_attention_ref
+from tests.helpers import as_numpy, brute, rebatch, restatement, small_case
+
+CASES = [
+    # (seq_lens, ext_lens, hq, hkv) covering the three reference branches
+    ([7], [1], 4, 1),               # bsz == 1, decode
+    ([9], [5], 4, 2),               # bsz == 1, extend with a prefix
+    ([6], [6], 2, 2),               # bsz == 1, pure prefill
+    ([5, 9, 3], [1, 1, 1], 4, 1),   # batched pure decode
+    ([8, 4, 11], [4, 1, 2], 8, 2),  # batched extend / mixed
+    ([12, 12], [12, 3], 4, 4),      # prefill + extend, MHA
+]
+
+
+@pytest.mark.parametrize("seq,ext,hq,hkv", CASES)
+def test_dense_oracle_matches_loop_oracle(seq, ext, hq, hkv):
+    wl = small_case(seq, ext, hq, hkv, d=16, seed=1)
+    np.testing.assert_allclose(brute(wl, dense=True), brute(wl), rtol=1e-12, atol=1e-12)
+
+
+@pytest.mark.parametrize("seq,ext,hq,hkv", CASES)
+def test_restatement_matches_loop_oracle(seq, ext, hq, hkv):
+    wl = small_case(seq, ext, hq, hkv, d=32, seed=2)
+    got = as_numpy(restatement(wl))
+    np.testing.assert_allclose(got, brute(wl), rtol=1e-5, atol=2e-6)
+
+
+def test_restatement_matches_oracle_at_head_dim_256_with_shared_prefixes():
+    wl = small_case([40, 37, 12, 30], [9, 1, 1, 6], hq=6, hkv=1, d=256, seed=3,
+                    groups=[0, 0, 1, 1], prefixes=[28, 5])
+    np.testing.assert_allclose(as_numpy(restatement(wl)), brute(wl, dense=True),
+                               rtol=2e-5, atol=2e-6)
+
+
+# ----------------------------------------------------------------- closed forms
+
+def _visible_slots(wl, b, t):
+    """Slot ids visible to new token t of request b (positions 0 .. P + t)."""
+    L = wl.batch.max_seq_len if wl.batch.batch_size == 1 else wl.seq_lens[b]
+    P = L - wl.ext_lens[b]
+    rtt = wl.batch.req_to_token.cpu().numpy()
+    return [max(int(rtt[wl.rows[b], k]), 0) for k in range(P + t + 1)]
+
+
+def pin_single_key_returns_value(attn):
+    wl = small_case([1, 1, 1], [1, 1, 1], hq=4, hkv=2, d=16, seed=4)
+    out = attn(wl)
+    vp = wl.v_pool.numpy()
+    for b in range(3):
+        slot = _visible_slots(wl, b, 0)[0]
+        for h in range(4):
+            if not np.allclose(out[b, h], vp[slot, h // 2], atol=1e-6):
+                return False
+    return True
+
+
+def pin_equal_keys_average_visible_values(attn):
+    wl = small_case([10, 7, 13], [4, 1, 6], hq=4, hkv=2, d=16, seed=5)
+    wl.k_pool[:] = wl.k_pool[1:2].clone()          # every key row identical
+    out = attn(wl)
+    vp = wl.v_pool.numpy().astype(np.float64)
+    row = 0
+    for b in range(3):
+        for t in range(wl.ext_lens[b]):
+            slots = _visible_slots(wl, b, t)
+            for h in range(4):
+                want = vp[slots, h // 2].mean(axis=0)
+                if not np.allclose(out[row, h], want, atol=1e-5):
+                    return False
+            row += 1
+    return True
+
+
+def pin_dominant_key_selects_its_value(attn):
+    """q of head h aligned with one key of kv head h // G: softmax ~ one-hot."""
+    wl = small_case([9, 12], [3, 1], hq=4, hkv=2, d=16, seed=6)
+    rng = np.random.default_rng(0)
+    row = 0
+    targets = []
+    for b in range(2):
+        for t in range(wl.ext_lens[b]):
+            slots = _visible_slots(wl, b, t)
+            for h in range(4):
+                s = slots[int(rng.integers(len(slots)))]
+                key = wl.k_pool[s, h // 2]
+                wl.q[row, h] = key / key.norm() * 400.0
+                targets.append((row, h, s))
+            row += 1
+    # Give the chosen keys a large norm so they dominate every other key.
+    for _, h, s in targets:
+        wl.k_pool[s, h // 2] = wl.k_pool[s, h // 2] / wl.k_pool[s, h // 2].norm() * 4.0
+    for row, h, s in targets:
+        key = wl.k_pool[s, h // 2]
+        wl.q[row, h] = key / key.norm() * 400.0
+    out = attn(wl)
+    vp = wl.v_pool.numpy()
+    return all(np.allclose(out[row, h], vp[s, h // 2], atol=1e-4) for row, h, s in targets)
+
+
+def pin_slot_permutation_invariance(attn):
+    wl = small_case([11, 6], [4, 1], hq=4, hkv=1, d=16, seed=7, pool=64)
+    base = attn(wl)
+    perm = torch.randperm(63, generator=torch.Generator().manual_seed(3)) + 1
+    new_of_old = torch.zeros(64, dtype=torch.long)
+    new_of_old[1:] = perm
+    kp, vp = wl.k_pool.clone(), wl.v_pool.clone()
+    wl.k_pool[new_of_old] = kp
+    wl.v_pool[new_of_old] = vp
+    rtt = wl.batch.req_to_token
+    live = rtt >= 0
+    rtt[live] = new_of_old[rtt[live]]
+    return np.allclose(attn(wl), base, atol=1e-6)
+
+
+def pin_prefix_extend_equals_full_prefill_rows(attn):
+    """A request whose first P positions are a cached prefix gives the same rows
+    as a fresh prefill of all P + N tokens (the reference's own equivalence)."""
+    P, N = 9, 5
+    full = small_case([P + N], [P + N], hq=4, hkv=2, d=16, seed=8)
+    ref = attn(full)
+    ext = rebatch(full, [P + N], [N], full.q[P:].clone())
+    return np.allclose(attn(ext), ref[P:], atol=1e-6)
+
+
+def pin_chunked_extend_equals_one_shot(attn):
+    P, N1, N2 = 6, 4, 3
+    one = small_case([P + N1 + N2, 5], [N1 + N2, 1], hq=4, hkv=1, d=16, seed=9)
+    ref = attn(one)
+    a = rebatch(one, [P + N1, 5], [N1, 1], torch.cat([one.q[:N1], one.q[N1 + N2:]]))
+    b = rebatch(one, [P + N1 + N2, 5], [N2, 1], torch.cat([one.q[N1:N1 + N2],
+                                                           one.q[N1 + N2:]]))
+    got = np.concatenate([attn(a)[:N1], attn(b)[:N2]])
+    return np.allclose(got, ref[:N1 + N2], atol=1e-6)
+
+
+def pin_decode_equals_last_prefill_row(attn):
+    L = 10
+    pre = small_case([L, 4], [L, 1], hq=4, hkv=2, d=16, seed=10)
+    ref = attn(pre)
+    dec = rebatch(pre, [L, 4], [1, 1], torch.stack([pre.q[L - 1], pre.q[L]]))
+    return np.allclose(attn(dec)[0], ref[L - 1], atol=1e-6)
+
+
+def pin_two_keys_logistic_weight(attn):
+    """Two visible keys and a one-hot query: the weight of key 0 is the logistic
+    function 1 / (1 + exp(scale * c * (x1 - x0))) of the score gap."""
+    import math
+    wl = small_case([2, 2], [1, 1], hq=2, hkv=1, d=16, seed=12, scale=0.3)
+    rtt = wl.batch.req_to_token.numpy()
+    for b in range(2):
+        s0, s1 = (int(rtt[wl.rows[b], k]) for k in range(2))
+        wl.k_pool[s0, 0, 0] = 1.5 + b
+        wl.k_pool[s1, 0, 0] = -0.5
+        wl.q[b] = 0.0
+        wl.q[b, :, 0] = torch.tensor([2.0, -1.0])
+    out = attn(wl)
+    vp = wl.v_pool.double().numpy()
+    for b in range(2):
+        s0, s1 = (int(rtt[wl.rows[b], k]) for k in range(2))
+        x0, x1 = float(wl.k_pool[s0, 0, 0]), float(wl.k_pool[s1, 0, 0])
+        for h, c in enumerate((2.0, -1.0)):
+            w0 = 1.0 / (1.0 + math.exp(0.3 * c * (x1 - x0)))
+            want = w0 * vp[s0, 0] + (1 - w0) * vp[s1, 0]
+            if not np.allclose(out[b, h], want, atol=1e-5):
+                return False
+    return True
+
+
+PINS = [pin_single_key_returns_value, pin_equal_keys_average_visible_values,
+        pin_two_keys_logistic_weight,
+        pin_dominant_key_selects_its_value, pin_slot_permutation_invariance,
+        pin_prefix_extend_equals_full_prefill_rows, pin_chunked_extend_equals_one_shot,
+        pin_decode_equals_last_prefill_row]
+
+
+def _restatement_np(wl):
+    return as_numpy(restatement(wl))
+
+
+def _brute_np(wl):
+    return brute(wl)
+
+
+@pytest.mark.parametrize("pin", PINS, ids=lambda f: f.__name__)
+@pytest.mark.parametrize("impl", [_restatement_np, _brute_np], ids=["restatement", "brute"])
+def test_oracle_satisfies_pin(pin, impl):
+    assert pin(impl)
+
+
+# ----------------------------------------------------------------- planted mistakes
+
+def _mutant(kind):
+    """A float64 attention with one deliberate mistake (pins must reject it)."""
+
+    def attn(wl):
+        q = wl.q.double().numpy()
+        kp = wl.k_pool.double().numpy()
+        vp = wl.v_pool.double().numpy()
+        rtt = wl.batch.req_to_token.numpy()
+        n_q, n_kv = wl.num_q_heads, wl.num_kv_heads
+        group = n_q // n_kv
+        seq = [wl.batch.max_seq_len] if wl.batch.batch_size == 1 else wl.seq_lens
+        out = np.zeros_like(q)
+        base = 0
+        for b, row in enumerate(wl.rows):
+            L, e = seq[b], wl.ext_lens[b]
+            P = L - e
+            for t in range(e):
+                last = P + t + (1 if kind == "causal_off_by_one" else 0)
+                last = min(last, L - 1) if kind != "no_length_mask" else L - 1
+                if kind == "causal_off_by_one" and e > 1:
+                    last = P + t - 1 if t > 0 else P + t
+                slots = [max(int(x), 0) for x in rtt[row, :last + 1]]
+                for h in range(n_q):
+                    kvh = (h % n_kv) if kind == "gqa_modulo" else h // group
+                    sc = kp[slots, kvh] @ q[base + t, h]
+                    if kind != "no_scale":
+                        sc = sc * wl.scale
+                    w = np.exp(sc - sc.max())
+                    out[base + t, h] = (w / w.sum()) @ vp[slots, kvh]
+            base += e
+        return out
+
+    return attn
+
+
+@pytest.mark.parametrize("kind", ["gqa_modulo", "causal_off_by_one", "no_scale"])
+def test_planted_mistake_fails_a_pin(kind):
+    attn = _mutant(kind)
+    failed = [p.__name__ for p in PINS if not p(attn)]
+    assert failed, f"mutation {kind} passed every pin"
+
+
+def test_unmutated_mutant_harness_passes_all_pins():
+    attn = _mutant("none")
+    assert all(p(attn) for p in PINS)
+
+
+# ----------------------------------------------------------------- slot gather
+
+def test_gather_ref_matches_explicit_loops_and_clamps_padding():
+    wl = small_case([5, 9, 2], [1, 1, 1], hq=2, hkv=2, d=8, seed=11)
+    got = gather_kv_ref(wl.k_pool, wl.batch.req_to_token, wl.batch.req_pool_indices,
+                        wl.batch.max_seq_len).numpy()
+    rtt = wl.batch.req_to_token.numpy()
+    kp = wl.k_pool.numpy()
+    for b, row in enumerate(wl.rows):
+        for t in range(wl.batch.max_seq_len):
+            sid = rtt[row, t]
+            want = kp[0] if sid < 0 else kp[sid]
+            assert (sid >= 0) == (t < wl.seq_lens[b])
+            np.testing.assert_array_equal(got[b, t], want)
+
+
+def test_forward_batch_defaults_follow_reference_rules():
+    from tokenfactory_amd import ForwardBatch
+    fb = ForwardBatch(batch_size=2, req_pool_indices=torch.tensor([3, 1]),
+                      seq_lens=torch.tensor([7, 12]), prefix_lens=torch.tensor([6, 9]),
+                      extend_lens=[1, 3], out_cache_loc=torch.arange(4),
+                      req_to_token=torch.full((4, 16), -1))
+    assert fb.max_extend_len == 3 and fb.max_seq_len == 12
+    assert fb.extend_lens_tensor.tolist() == [1, 3]
+    assert fb.req_pool_indices_list == [3, 1]

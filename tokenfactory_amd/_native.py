@@ -1,0 +1,140 @@
+"""ctypes binding of ``libtf_attn.so`` (declared in ``include/tf_attn.h``).
+
+The library is loaded from ``tokenfactory_amd/_lib/`` only; there is no
+fallback of any kind: if it is missing or fails to load, every entry point
+raises ``NativeLibraryError``.
+"""
+from __future__ import annotations
+
+import ctypes
+import threading
+from pathlib import Path
+from typing import Optional
+
+LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libtf_attn.so"
+ABI_VERSION = 1
+
+TF_DTYPE_BF16 = 0
+TF_DTYPE_FP8_E4M3 = 1
+TF_DTYPE_FP32 = 2
+
+TF_OK = 0
+TF_ERR_INVALID = -1
+TF_ERR_UNSUPPORTED = -2
+TF_ERR_HIP = -3
+
+# Exported symbols and their ctypes signatures (restype, argtypes).
+_p = ctypes.c_void_p
+_i32 = ctypes.c_int32
+_i64 = ctypes.c_int64
+_f32 = ctypes.c_float
+
+SIGNATURES = {
+    "tf_attn_abi_version": (_i32, []),
+    "tf_attn_last_error": (ctypes.c_char_p, []),
+    "tf_attn_decode_workspace_bytes": (_i64, [_i32, _i32, _i32, _i32, _i32, _i32]),
+    "tf_attn_decode": (_i32, [
+        _p, _i64,                      # q, q_row_stride
+        _p, _p, _i64, _i32, _p, _p,    # k_pool, v_pool, pool_slots, kv_dtype, k_scale, v_scale
+        _p, _i64, _i64, _i64,          # req_to_token, rtt_rows, rtt_row_stride, rtt_cols
+        _p, _p, _i32,                  # req_pool_indices, seq_lens, seq_len_override
+        _p, _p, _i32,                  # items, q_rows, n_items
+        _i32, _i32, _i32, _f32,        # num_q_heads, num_kv_heads, head_dim, scale
+        _p, _i64,                      # out, out_row_stride
+        _p, _i64, _i32, _i32,          # workspace, workspace_bytes, max_seq_len, chunk_tokens
+        _p,                            # stream
+    ]),
+    "tf_attn_extend": (_i32, [
+        _p, _i64,
+        _p, _p, _i64, _i32, _p, _p,
+        _p, _i64, _i64, _i64,
+        _p, _p, _i32,
+        _p, _i32,                      # work, n_work
+        _i32, _i32, _i32, _f32,
+        _p, _i64,
+        _p,
+    ]),
+    "tf_attn_plan_extend": (_i32, [_p, _i32, _i32, _i32, _i32, _p, _i32]),
+    "tf_attn_plan_decode_items": (_i32, [_p, _i32, _p, _p, _i32]),
+    "tf_kv_write": (_i32, [
+        _p, _p, _i64, _i32,            # k, v, src_row_stride, src_dtype
+        _p, _i64,                      # out_cache_loc, n_tokens
+        _p, _p, _i64, _i32, _p, _p,    # k_pool, v_pool, pool_slots, kv_dtype, k_scale, v_scale
+        _i32, _i32, _p,                # num_kv_heads, head_dim, stream
+    ]),
+    "tf_gather_kv": (_i32, [
+        _p, _i32, _i64, _i64,          # pool, kv_dtype, pool_slots, row_elems
+        _p, _i64, _i64, _i64,          # req_to_token, rtt_rows, rtt_row_stride, rtt_cols
+        _p, _i32, _i32, _p, _p,        # req_pool_indices, batch_size, max_len, out, stream
+    ]),
+}
+
+
+class NativeLibraryError(RuntimeError):
+    """libtf_attn.so is missing, stale or failed to load."""
+
+
+class NativeCallError(RuntimeError):
+    """A libtf_attn entry point returned an error status."""
+
+    def __init__(self, fn: str, code: int, message: str):
+        super().__init__(f"{fn} failed with status {code}: {message}")
+        self.code = code
+
+
+_lock = threading.Lock()
+_lib: Optional[ctypes.CDLL] = None
+
+
+def load(path: Optional[Path] = None) -> ctypes.CDLL:
+    """Loads (once) and returns the library with every signature declared."""
+    global _lib
+    with _lock:
+        if _lib is not None and path is None:
+            return _lib
+        target = Path(path) if path is not None else LIB_PATH
+        if not target.exists():
+            raise NativeLibraryError(
+                f"{target} not found: build it with `python -m tokenfactory_amd.build` "
+                "(the attention path has no non-native fallback)")
+        try:
+            lib = ctypes.CDLL(str(target))
+        except OSError as exc:
+            raise NativeLibraryError(f"cannot load {target}: {exc}") from exc
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(lib, name)
+            fn.restype = res
+            fn.argtypes = args
+        ver = lib.tf_attn_abi_version()
+        if ver != ABI_VERSION:
+            raise NativeLibraryError(f"{target}: ABI version {ver}, expected {ABI_VERSION}")
+        if path is None:
+            _lib = lib
+        return lib
+
+
+def call(name: str, *args) -> int:
+    """Calls an int32-status entry point and raises on a negative status."""
+    lib = load()
+    rc = getattr(lib, name)(*args)
+    if rc < 0:
+        msg = lib.tf_attn_last_error().decode(errors="replace")
+        if rc == TF_ERR_INVALID:
+            raise ValueError(f"{name}: {msg}")
+        if rc == TF_ERR_UNSUPPORTED:
+            raise NotImplementedError(f"{name}: {msg}")
+        raise NativeCallError(name, rc, msg)
+    return rc
+
+
+def decode_workspace_bytes(n_items, num_q_heads, num_kv_heads, head_dim, max_seq_len,
+                           chunk_tokens=0) -> int:
+    lib = load()
+    n = lib.tf_attn_decode_workspace_bytes(n_items, num_q_heads, num_kv_heads, head_dim,
+                                           max_seq_len, chunk_tokens)
+    if n < 0:
+        msg = lib.tf_attn_last_error().decode(errors="replace")
+        if n == TF_ERR_UNSUPPORTED:
+            raise NotImplementedError(msg)
+        raise ValueError(msg)
+    return int(n)

@@ -1,0 +1,255 @@
+"""``slot_based_attention``: the reference's ``_slot_based_attention`` on gfx950 kernels.
+
+Same inputs, output and branch semantics as
+``Qwen3_8FullAttention._slot_based_attention`` (reference
+``qwen3_8/full_attention.py:163-283``):
+
+* ``bsz == 1``: context length from ``batch.max_seq_len`` (``:186``); causal
+  mask only when ``ext_len > 1`` (``:200-208``);
+* pure decode (``max_extend_len == 1``): one query per request, keys
+  ``k < seq_lens[b]`` (``:231-242``) -> ``tf_attn_decode`` over the whole batch,
+  no host metadata at all;
+* extend / mixed: query ``t`` of request ``b`` sees keys
+  ``k <= seq_lens[b] - ext_b + t`` (``:266-278``) -> ``tf_attn_extend`` over
+  the requests with ``ext_b > 1`` plus ``tf_attn_decode`` over the ``ext_b == 1``
+  rows of a mixed batch; the two work lists are planned on the host from
+  ``batch.extend_lens`` and uploaded in one copy.
+
+Only ROCm device tensors are accepted; there is no CPU path.
+"""
+from __future__ import annotations
+
+import threading
+from typing import Dict, Optional, Tuple
+
+import numpy as np
+import torch
+
+from . import _native
+from .planning import plan_decode_items, plan_extend
+
+_KV_DTYPES = {
+    torch.bfloat16: _native.TF_DTYPE_BF16,
+    torch.float8_e4m3fn: _native.TF_DTYPE_FP8_E4M3,
+}
+
+_ws_lock = threading.Lock()
+_workspaces: Dict[Tuple[int, int], torch.Tensor] = {}
+
+
+def _workspace(device: torch.device, stream: torch.cuda.Stream, nbytes: int) -> torch.Tensor:
+    """Zero-filled decode scratch, one per (device, stream); the kernel leaves it zeroed."""
+    key = (device.index if device.index is not None else torch.cuda.current_device(),
+           stream.cuda_stream)
+    with _ws_lock:
+        ws = _workspaces.get(key)
+        if ws is None or ws.numel() < nbytes:
+            size = max(nbytes, 1 << 20)
+            ws = torch.zeros(size, dtype=torch.uint8, device=device)
+            _workspaces[key] = ws
+        return ws
+
+
+def _ptr(t: Optional[torch.Tensor]):
+    return None if t is None else t.data_ptr()
+
+
+def _require_device(name: str, t: torch.Tensor, device: torch.device) -> None:
+    if t.device != device:
+        raise ValueError(f"{name} is on {t.device}, expected {device}")
+
+
+def _check_inputs(q, k_buf, v_buf, batch):
+    if not q.is_cuda:
+        raise RuntimeError(
+            "slot_based_attention runs only on ROCm devices (q is on "
+            f"{q.device}); there is no CPU implementation")
+    if q.dim() != 3 or k_buf.dim() != 3 or v_buf.shape != k_buf.shape:
+        raise ValueError(f"expected q [T,Hq,D] and pools [S,Hkv,D], got {tuple(q.shape)}, "
+                         f"{tuple(k_buf.shape)}, {tuple(v_buf.shape)}")
+    if q.dtype != torch.bfloat16:
+        raise NotImplementedError(f"q dtype {q.dtype} (bf16 only)")
+    if k_buf.dtype not in _KV_DTYPES or v_buf.dtype != k_buf.dtype:
+        raise NotImplementedError(f"KV pool dtype {k_buf.dtype}")
+    if q.shape[2] != k_buf.shape[2]:
+        raise ValueError("q and pool head_dim differ")
+    if not (k_buf.is_contiguous() and v_buf.is_contiguous()):
+        raise ValueError("KV pools must be contiguous [S, Hkv, D] layer views")
+    dev = q.device
+    for name, t in (("layer_k_buffer", k_buf), ("layer_v_buffer", v_buf),
+                    ("req_to_token", batch.req_to_token),
+                    ("req_pool_indices", batch.req_pool_indices),
+                    ("seq_lens", batch.seq_lens)):
+        _require_device(name, t, dev)
+    rtt = batch.req_to_token
+    if rtt.dtype != torch.int64 or rtt.dim() != 2 or rtt.stride(1) != 1:
+        raise ValueError("req_to_token must be a row-major int64 [max_reqs, max_ctx] tensor")
+    if batch.req_pool_indices.dtype != torch.int64 or batch.seq_lens.dtype != torch.int64:
+        raise ValueError("req_pool_indices / seq_lens must be int64")
+    if batch.max_seq_len > rtt.shape[1]:
+        raise ValueError(f"max_seq_len {batch.max_seq_len} exceeds req_to_token width "
+                         f"{rtt.shape[1]}")
+
+
+def slot_based_attention(
+    q: torch.Tensor,
+    layer_k_buffer: torch.Tensor,
+    layer_v_buffer: torch.Tensor,
+    batch,
+    *,
+    scaling: Optional[float] = None,
+    k_scale: Optional[torch.Tensor] = None,
+    v_scale: Optional[torch.Tensor] = None,
+    chunk_tokens: int = 0,
+    out: Optional[torch.Tensor] = None,
+) -> torch.Tensor:
+    """Attention of ``q [T, Hq, D]`` over one layer's slot pool; returns ``[T, Hq, D]``.
+
+    ``scaling`` defaults to ``head_dim ** -0.5`` (``full_attention.py:40``).
+    ``k_scale`` / ``v_scale`` (fp32 device scalars) are required for an
+    ``float8_e4m3fn`` pool. ``chunk_tokens`` overrides the decode split size
+    (0 = automatic).
+    """
+    _check_inputs(q, layer_k_buffer, layer_v_buffer, batch)
+    n_tok, n_q, head_dim = q.shape
+    n_slots, n_kv, _ = layer_k_buffer.shape
+    if n_q % n_kv:
+        raise ValueError(f"num_q_heads {n_q} is not a multiple of num_kv_heads {n_kv}")
+    if scaling is None:
+        scaling = head_dim ** -0.5
+    kv_dtype = _KV_DTYPES[layer_k_buffer.dtype]
+    if kv_dtype == _native.TF_DTYPE_FP8_E4M3:
+        if k_scale is None or v_scale is None:
+            raise ValueError("an fp8 KV pool needs k_scale and v_scale")
+        k_scale = k_scale.to(device=q.device, dtype=torch.float32).reshape(1)
+        v_scale = v_scale.to(device=q.device, dtype=torch.float32).reshape(1)
+    else:
+        k_scale = v_scale = None
+    if q.stride(2) != 1 or q.stride(1) != head_dim:
+        q = q.contiguous()
+    if out is None:
+        out = torch.empty((n_tok, n_q, head_dim), dtype=q.dtype, device=q.device)
+    elif out.shape != q.shape or out.dtype != q.dtype or out.stride(2) != 1 \
+            or out.stride(1) != head_dim:
+        raise ValueError("out must match q's shape/dtype with dense heads and dims")
+
+    bsz = batch.batch_size
+    ext_lens = list(batch.extend_lens)
+    if len(ext_lens) != bsz or sum(ext_lens) != n_tok:
+        raise ValueError(f"extend_lens {ext_lens[:8]}... do not match batch_size={bsz}, "
+                         f"T={n_tok}")
+    if n_tok == 0:
+        return out
+
+    stream = torch.cuda.current_stream(q.device)
+    rtt = batch.req_to_token
+    seq_override = int(batch.max_seq_len) if bsz == 1 else 0
+    max_len = int(batch.max_seq_len)
+    common_pool = (layer_k_buffer.data_ptr(), layer_v_buffer.data_ptr(), n_slots, kv_dtype,
+                   _ptr(k_scale), _ptr(v_scale),
+                   rtt.data_ptr(), rtt.shape[0], rtt.stride(0), rtt.shape[1],
+                   batch.req_pool_indices.data_ptr(), batch.seq_lens.data_ptr(), seq_override)
+
+    def run_decode(items_t, rows_t, n_items):
+        nbytes = _native.decode_workspace_bytes(n_items, n_q, n_kv, head_dim, max_len,
+                                                chunk_tokens)
+        ws = _workspace(q.device, stream, nbytes) if nbytes else None
+        _native.call("tf_attn_decode", q.data_ptr(), q.stride(0), *common_pool,
+                     _ptr(items_t), _ptr(rows_t), n_items,
+                     n_q, n_kv, head_dim, float(scaling), out.data_ptr(), out.stride(0),
+                     _ptr(ws), 0 if ws is None else ws.numel(), max_len, chunk_tokens,
+                     stream.cuda_stream)
+
+    if batch.max_extend_len == 1 or (bsz == 1 and ext_lens[0] == 1):
+        # Pure decode: batch entry b is query row b; nothing to upload.
+        run_decode(None, None, bsz)
+        return out
+
+    # Extend / mixed: plan on the host from extend_lens, one H2D copy.
+    work = plan_extend(ext_lens, n_q, n_kv, decode_to_decode_kernel=True)
+    items, rows = plan_decode_items(ext_lens)
+    n_work, n_dec = len(work), len(items)
+    meta = np.zeros(n_work * 8 + 2 * n_dec + 4, dtype=np.int32)
+    meta[: n_work * 8] = work.reshape(-1)
+    meta[n_work * 8: n_work * 8 + n_dec] = items
+    meta[n_work * 8 + n_dec: n_work * 8 + 2 * n_dec] = rows
+    meta_dev = torch.from_numpy(meta).pin_memory().to(q.device, non_blocking=True)
+    if n_work:
+        _native.call("tf_attn_extend", q.data_ptr(), q.stride(0), *common_pool,
+                     meta_dev.data_ptr(), n_work, n_q, n_kv, head_dim, float(scaling),
+                     out.data_ptr(), out.stride(0), stream.cuda_stream)
+    if n_dec:
+        base = meta_dev.data_ptr() + 4 * n_work * 8
+        items_p = _DevPtr(base)
+        rows_p = _DevPtr(base + 4 * n_dec)
+        run_decode(items_p, rows_p, n_dec)
+    # Keep the upload alive until the kernels that read it have run.
+    meta_dev.record_stream(stream)
+    return out
+
+
+class _DevPtr:
+    """A raw device address posing as a tensor for ``_ptr``."""
+
+    __slots__ = ("_addr",)
+
+    def __init__(self, addr: int):
+        self._addr = addr
+
+    def data_ptr(self) -> int:
+        return self._addr
+
+
+def gather_kv(pool: torch.Tensor, req_to_token: torch.Tensor, req_pool_indices: torch.Tensor,
+              max_len: int) -> torch.Tensor:
+    """``pool[req_to_token[req_pool_indices, :max_len].clamp(min=0)]`` via ``tf_gather_kv``."""
+    if not pool.is_cuda:
+        raise RuntimeError("gather_kv runs only on ROCm devices")
+    dtype_code = {torch.bfloat16: _native.TF_DTYPE_BF16,
+                  torch.float8_e4m3fn: _native.TF_DTYPE_FP8_E4M3,
+                  torch.float32: _native.TF_DTYPE_FP32}[pool.dtype]
+    if not pool.is_contiguous():
+        raise ValueError("pool must be contiguous")
+    if req_to_token.stride(1) != 1 or req_to_token.dtype != torch.int64:
+        raise ValueError("req_to_token must be row-major int64")
+    bsz = req_pool_indices.numel()
+    row_elems = int(np.prod(pool.shape[1:]))
+    out = torch.empty((bsz, max_len, *pool.shape[1:]), dtype=pool.dtype, device=pool.device)
+    _native.call("tf_gather_kv", pool.data_ptr(), dtype_code, pool.shape[0], row_elems,
+                 req_to_token.data_ptr(), req_to_token.shape[0], req_to_token.stride(0),
+                 req_to_token.shape[1], req_pool_indices.contiguous().data_ptr(), bsz, max_len,
+                 out.data_ptr(), torch.cuda.current_stream(pool.device).cuda_stream)
+    return out
+
+
+def write_kv(layer_k_buffer: torch.Tensor, layer_v_buffer: torch.Tensor,
+             out_cache_loc: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
+             k_scale: Optional[torch.Tensor] = None,
+             v_scale: Optional[torch.Tensor] = None) -> None:
+    """``layer_k_buffer[out_cache_loc] = k`` (and v) via ``tf_kv_write``
+    (``full_attention.py:146-149``); quantises for an fp8 pool."""
+    if not k.is_cuda:
+        raise RuntimeError("write_kv runs only on ROCm devices")
+    if k.shape != v.shape or k.dim() != 3 or k.shape[1:] != layer_k_buffer.shape[1:]:
+        raise ValueError(f"k/v {tuple(k.shape)} do not match pool rows "
+                         f"{tuple(layer_k_buffer.shape[1:])}")
+    src = {torch.bfloat16: _native.TF_DTYPE_BF16, torch.float32: _native.TF_DTYPE_FP32}
+    if k.dtype not in src or v.dtype != k.dtype:
+        raise NotImplementedError(f"k/v dtype {k.dtype}")
+    kv_dtype = _KV_DTYPES.get(layer_k_buffer.dtype)
+    if kv_dtype is None:
+        raise NotImplementedError(f"pool dtype {layer_k_buffer.dtype}")
+    if not (k.is_contiguous() and v.is_contiguous()):
+        k, v = k.contiguous(), v.contiguous()
+    loc = out_cache_loc.to(torch.int64).contiguous()
+    if kv_dtype == _native.TF_DTYPE_FP8_E4M3:
+        if k_scale is None or v_scale is None:
+            raise ValueError("an fp8 KV pool needs k_scale and v_scale")
+        k_scale = k_scale.to(device=k.device, dtype=torch.float32).reshape(1)
+        v_scale = v_scale.to(device=k.device, dtype=torch.float32).reshape(1)
+    n_kv, head_dim = k.shape[1], k.shape[2]
+    _native.call("tf_kv_write", k.data_ptr(), v.data_ptr(), k.stride(0), src[k.dtype],
+                 loc.data_ptr(), loc.numel(), layer_k_buffer.data_ptr(),
+                 layer_v_buffer.data_ptr(), layer_k_buffer.shape[0], kv_dtype,
+                 _ptr(k_scale), _ptr(v_scale), n_kv, head_dim,
+                 torch.cuda.current_stream(k.device).cuda_stream)

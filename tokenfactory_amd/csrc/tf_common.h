@@ -1,0 +1,106 @@
+// Shared device helpers for the gfx950 full-attention kernels.
+//
+// Everything here is CDNA4-specific: 64-lane wavefronts, the bf16 MFMA
+// instructions v_mfma_f32_16x16x32_bf16 / v_mfma_f32_16x16x16_bf16 /
+// v_mfma_f32_32x32x16_bf16, and the OCP e4m3 conversions of gfx950.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace tfa {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+enum : int { DT_BF16 = 0, DT_FP8_E4M3 = 1, DT_FP32 = 2 };
+
+constexpr int kWave = 64;
+constexpr float kLog2e = 1.4426950408889634f;
+
+// ---------------------------------------------------------------- loads
+__device__ __forceinline__ u32x4 ld_g16(const void* p) {
+  return *reinterpret_cast<const u32x4*>(p);
+}
+__device__ __forceinline__ u32x2 ld_g8(const void* p) {
+  return *reinterpret_cast<const u32x2*>(p);
+}
+__device__ __forceinline__ u32x4 ld_s16(const void* p) {
+  return *reinterpret_cast<const u32x4*>(p);
+}
+__device__ __forceinline__ void st_s16(void* p, u32x4 v) {
+  *reinterpret_cast<u32x4*>(p) = v;
+}
+__device__ __forceinline__ void st_s8(void* p, u32x2 v) {
+  *reinterpret_cast<u32x2*>(p) = v;
+}
+
+// ---------------------------------------------------------------- MFMA
+// D = A * B + C.  Operand/result lane layouts (l = lane id):
+//  16x16x32: A[i=l%16][k=8*(l/16)+j], B[k=8*(l/16)+j][n=l%16], C[4*(l/16)+r][l%16]
+//  16x16x16: A[i=l%16][k=4*(l/16)+j], B[k=4*(l/16)+j][n=l%16], C[4*(l/16)+r][l%16]
+//  32x32x16: A[i=l%32][k=8*(l/32)+j], B[k=8*(l/32)+j][n=l%32],
+//            C[8*(r/4)+4*(l/32)+r%4][l%32]
+__device__ __forceinline__ f32x4 mfma_16x16x32(u32x4 a, u32x4 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
+                                                 __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+}
+__device__ __forceinline__ f32x4 mfma_16x16x16(u32x2 a, u32x2 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(bf16x4, a),
+                                                   __builtin_bit_cast(bf16x4, b), c, 0, 0, 0);
+}
+__device__ __forceinline__ f32x16 mfma_32x32x16(u32x4 a, u32x4 b, f32x16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a),
+                                                 __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+}
+
+// ---------------------------------------------------------------- packing
+// Two fp32 -> packed bf16 pair (round to nearest even; v_cvt_pk_bf16_f32).
+__device__ __forceinline__ uint32_t pack_bf16(float lo, float hi) {
+  bf16x2 v = {(__bf16)lo, (__bf16)hi};
+  return __builtin_bit_cast(uint32_t, v);
+}
+// Low (sel_hi=false) or high halves of two dwords -> (b.half | a.half << 16).
+__device__ __forceinline__ uint32_t pair_lo(uint32_t a, uint32_t b) {
+  return __builtin_amdgcn_perm(a, b, 0x05040100u);
+}
+__device__ __forceinline__ uint32_t pair_hi(uint32_t a, uint32_t b) {
+  return __builtin_amdgcn_perm(a, b, 0x07060302u);
+}
+__device__ __forceinline__ uint32_t pair_sel(uint32_t a, uint32_t b, int hi) {
+  return hi ? pair_hi(a, b) : pair_lo(a, b);
+}
+
+// Two OCP e4m3 bytes (low or high 16-bit word of src) -> packed bf16 pair.
+// Exact: every e4m3 value, subnormals included, is representable in bf16.
+template <bool HI>
+__device__ __forceinline__ uint32_t e4m3x2_to_bf16x2(uint32_t src) {
+  return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(src, 1.0f, HI));
+}
+// 8 e4m3 bytes (two dwords) -> 8 bf16 (four dwords), element order kept.
+__device__ __forceinline__ u32x4 e4m3x8_to_bf16x8(uint32_t d0, uint32_t d1) {
+  u32x4 r;
+  r[0] = e4m3x2_to_bf16x2<false>(d0);
+  r[1] = e4m3x2_to_bf16x2<true>(d0);
+  r[2] = e4m3x2_to_bf16x2<false>(d1);
+  r[3] = e4m3x2_to_bf16x2<true>(d1);
+  return r;
+}
+
+// ---------------------------------------------------------------- math
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+__device__ __forceinline__ float wave_max_xor(float v, int mask) {
+  return fmaxf(v, __shfl_xor(v, mask, kWave));
+}
+
+__device__ __forceinline__ int64_t clamp_i64(int64_t v, int64_t lo, int64_t hi) {
+  return v < lo ? lo : (v > hi ? hi : v);
+}
+
+}  // namespace tfa

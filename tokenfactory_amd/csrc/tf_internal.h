@@ -1,0 +1,34 @@
+// Host-side helpers shared by the C-ABI translation units.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "tf_attn.h"
+
+namespace tfa {
+
+// Records a formatted message for tf_attn_last_error() and returns `code`.
+int fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+// Clears the thread's last error.
+void clear_error();
+// Maps the most recent launch status to TF_OK / TF_ERR_HIP.
+int launch_status(const char* what);
+
+inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+inline bool aligned8(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 7u) == 0; }
+
+// Decode split plan shared by the launcher and the workspace-size query.
+struct DecodePlan {
+  int32_t chunk;        // context tokens per workgroup
+  int32_t max_splits;   // ceil(max_seq_len / chunk)
+  int32_t n_hgroups;    // ceil(group / 16)
+  int32_t gmax;         // min(group, 16)
+  int64_t n_units;      // items * kv_heads * n_hgroups
+  int64_t cnt_bytes, ml_bytes, o_bytes, total_bytes;
+};
+int make_decode_plan(int32_t n_items, int32_t num_q_heads, int32_t num_kv_heads,
+                     int32_t head_dim, int32_t max_seq_len, int32_t chunk_tokens,
+                     DecodePlan* plan);
+
+}  // namespace tfa
