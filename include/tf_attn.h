@@ -74,14 +74,21 @@ const char* tf_attn_last_error(void);
  * items is NULL) and reads / writes query row q_rows[i] (or items[i] / i when
  * q_rows is NULL) of q and out.
  *
- * workspace: device scratch of tf_attn_decode_workspace_bytes(...) bytes that
- * is zero-filled before its first use; every call leaves it zero-filled again
- * (it holds split partials and arrival counters).  Calls that overlap in time
+ * workspace: device scratch of tf_attn_decode_workspace_bytes(...) bytes (no
+ * initialisation needed; 0 bytes when every request fits one split).  It holds
+ * the fp32 split partials between the two phases.  Calls that overlap in time
  * must not share a workspace.
- * chunk_tokens: context tokens per workgroup (multiple of 64), or 0 to let the
- * library choose from max_seq_len and n_items.
+ * chunk_tokens: context tokens per workgroup (multiple of 64, <= 4096), or 0 to
+ * let the library choose from max_seq_len and n_items.
  * max_seq_len: an upper bound of every L_b processed (host int, as
  * ForwardBatch.max_seq_len).
+ *
+ * tf_attn_decode runs both phases.  tf_attn_decode_partial runs the
+ * HBM-streaming split kernel only (requests that fit one split get their final
+ * output, the others leave partials in the workspace); tf_attn_decode_merge then
+ * combines the partials.  Calling the two phases back to back with identical
+ * arguments is exactly tf_attn_decode; the split lets a caller time the
+ * streaming kernel alone or merge partials computed elsewhere.
  */
 int64_t tf_attn_decode_workspace_bytes(int32_t n_items, int32_t num_q_heads,
                                        int32_t num_kv_heads, int32_t head_dim,
@@ -99,6 +106,32 @@ int32_t tf_attn_decode(const void* q, int64_t q_row_stride,
                        float scale, void* out, int64_t out_row_stride,
                        void* workspace, int64_t workspace_bytes,
                        int32_t max_seq_len, int32_t chunk_tokens, tf_stream_t stream);
+
+int32_t tf_attn_decode_partial(const void* q, int64_t q_row_stride,
+                               const void* k_pool, const void* v_pool, int64_t pool_slots,
+                               int32_t kv_dtype, const float* k_scale, const float* v_scale,
+                               const int64_t* req_to_token, int64_t rtt_rows,
+                               int64_t rtt_row_stride, int64_t rtt_cols,
+                               const int64_t* req_pool_indices, const int64_t* seq_lens,
+                               int32_t seq_len_override,
+                               const int32_t* items, const int32_t* q_rows, int32_t n_items,
+                               int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
+                               float scale, void* out, int64_t out_row_stride,
+                               void* workspace, int64_t workspace_bytes,
+                               int32_t max_seq_len, int32_t chunk_tokens, tf_stream_t stream);
+
+int32_t tf_attn_decode_merge(const void* q, int64_t q_row_stride,
+                             const void* k_pool, const void* v_pool, int64_t pool_slots,
+                             int32_t kv_dtype, const float* k_scale, const float* v_scale,
+                             const int64_t* req_to_token, int64_t rtt_rows,
+                             int64_t rtt_row_stride, int64_t rtt_cols,
+                             const int64_t* req_pool_indices, const int64_t* seq_lens,
+                             int32_t seq_len_override,
+                             const int32_t* items, const int32_t* q_rows, int32_t n_items,
+                             int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
+                             float scale, void* out, int64_t out_row_stride,
+                             void* workspace, int64_t workspace_bytes,
+                             int32_t max_seq_len, int32_t chunk_tokens, tf_stream_t stream);
 
 /* ------------------------------------------------------------------ extend
  * Causal prefill / extend attention over cached prefix + new tokens, bf16
@@ -134,6 +167,8 @@ int32_t tf_attn_extend(const void* q, int64_t q_row_stride,
  *
  * tf_attn_plan_decode_items: lists the requests with extend_lens[b] == 1 in
  * items (batch index) and q_rows (their row in q); returns the count.
+ *
+ * With work == NULL (or items / q_rows == NULL) the planners only count.
  */
 int32_t tf_attn_plan_extend(const int64_t* extend_lens, int32_t batch_size,
                             int32_t num_q_heads, int32_t num_kv_heads,

@@ -44,6 +44,8 @@ SIGNATURES = {
         _p, _i64, _i32, _i32,          # workspace, workspace_bytes, max_seq_len, chunk_tokens
         _p,                            # stream
     ]),
+    "tf_attn_decode_partial": None,   # same signature as tf_attn_decode
+    "tf_attn_decode_merge": None,
     "tf_attn_extend": (_i32, [
         _p, _i64,
         _p, _p, _i64, _i32, _p, _p,
@@ -68,6 +70,10 @@ SIGNATURES = {
         _p, _i32, _i32, _p, _p,        # req_pool_indices, batch_size, max_len, out, stream
     ]),
 }
+
+
+SIGNATURES["tf_attn_decode_partial"] = SIGNATURES["tf_attn_decode"]
+SIGNATURES["tf_attn_decode_merge"] = SIGNATURES["tf_attn_decode"]
 
 
 class NativeLibraryError(RuntimeError):

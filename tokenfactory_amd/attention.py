@@ -15,7 +15,9 @@ Same inputs, output and branch semantics as
   rows of a mixed batch; the two work lists are planned on the host from
   ``batch.extend_lens`` and uploaded in one copy.
 
-Only ROCm device tensors are accepted; there is no CPU path.
+``SlotAttentionCall`` separates planning (argument checks, work lists, upload,
+workspace) from launching, so a step's launches can be repeated or timed phase
+by phase. Only ROCm device tensors are accepted; there is no CPU path.
 """
 from __future__ import annotations
 
@@ -38,19 +40,18 @@ _workspaces: Dict[Tuple[int, int], torch.Tensor] = {}
 
 
 def _workspace(device: torch.device, stream: torch.cuda.Stream, nbytes: int) -> torch.Tensor:
-    """Zero-filled decode scratch, one per (device, stream); the kernel leaves it zeroed."""
+    """Decode split-partial scratch, one per (device, stream), grown on demand."""
     key = (device.index if device.index is not None else torch.cuda.current_device(),
            stream.cuda_stream)
     with _ws_lock:
         ws = _workspaces.get(key)
         if ws is None or ws.numel() < nbytes:
-            size = max(nbytes, 1 << 20)
-            ws = torch.zeros(size, dtype=torch.uint8, device=device)
+            ws = torch.empty(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
             _workspaces[key] = ws
         return ws
 
 
-def _ptr(t: Optional[torch.Tensor]):
+def _ptr(t) -> Optional[int]:
     return None if t is None else t.data_ptr()
 
 
@@ -86,9 +87,139 @@ def _check_inputs(q, k_buf, v_buf, batch):
         raise ValueError("req_to_token must be a row-major int64 [max_reqs, max_ctx] tensor")
     if batch.req_pool_indices.dtype != torch.int64 or batch.seq_lens.dtype != torch.int64:
         raise ValueError("req_pool_indices / seq_lens must be int64")
+    if not (batch.req_pool_indices.is_contiguous() and batch.seq_lens.is_contiguous()):
+        raise ValueError("req_pool_indices / seq_lens must be contiguous")
     if batch.max_seq_len > rtt.shape[1]:
         raise ValueError(f"max_seq_len {batch.max_seq_len} exceeds req_to_token width "
                          f"{rtt.shape[1]}")
+
+
+class _DevPtr:
+    """A raw device address posing as a tensor for ``_ptr``."""
+
+    __slots__ = ("_addr",)
+
+    def __init__(self, addr: int):
+        self._addr = addr
+
+    def data_ptr(self) -> int:
+        return self._addr
+
+
+class SlotAttentionCall:
+    """One planned ``_slot_based_attention`` step: validated arguments, uploaded
+    work lists and workspace, ready to launch (repeatedly) on ``stream``.
+
+    ``run()`` enqueues every kernel of the step. For timing, ``run_extend()``,
+    ``run_decode_partial()`` and ``run_decode_merge()`` enqueue the individual
+    launches; run in that order they are exactly ``run()``.
+    """
+
+    def __init__(self, q, layer_k_buffer, layer_v_buffer, batch, *, scaling=None,
+                 k_scale=None, v_scale=None, chunk_tokens: int = 0, out=None, stream=None):
+        _check_inputs(q, layer_k_buffer, layer_v_buffer, batch)
+        n_tok, n_q, head_dim = q.shape
+        n_slots, n_kv, _ = layer_k_buffer.shape
+        if n_q % n_kv:
+            raise ValueError(f"num_q_heads {n_q} is not a multiple of num_kv_heads {n_kv}")
+        if scaling is None:
+            scaling = head_dim ** -0.5
+        kv_dtype = _KV_DTYPES[layer_k_buffer.dtype]
+        if kv_dtype == _native.TF_DTYPE_FP8_E4M3:
+            if k_scale is None or v_scale is None:
+                raise ValueError("an fp8 KV pool needs k_scale and v_scale")
+            k_scale = k_scale.to(device=q.device, dtype=torch.float32).reshape(1).contiguous()
+            v_scale = v_scale.to(device=q.device, dtype=torch.float32).reshape(1).contiguous()
+        else:
+            k_scale = v_scale = None
+        if q.stride(2) != 1 or q.stride(1) != head_dim:
+            q = q.contiguous()
+        if out is None:
+            out = torch.empty((n_tok, n_q, head_dim), dtype=q.dtype, device=q.device)
+        elif out.shape != q.shape or out.dtype != q.dtype or out.stride(2) != 1 \
+                or out.stride(1) != head_dim:
+            raise ValueError("out must match q's shape/dtype with dense heads and dims")
+
+        bsz = batch.batch_size
+        ext_lens = [int(e) for e in batch.extend_lens]
+        if len(ext_lens) != bsz or sum(ext_lens) != n_tok:
+            raise ValueError(f"extend_lens {ext_lens[:8]}... do not match batch_size={bsz}, "
+                             f"T={n_tok}")
+        self.q, self.out = q, out
+        self.k_buf, self.v_buf = layer_k_buffer, layer_v_buffer
+        self.k_scale, self.v_scale = k_scale, v_scale
+        self.batch = batch
+        self.stream = stream if stream is not None else torch.cuda.current_stream(q.device)
+        self.n_q, self.n_kv, self.head_dim = n_q, n_kv, head_dim
+        self.scaling = float(scaling)
+        self.chunk_tokens = int(chunk_tokens)
+        self.max_len = int(batch.max_seq_len)
+        rtt = batch.req_to_token
+        seq_override = self.max_len if bsz == 1 else 0
+        self._pool_args = (layer_k_buffer.data_ptr(), layer_v_buffer.data_ptr(), n_slots,
+                           kv_dtype, _ptr(k_scale), _ptr(v_scale),
+                           rtt.data_ptr(), rtt.shape[0], rtt.stride(0), rtt.shape[1],
+                           batch.req_pool_indices.data_ptr(), batch.seq_lens.data_ptr(),
+                           seq_override)
+        self.n_work = 0
+        self.n_dec = 0
+        self._meta = None
+        self._items = self._rows = None
+        if n_tok == 0:
+            return
+        if batch.max_extend_len == 1 or (bsz == 1 and ext_lens[0] == 1):
+            # Pure decode: batch entry b is query row b; nothing to upload.
+            self.n_dec = bsz
+        else:
+            work = plan_extend(ext_lens, n_q, n_kv, decode_to_decode_kernel=True)
+            items, rows = plan_decode_items(ext_lens)
+            self.n_work, self.n_dec = len(work), len(items)
+            meta = np.zeros(self.n_work * 8 + 2 * self.n_dec + 4, dtype=np.int32)
+            meta[: self.n_work * 8] = work.reshape(-1)
+            meta[self.n_work * 8: self.n_work * 8 + self.n_dec] = items
+            meta[self.n_work * 8 + self.n_dec: self.n_work * 8 + 2 * self.n_dec] = rows
+            with torch.cuda.stream(self.stream):
+                self._meta = torch.from_numpy(meta).pin_memory().to(q.device, non_blocking=True)
+            base = self._meta.data_ptr() + 4 * self.n_work * 8
+            if self.n_dec:
+                self._items = _DevPtr(base)
+                self._rows = _DevPtr(base + 4 * self.n_dec)
+        self.ws = None
+        if self.n_dec:
+            nbytes = _native.decode_workspace_bytes(self.n_dec, n_q, n_kv, head_dim,
+                                                    self.max_len, self.chunk_tokens)
+            if nbytes:
+                self.ws = _workspace(q.device, self.stream, nbytes)
+
+    # -- launches
+    def _decode(self, entry: str) -> None:
+        if not self.n_dec:
+            return
+        ws = self.ws
+        _native.call(entry, self.q.data_ptr(), self.q.stride(0), *self._pool_args,
+                     _ptr(self._items), _ptr(self._rows), self.n_dec,
+                     self.n_q, self.n_kv, self.head_dim, self.scaling,
+                     self.out.data_ptr(), self.out.stride(0),
+                     _ptr(ws), 0 if ws is None else ws.numel(), self.max_len,
+                     self.chunk_tokens, self.stream.cuda_stream)
+
+    def run_extend(self) -> None:
+        if self.n_work:
+            _native.call("tf_attn_extend", self.q.data_ptr(), self.q.stride(0),
+                         *self._pool_args, self._meta.data_ptr(), self.n_work,
+                         self.n_q, self.n_kv, self.head_dim, self.scaling,
+                         self.out.data_ptr(), self.out.stride(0), self.stream.cuda_stream)
+
+    def run_decode_partial(self) -> None:
+        self._decode("tf_attn_decode_partial")
+
+    def run_decode_merge(self) -> None:
+        self._decode("tf_attn_decode_merge")
+
+    def run(self) -> torch.Tensor:
+        self.run_extend()
+        self._decode("tf_attn_decode")
+        return self.out
 
 
 def slot_based_attention(
@@ -106,98 +237,14 @@ def slot_based_attention(
     """Attention of ``q [T, Hq, D]`` over one layer's slot pool; returns ``[T, Hq, D]``.
 
     ``scaling`` defaults to ``head_dim ** -0.5`` (``full_attention.py:40``).
-    ``k_scale`` / ``v_scale`` (fp32 device scalars) are required for an
+    ``k_scale`` / ``v_scale`` (fp32 device scalars) are required for a
     ``float8_e4m3fn`` pool. ``chunk_tokens`` overrides the decode split size
     (0 = automatic).
     """
-    _check_inputs(q, layer_k_buffer, layer_v_buffer, batch)
-    n_tok, n_q, head_dim = q.shape
-    n_slots, n_kv, _ = layer_k_buffer.shape
-    if n_q % n_kv:
-        raise ValueError(f"num_q_heads {n_q} is not a multiple of num_kv_heads {n_kv}")
-    if scaling is None:
-        scaling = head_dim ** -0.5
-    kv_dtype = _KV_DTYPES[layer_k_buffer.dtype]
-    if kv_dtype == _native.TF_DTYPE_FP8_E4M3:
-        if k_scale is None or v_scale is None:
-            raise ValueError("an fp8 KV pool needs k_scale and v_scale")
-        k_scale = k_scale.to(device=q.device, dtype=torch.float32).reshape(1)
-        v_scale = v_scale.to(device=q.device, dtype=torch.float32).reshape(1)
-    else:
-        k_scale = v_scale = None
-    if q.stride(2) != 1 or q.stride(1) != head_dim:
-        q = q.contiguous()
-    if out is None:
-        out = torch.empty((n_tok, n_q, head_dim), dtype=q.dtype, device=q.device)
-    elif out.shape != q.shape or out.dtype != q.dtype or out.stride(2) != 1 \
-            or out.stride(1) != head_dim:
-        raise ValueError("out must match q's shape/dtype with dense heads and dims")
-
-    bsz = batch.batch_size
-    ext_lens = list(batch.extend_lens)
-    if len(ext_lens) != bsz or sum(ext_lens) != n_tok:
-        raise ValueError(f"extend_lens {ext_lens[:8]}... do not match batch_size={bsz}, "
-                         f"T={n_tok}")
-    if n_tok == 0:
-        return out
-
-    stream = torch.cuda.current_stream(q.device)
-    rtt = batch.req_to_token
-    seq_override = int(batch.max_seq_len) if bsz == 1 else 0
-    max_len = int(batch.max_seq_len)
-    common_pool = (layer_k_buffer.data_ptr(), layer_v_buffer.data_ptr(), n_slots, kv_dtype,
-                   _ptr(k_scale), _ptr(v_scale),
-                   rtt.data_ptr(), rtt.shape[0], rtt.stride(0), rtt.shape[1],
-                   batch.req_pool_indices.data_ptr(), batch.seq_lens.data_ptr(), seq_override)
-
-    def run_decode(items_t, rows_t, n_items):
-        nbytes = _native.decode_workspace_bytes(n_items, n_q, n_kv, head_dim, max_len,
-                                                chunk_tokens)
-        ws = _workspace(q.device, stream, nbytes) if nbytes else None
-        _native.call("tf_attn_decode", q.data_ptr(), q.stride(0), *common_pool,
-                     _ptr(items_t), _ptr(rows_t), n_items,
-                     n_q, n_kv, head_dim, float(scaling), out.data_ptr(), out.stride(0),
-                     _ptr(ws), 0 if ws is None else ws.numel(), max_len, chunk_tokens,
-                     stream.cuda_stream)
-
-    if batch.max_extend_len == 1 or (bsz == 1 and ext_lens[0] == 1):
-        # Pure decode: batch entry b is query row b; nothing to upload.
-        run_decode(None, None, bsz)
-        return out
-
-    # Extend / mixed: plan on the host from extend_lens, one H2D copy.
-    work = plan_extend(ext_lens, n_q, n_kv, decode_to_decode_kernel=True)
-    items, rows = plan_decode_items(ext_lens)
-    n_work, n_dec = len(work), len(items)
-    meta = np.zeros(n_work * 8 + 2 * n_dec + 4, dtype=np.int32)
-    meta[: n_work * 8] = work.reshape(-1)
-    meta[n_work * 8: n_work * 8 + n_dec] = items
-    meta[n_work * 8 + n_dec: n_work * 8 + 2 * n_dec] = rows
-    meta_dev = torch.from_numpy(meta).pin_memory().to(q.device, non_blocking=True)
-    if n_work:
-        _native.call("tf_attn_extend", q.data_ptr(), q.stride(0), *common_pool,
-                     meta_dev.data_ptr(), n_work, n_q, n_kv, head_dim, float(scaling),
-                     out.data_ptr(), out.stride(0), stream.cuda_stream)
-    if n_dec:
-        base = meta_dev.data_ptr() + 4 * n_work * 8
-        items_p = _DevPtr(base)
-        rows_p = _DevPtr(base + 4 * n_dec)
-        run_decode(items_p, rows_p, n_dec)
-    # Keep the upload alive until the kernels that read it have run.
-    meta_dev.record_stream(stream)
-    return out
-
-
-class _DevPtr:
-    """A raw device address posing as a tensor for ``_ptr``."""
-
-    __slots__ = ("_addr",)
-
-    def __init__(self, addr: int):
-        self._addr = addr
-
-    def data_ptr(self) -> int:
-        return self._addr
+    call = SlotAttentionCall(q, layer_k_buffer, layer_v_buffer, batch, scaling=scaling,
+                             k_scale=k_scale, v_scale=v_scale, chunk_tokens=chunk_tokens,
+                             out=out)
+    return call.run()
 
 
 def gather_kv(pool: torch.Tensor, req_to_token: torch.Tensor, req_pool_indices: torch.Tensor,
@@ -213,11 +260,12 @@ def gather_kv(pool: torch.Tensor, req_to_token: torch.Tensor, req_pool_indices: 
     if req_to_token.stride(1) != 1 or req_to_token.dtype != torch.int64:
         raise ValueError("req_to_token must be row-major int64")
     bsz = req_pool_indices.numel()
+    rpi = req_pool_indices.to(torch.int64).contiguous()
     row_elems = int(np.prod(pool.shape[1:]))
     out = torch.empty((bsz, max_len, *pool.shape[1:]), dtype=pool.dtype, device=pool.device)
     _native.call("tf_gather_kv", pool.data_ptr(), dtype_code, pool.shape[0], row_elems,
                  req_to_token.data_ptr(), req_to_token.shape[0], req_to_token.stride(0),
-                 req_to_token.shape[1], req_pool_indices.contiguous().data_ptr(), bsz, max_len,
+                 req_to_token.shape[1], rpi.data_ptr(), bsz, max_len,
                  out.data_ptr(), torch.cuda.current_stream(pool.device).cuda_stream)
     return out
 
@@ -239,14 +287,18 @@ def write_kv(layer_k_buffer: torch.Tensor, layer_v_buffer: torch.Tensor,
     kv_dtype = _KV_DTYPES.get(layer_k_buffer.dtype)
     if kv_dtype is None:
         raise NotImplementedError(f"pool dtype {layer_k_buffer.dtype}")
+    if not (layer_k_buffer.is_contiguous() and layer_v_buffer.is_contiguous()):
+        raise ValueError("KV pools must be contiguous")
     if not (k.is_contiguous() and v.is_contiguous()):
         k, v = k.contiguous(), v.contiguous()
     loc = out_cache_loc.to(torch.int64).contiguous()
+    if loc.numel() != k.shape[0]:
+        raise ValueError(f"out_cache_loc has {loc.numel()} slots for {k.shape[0]} tokens")
     if kv_dtype == _native.TF_DTYPE_FP8_E4M3:
         if k_scale is None or v_scale is None:
             raise ValueError("an fp8 KV pool needs k_scale and v_scale")
-        k_scale = k_scale.to(device=k.device, dtype=torch.float32).reshape(1)
-        v_scale = v_scale.to(device=k.device, dtype=torch.float32).reshape(1)
+        k_scale = k_scale.to(device=k.device, dtype=torch.float32).reshape(1).contiguous()
+        v_scale = v_scale.to(device=k.device, dtype=torch.float32).reshape(1).contiguous()
     n_kv, head_dim = k.shape[1], k.shape[2]
     _native.call("tf_kv_write", k.data_ptr(), v.data_ptr(), k.stride(0), src[k.dtype],
                  loc.data_ptr(), loc.numel(), layer_k_buffer.data_ptr(),

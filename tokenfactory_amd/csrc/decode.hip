@@ -10,13 +10,15 @@
 //           interleaved 16-token tiles of the chunk.
 //   A block keeps the whole GQA head group together, so each K/V row read from
 //   HBM feeds all of the group's q heads.
+// Block prologue: the chunk's slot ids (int64 req_to_token entries, clamped to
+// the pool) are staged in LDS with coalesced loads, and the group's Q^T MFMA
+// fragments are staged in LDS once.
 // Per 16-token tile a wave
-//   * reads the 16 slot ids (lane n <- req_to_token[row, t0 + n]) one tile ahead,
 //   * loads each lane's K slice straight into MFMA A-operand registers
-//     (16-byte loads, 64 contiguous bytes per row per instruction) and its V
-//     slice (four token rows x 16 bytes),
-//   * S^T[token, head] = K * Q^T with v_mfma_f32_16x16x32_bf16 (Q is the
-//     register-resident B operand, heads padded to 16),
+//     (16-byte loads, 64 contiguous bytes of a row per 4 lanes) and its V slice
+//     (four token rows x 16 bytes per lane); the next tile's loads are always in
+//     flight while the current tile computes (register double buffering),
+//   * S^T[token, head] = K * Q^T with v_mfma_f32_16x16x32_bf16 (heads padded to 16),
 //   * online softmax per head (lane-local scores, two xor-shuffles for the max),
 //   * O^T[dim, head] += V^T * P^T with v_mfma_f32_16x16x16_bf16, V^T built in
 //     registers with v_perm_b32 (fp8: byte permutes + v_cvt_scalef32_pk_bf16_fp8).
@@ -26,8 +28,10 @@
 // Merging
 //   waves of a block merge pairwise through LDS in the same lane layout; a block
 //   that is the only split of its unit writes bf16 output directly, otherwise it
-//   stores an fp32 partial (O, max, sum) and bumps the unit's arrival counter; the
-//   last block to arrive merges all partials and resets the counter to zero.
+//   stores an fp32 partial (O, max, sum). A second, small kernel merges the
+//   partials of multi-split units (one workgroup per unit). Keeping the merge in
+//   its own launch avoids device-scope fences in the streaming kernel: on gfx950
+//   those write back and invalidate the whole L2 of the XCD.
 #include <math.h>
 
 #include "tf_common.h"
@@ -36,10 +40,11 @@
 namespace tfa {
 namespace {
 
-constexpr int kD = 256;       // head_dim (Qwen3.8: 256)
+constexpr int kD = 256;         // head_dim (Qwen3.8: 256)
 constexpr int kWaves = 4;
-constexpr int kTile = 16;     // tokens per wave iteration
-constexpr int kAcc = 16;      // f32x4 accumulators per lane (64 output dims)
+constexpr int kTile = 16;       // tokens per wave iteration
+constexpr int kAcc = 16;        // f32x4 accumulators per lane (64 output dims)
+constexpr int kMaxChunk = 4096; // slot ids staged in LDS per block
 
 struct DecodeArgs {
   const __bf16* q;
@@ -60,7 +65,6 @@ struct DecodeArgs {
   float scale_log2;
   __bf16* out;
   int64_t out_stride;
-  int32_t* ws_cnt;
   float* ws_ml;
   float* ws_o;
   int32_t chunk, max_splits;
@@ -71,12 +75,26 @@ struct WaveState {
   f32x4 acc[kAcc];
 };
 
-// Output dim of accumulator element (i, r) for lane group g.
+// LDS slot for one wave's state, element-major so lanes hit consecutive banks.
+struct StateSlot {
+  f32x4 acc[kAcc][kWave];
+  float m[kWave];
+  float l[kWave];
+};
+
+struct DecodeSmem {
+  union {
+    int32_t slots[kMaxChunk];   // main loop: slot id of each chunk token
+    StateSlot merge[2];         // epilogue: wave-state exchange
+  } u;
+  u32x4 qfrag[8][kWave];        // Q^T B-operand fragments, lane-major
+};
+
 template <bool FP8>
-__device__ __forceinline__ int acc_dim(int i, int r, int g) {
-  if (FP8) return 64 * g + 16 * r + i;            // i = e (0..15)
-  return 128 * (i >> 3) + 32 * g + 8 * r + (i & 7);  // i = s*8 + e
-}
+struct TileBuf {
+  u32x4 k[FP8 ? 4 : 8];
+  u32x4 v[4][FP8 ? 1 : 2];
+};
 
 __device__ __forceinline__ void merge_into(WaveState& st, float m2, float l2, const f32x4* acc2) {
   const float M = fmaxf(st.m, m2);
@@ -87,13 +105,6 @@ __device__ __forceinline__ void merge_into(WaveState& st, float m2, float l2, co
   for (int i = 0; i < kAcc; ++i) st.acc[i] = st.acc[i] * a1 + acc2[i] * a2;
   st.m = M;
 }
-
-// LDS slot for one wave's state, element-major so lanes hit consecutive banks.
-struct StateSlot {
-  f32x4 acc[kAcc][kWave];
-  float m[kWave];
-  float l[kWave];
-};
 
 __device__ __forceinline__ void put_state(StateSlot* s, int lane, const WaveState& st) {
 #pragma unroll
@@ -153,16 +164,111 @@ __device__ __forceinline__ void write_output(const DecodeArgs& a, int qrow, int 
   }
 }
 
+// Issues the global loads of tile `it` (tokens it*16 .. it*16+15 of the chunk,
+// clamped to the chunk's last token so every address is a valid row).
 template <bool FP8>
-__global__ void __launch_bounds__(kWaves * kWave)
+__device__ __forceinline__ void issue_tile(TileBuf<FP8>& tb, const int32_t* slots, int it,
+                                           int n_loc, int g, int n, const uint8_t* kbase,
+                                           const uint8_t* vbase, int64_t slot_bytes) {
+  const int last = n_loc - 1;
+  const int t0 = it * kTile;
+  const int64_t ks = slots[min(t0 + n, last)];
+  const uint8_t* kp = kbase + ks * slot_bytes;
+#pragma unroll
+  for (int u = 0; u < (FP8 ? 4 : 8); ++u) tb.k[u] = ld_g16(kp + 64 * u + 16 * g);
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int64_t vs = slots[min(t0 + 4 * g + j, last)];
+    const uint8_t* vp = vbase + vs * slot_bytes;
+#pragma unroll
+    for (int s = 0; s < (FP8 ? 1 : 2); ++s) tb.v[j][s] = ld_g16(vp + 16 * n + 256 * s);
+  }
+}
+
+template <bool FP8>
+__device__ __forceinline__ void compute_tile(const TileBuf<FP8>& tb, const u32x4 (*qfrag)[kWave],
+                                             int it, int n_loc, int g, int lane, float sl2,
+                                             WaveState& st) {
+  // ---- S^T = K Q^T
+  f32x4 sacc = {0.f, 0.f, 0.f, 0.f};
+  if (FP8) {
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      sacc = mfma_16x16x32(e4m3x8_to_bf16x8(tb.k[u][0], tb.k[u][1]), qfrag[2 * u][lane], sacc);
+      sacc = mfma_16x16x32(e4m3x8_to_bf16x8(tb.k[u][2], tb.k[u][3]), qfrag[2 * u + 1][lane],
+                           sacc);
+    }
+  } else {
+#pragma unroll
+    for (int kk = 0; kk < 8; ++kk) sacc = mfma_16x16x32(tb.k[kk], qfrag[kk][lane], sacc);
+  }
+
+  // ---- online softmax for head n over chunk tokens it*16 + 4g + r
+  float sc[4];
+  float mx = -INFINITY;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int t = it * kTile + 4 * g + r;
+    sc[r] = (t < n_loc) ? sacc[r] * sl2 : -INFINITY;
+    mx = fmaxf(mx, sc[r]);
+  }
+  mx = wave_max_xor(mx, 16);
+  mx = wave_max_xor(mx, 32);
+  const float mnew = fmaxf(st.m, mx);
+  const float alpha = fast_exp2(st.m - mnew);
+  float p[4];
+  float psum = 0.f;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    p[r] = fast_exp2(sc[r] - mnew);
+    psum += p[r];
+  }
+  st.l = st.l * alpha + psum;
+  st.m = mnew;
+  if (__ballot(alpha != 1.f)) {
+#pragma unroll
+    for (int i = 0; i < kAcc; ++i) st.acc[i] *= alpha;
+  }
+
+  // ---- O^T += V^T P^T
+  const u32x2 pt = {pack_bf16(p[0], p[1]), pack_bf16(p[2], p[3])};
+  if (FP8) {
+#pragma unroll
+    for (int e = 0; e < 16; e += 2) {
+      const int dw = e >> 2;
+      const uint32_t b0 = e & 3;
+      const uint32_t sel = b0 | ((4 + b0) << 8) | ((b0 + 1) << 16) | ((5 + b0) << 24);
+      const uint32_t x = __builtin_amdgcn_perm(tb.v[1][0][dw], tb.v[0][0][dw], sel);
+      const uint32_t y = __builtin_amdgcn_perm(tb.v[3][0][dw], tb.v[2][0][dw], sel);
+      const u32x2 va = {e4m3x2_to_bf16x2<false>(x), e4m3x2_to_bf16x2<false>(y)};
+      const u32x2 vb = {e4m3x2_to_bf16x2<true>(x), e4m3x2_to_bf16x2<true>(y)};
+      st.acc[e] = mfma_16x16x16(va, pt, st.acc[e]);
+      st.acc[e + 1] = mfma_16x16x16(vb, pt, st.acc[e + 1]);
+    }
+  } else {
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const int dw = e >> 1;
+        const int hi = e & 1;
+        const u32x2 va = {pair_sel(tb.v[1][s][dw], tb.v[0][s][dw], hi),
+                          pair_sel(tb.v[3][s][dw], tb.v[2][s][dw], hi)};
+        st.acc[8 * s + e] = mfma_16x16x16(va, pt, st.acc[8 * s + e]);
+      }
+    }
+  }
+}
+
+template <bool FP8>
+__global__ void __launch_bounds__(kWaves * kWave, 2)
 decode_kernel(DecodeArgs a) {
   constexpr int kRowBytes = FP8 ? kD : 2 * kD;
-  __shared__ StateSlot slots[2];
-  __shared__ int s_last;
+  __shared__ DecodeSmem sm;
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int w = tid >> 6;
+  const int w = wave_id();
   const int g = lane >> 4;
   const int n = lane & 15;
 
@@ -198,29 +304,31 @@ decode_kernel(DecodeArgs a) {
   const int n_split = (L + a.chunk - 1) / a.chunk;
   if (split >= n_split) return;
   const int c0 = split * a.chunk;
-  const int c1 = min(L, c0 + a.chunk);
-  const int n_tiles = (c1 - c0 + kTile - 1) / kTile;
+  const int n_loc = min(L, c0 + a.chunk) - c0;
+  const int n_tiles = (n_loc + kTile - 1) / kTile;
 
-  const int64_t row = clamp_i64(a.rpi[b], 0, a.rtt_rows - 1);
-  const int64_t* rtt = a.rtt + row * a.rtt_stride;
+  // ---- prologue: slot ids of the chunk and the Q^T fragments into LDS
+  {
+    const int64_t row = clamp_i64(a.rpi[b], 0, a.rtt_rows - 1);
+    const int64_t* rtt = a.rtt + row * a.rtt_stride + c0;
+    for (int i = tid; i < n_loc; i += kWaves * kWave)
+      sm.u.slots[i] = (int32_t)clamp_i64(rtt[i], 0, a.pool_slots - 1);
+    if (w == 0) {
+      const __bf16* qp = a.q + (int64_t)qrow * a.q_stride + (int64_t)hq * kD;
+#pragma unroll
+      for (int kk = 0; kk < 8; ++kk) {
+        const int d0 = FP8 ? (64 * (kk >> 1) + 16 * g + 8 * (kk & 1)) : (32 * kk + 8 * g);
+        sm.qfrag[kk][lane] = head_ok ? ld_g16(qp + d0) : u32x4{0u, 0u, 0u, 0u};
+      }
+    }
+  }
   const float kscale = FP8 ? a.k_scale[0] : 1.f;
   const float vscale = FP8 ? a.v_scale[0] : 1.f;
   const float sl2 = a.scale_log2 * kscale;
-
-  // Q^T fragments: lane (g, n) holds q[head n][dims of k-step kk].
-  u32x4 qf[8];
-  {
-    const __bf16* qp = a.q + (int64_t)qrow * a.q_stride + (int64_t)hq * kD;
-#pragma unroll
-    for (int kk = 0; kk < 8; ++kk) {
-      const int d0 = FP8 ? (64 * (kk >> 1) + 16 * g + 8 * (kk & 1)) : (32 * kk + 8 * g);
-      qf[kk] = head_ok ? ld_g16(qp + d0) : u32x4{0u, 0u, 0u, 0u};
-    }
-  }
-
   const uint8_t* kbase = a.k_pool + (int64_t)hk * kRowBytes;
   const uint8_t* vbase = a.v_pool + (int64_t)hk * kRowBytes;
   const int64_t slot_bytes = (int64_t)a.hkv * kRowBytes;
+  __syncthreads();
 
   WaveState st;
   st.m = -INFINITY;
@@ -228,100 +336,21 @@ decode_kernel(DecodeArgs a) {
 #pragma unroll
   for (int i = 0; i < kAcc; ++i) st.acc[i] = f32x4{0.f, 0.f, 0.f, 0.f};
 
+  // ---- main loop: the next tile's loads are issued before the current tile
+  // computes. Issues are unconditional (clamped rows) so the wait counts are
+  // exact; a past-the-end issue re-reads cached rows of the chunk's last token.
   int it = w;
-  int64_t slot_next = 0;
-  if (it < n_tiles) slot_next = rtt[min(c0 + it * kTile + n, c1 - 1)];
-
-  for (; it < n_tiles; it += kWaves) {
-    const int t0 = c0 + it * kTile;
-    const int slot = (int)clamp_i64(slot_next, 0, a.pool_slots - 1);
-    if (it + kWaves < n_tiles) slot_next = rtt[min(t0 + kWaves * kTile + n, c1 - 1)];
-    int vslot[4];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) vslot[j] = __shfl(slot, 4 * g + j, kWave);
-
-    // ---- loads: K row of token t0 + n, V rows of tokens t0 + 4g + j
-    const uint8_t* kp = kbase + (int64_t)slot * slot_bytes;
-    constexpr int kKL = FP8 ? 4 : 8;
-    u32x4 kr[kKL];
-#pragma unroll
-    for (int u = 0; u < kKL; ++u) kr[u] = ld_g16(kp + 64 * u + 16 * g);
-    constexpr int kVL = FP8 ? 1 : 2;
-    u32x4 vr[4][kVL];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const uint8_t* vp = vbase + (int64_t)vslot[j] * slot_bytes;
-#pragma unroll
-      for (int s = 0; s < kVL; ++s) vr[j][s] = ld_g16(vp + 16 * n + 256 * s);
-    }
-
-    // ---- S^T = K Q^T
-    f32x4 sacc = {0.f, 0.f, 0.f, 0.f};
-    if (FP8) {
-#pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        sacc = mfma_16x16x32(e4m3x8_to_bf16x8(kr[u][0], kr[u][1]), qf[2 * u], sacc);
-        sacc = mfma_16x16x32(e4m3x8_to_bf16x8(kr[u][2], kr[u][3]), qf[2 * u + 1], sacc);
-      }
-    } else {
-#pragma unroll
-      for (int kk = 0; kk < 8; ++kk) sacc = mfma_16x16x32(kr[kk], qf[kk], sacc);
-    }
-
-    // ---- online softmax for head n over tokens t0 + 4g + r
-    float sc[4];
-    float mx = -INFINITY;
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int t = t0 + 4 * g + r;
-      sc[r] = (t < c1) ? sacc[r] * sl2 : -INFINITY;
-      mx = fmaxf(mx, sc[r]);
-    }
-    mx = wave_max_xor(mx, 16);
-    mx = wave_max_xor(mx, 32);
-    const float mnew = fmaxf(st.m, mx);
-    const float alpha = fast_exp2(st.m - mnew);
-    float p[4];
-    float psum = 0.f;
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      p[r] = fast_exp2(sc[r] - mnew);
-      psum += p[r];
-    }
-    st.l = st.l * alpha + psum;
-    st.m = mnew;
-    if (__ballot(alpha != 1.f)) {
-#pragma unroll
-      for (int i = 0; i < kAcc; ++i) st.acc[i] *= alpha;
-    }
-
-    // ---- O^T += V^T P^T
-    const u32x2 pt = {pack_bf16(p[0], p[1]), pack_bf16(p[2], p[3])};
-    if (FP8) {
-#pragma unroll
-      for (int e = 0; e < 16; e += 2) {
-        const int dw = e >> 2;
-        const uint32_t b0 = e & 3;
-        const uint32_t sel = b0 | ((4 + b0) << 8) | ((b0 + 1) << 16) | ((5 + b0) << 24);
-        const uint32_t x = __builtin_amdgcn_perm(vr[1][0][dw], vr[0][0][dw], sel);
-        const uint32_t y = __builtin_amdgcn_perm(vr[3][0][dw], vr[2][0][dw], sel);
-        const u32x2 va = {e4m3x2_to_bf16x2<false>(x), e4m3x2_to_bf16x2<false>(y)};
-        const u32x2 vb = {e4m3x2_to_bf16x2<true>(x), e4m3x2_to_bf16x2<true>(y)};
-        st.acc[e] = mfma_16x16x16(va, pt, st.acc[e]);
-        st.acc[e + 1] = mfma_16x16x16(vb, pt, st.acc[e + 1]);
-      }
-    } else {
-#pragma unroll
-      for (int s = 0; s < 2; ++s) {
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          const int dw = e >> 1;
-          const int hi = e & 1;
-          const u32x2 va = {pair_sel(vr[1][s][dw], vr[0][s][dw], hi),
-                            pair_sel(vr[3][s][dw], vr[2][s][dw], hi)};
-          st.acc[8 * s + e] = mfma_16x16x16(va, pt, st.acc[8 * s + e]);
-        }
-      }
+  if (it < n_tiles) {
+    TileBuf<FP8> A, B;
+    issue_tile<FP8>(A, sm.u.slots, it, n_loc, g, n, kbase, vbase, slot_bytes);
+    for (;;) {
+      issue_tile<FP8>(B, sm.u.slots, it + kWaves, n_loc, g, n, kbase, vbase, slot_bytes);
+      compute_tile<FP8>(A, sm.qfrag, it, n_loc, g, lane, sl2, st);
+      if (it + kWaves >= n_tiles) break;
+      issue_tile<FP8>(A, sm.u.slots, it + 2 * kWaves, n_loc, g, n, kbase, vbase, slot_bytes);
+      compute_tile<FP8>(B, sm.qfrag, it + kWaves, n_loc, g, lane, sl2, st);
+      if (it + 2 * kWaves >= n_tiles) break;
+      it += 2 * kWaves;
     }
   }
 
@@ -329,7 +358,7 @@ decode_kernel(DecodeArgs a) {
   st.l += __shfl_xor(st.l, 16, kWave);
   st.l += __shfl_xor(st.l, 32, kWave);
 
-  block_merge(slots, w, lane, st);
+  block_merge(sm.u.merge, w, lane, st);
 
   const int gmax = min(a.group, 16);
   if (n_split == 1) {
@@ -337,9 +366,11 @@ decode_kernel(DecodeArgs a) {
     return;
   }
 
-  // ---- multi-split: publish this block's partial, last arrival merges.
-  const int64_t part = (int64_t)unit * a.max_splits + split;
+  // ---- multi-split: publish this block's fp32 partial (lane layout) for the
+  // merge kernel. Partial p of unit u: O at ws_o[((p*16 + head)*4 + g)*64 ..],
+  // (max, sum) at ws_ml[(p*16 + head)*2 ..], p = u * max_splits + split.
   if (w == 0 && n < gmax) {
+    const int64_t part = (int64_t)unit * a.max_splits + split;
     float* po = a.ws_o + ((part * 16 + n) * 4 + g) * 64;
 #pragma unroll
     for (int i = 0; i < kAcc; ++i) reinterpret_cast<f32x4*>(po)[i] = st.acc[i];
@@ -348,16 +379,40 @@ decode_kernel(DecodeArgs a) {
       a.ws_ml[(part * 16 + n) * 2 + 1] = st.l;
     }
   }
-  __threadfence();
-  __syncthreads();
-  if (tid == 0) {
-    const int prev = atomicAdd(&a.ws_cnt[unit], 1);
-    s_last = (prev == n_split - 1);
-  }
-  __syncthreads();
-  if (!s_last) return;
-  __threadfence();
+}
 
+// Merges the split partials of every unit that has more than one split; one
+// workgroup per unit, waves take splits w, w+4, ... and tree-merge through LDS.
+template <bool FP8>
+__global__ void __launch_bounds__(kWaves * kWave)
+decode_merge_kernel(DecodeArgs a) {
+  __shared__ StateSlot slots[2];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int w = wave_id();
+  const int g = lane >> 4;
+  const int n = lane & 15;
+
+  const int unit = blockIdx.x;
+  const int per_item = a.hkv * a.n_hg;
+  const int item = unit / per_item;
+  const int rem = unit - item * per_item;
+  const int hk = rem / a.n_hg;
+  const int hg = rem - hk * a.n_hg;
+  const int b = a.items ? a.items[item] : item;
+  const int qrow = a.q_rows ? a.q_rows[item] : b;
+  int64_t len = a.seq_override > 0 ? (int64_t)a.seq_override : a.seq_lens[b];
+  if (len > a.rtt_cols) len = a.rtt_cols;
+  const int L = (int)len;
+  const int n_split = L > 0 ? (L + a.chunk - 1) / a.chunk : 0;
+  if (n_split <= 1) return;  // written directly by the split kernel
+  const int hl = hg * 16 + n;
+  const bool head_ok = hl < a.group;
+  const int hq = hk * a.group + (head_ok ? hl : 0);
+  const int gmax = min(a.group, 16);
+  const float vscale = FP8 ? a.v_scale[0] : 1.f;
+
+  WaveState st;
   st.m = -INFINITY;
   st.l = 0.f;
 #pragma unroll
@@ -374,7 +429,6 @@ decode_kernel(DecodeArgs a) {
   }
   block_merge(slots, w, lane, st);
   if (w == 0 && head_ok) write_output<FP8>(a, qrow, hq, g, st, vscale);
-  if (tid == 0) a.ws_cnt[unit] = 0;
 }
 
 }  // namespace
@@ -389,66 +443,53 @@ int make_decode_plan(int32_t n_items, int32_t num_q_heads, int32_t num_kv_heads,
   if (head_dim != kD)
     return fail(TF_ERR_UNSUPPORTED, "decode: head_dim=%d (only %d is built)", head_dim, kD);
   if (max_seq_len < 1) max_seq_len = 1;
-  if (chunk_tokens < 0 || chunk_tokens % 64)
-    return fail(TF_ERR_INVALID, "decode: chunk_tokens=%d must be a multiple of 64", chunk_tokens);
+  if (chunk_tokens < 0 || chunk_tokens % 64 || chunk_tokens > kMaxChunk)
+    return fail(TF_ERR_INVALID, "decode: chunk_tokens=%d must be a multiple of 64 <= %d",
+                chunk_tokens, kMaxChunk);
   const int32_t group = num_q_heads / num_kv_heads;
   p->n_hgroups = (group + 15) / 16;
   p->gmax = group < 16 ? group : 16;
   p->n_units = (int64_t)n_items * num_kv_heads * p->n_hgroups;
   int32_t chunk = chunk_tokens;
   if (chunk == 0) {
-    // Aim for ~8 workgroups per CU on a 256-CU part; keep chunks between
-    // 256 and 8192 tokens and at most 64 splits per unit.
+    // Aim for ~8 workgroups per CU on a 256-CU part; chunks of 256..4096 tokens.
     const int64_t units = p->n_units > 0 ? p->n_units : 1;
     int64_t want = (2048 + units - 1) / units;
     if (want < 1) want = 1;
     int64_t c = ((int64_t)max_seq_len + want - 1) / want;
     c = (c + 63) / 64 * 64;
-    const int64_t floor64 = ((int64_t)max_seq_len + 63) / 64 * 64;
+    const int64_t fit = ((int64_t)max_seq_len + 63) / 64 * 64;
     int64_t lo = 256;
-    if (lo > floor64) lo = floor64;
+    if (lo > fit) lo = fit;
     if (c < lo) c = lo;
-    if (c > 8192) c = 8192;
-    while ((max_seq_len + c - 1) / c > 64) c += 64;
+    if (c > kMaxChunk) c = kMaxChunk;
     chunk = (int32_t)c;
   }
   p->chunk = chunk;
   p->max_splits = (max_seq_len + chunk - 1) / chunk;
   const int64_t parts = p->n_units * p->max_splits;
-  p->cnt_bytes = (p->n_units * 4 + 255) / 256 * 256;
   p->ml_bytes = (parts * 16 * 2 * 4 + 255) / 256 * 256;
   p->o_bytes = parts * 16 * (int64_t)kD * 4;
-  p->total_bytes = p->max_splits > 1 ? p->cnt_bytes + p->ml_bytes + p->o_bytes : 0;
+  p->total_bytes = p->max_splits > 1 ? p->ml_bytes + p->o_bytes : 0;
   return TF_OK;
 }
 
 }  // namespace tfa
 
-extern "C" {
+namespace tfa {
+namespace {
 
-int64_t tf_attn_decode_workspace_bytes(int32_t n_items, int32_t num_q_heads,
-                                       int32_t num_kv_heads, int32_t head_dim,
-                                       int32_t max_seq_len, int32_t chunk_tokens) {
-  tfa::clear_error();
-  tfa::DecodePlan p;
-  const int rc = tfa::make_decode_plan(n_items, num_q_heads, num_kv_heads, head_dim,
-                                       max_seq_len, chunk_tokens, &p);
-  if (rc != TF_OK) return rc;
-  return p.total_bytes;
-}
+enum : int { kPhasePartial = 1, kPhaseMerge = 2 };
 
-int32_t tf_attn_decode(const void* q, int64_t q_row_stride, const void* k_pool,
-                       const void* v_pool, int64_t pool_slots, int32_t kv_dtype,
-                       const float* k_scale, const float* v_scale,
-                       const int64_t* req_to_token, int64_t rtt_rows,
-                       int64_t rtt_row_stride, int64_t rtt_cols,
-                       const int64_t* req_pool_indices, const int64_t* seq_lens,
-                       int32_t seq_len_override, const int32_t* items,
-                       const int32_t* q_rows, int32_t n_items, int32_t num_q_heads,
-                       int32_t num_kv_heads, int32_t head_dim, float scale, void* out,
-                       int64_t out_row_stride, void* workspace, int64_t workspace_bytes,
-                       int32_t max_seq_len, int32_t chunk_tokens, tf_stream_t stream) {
-  using namespace tfa;
+int decode_launch(const void* q, int64_t q_row_stride, const void* k_pool, const void* v_pool,
+                  int64_t pool_slots, int32_t kv_dtype, const float* k_scale,
+                  const float* v_scale, const int64_t* req_to_token, int64_t rtt_rows,
+                  int64_t rtt_row_stride, int64_t rtt_cols, const int64_t* req_pool_indices,
+                  const int64_t* seq_lens, int32_t seq_len_override, const int32_t* items,
+                  const int32_t* q_rows, int32_t n_items, int32_t num_q_heads,
+                  int32_t num_kv_heads, int32_t head_dim, float scale, void* out,
+                  int64_t out_row_stride, void* workspace, int64_t workspace_bytes,
+                  int32_t max_seq_len, int32_t chunk_tokens, tf_stream_t stream, int phases) {
   clear_error();
   DecodePlan p;
   int rc = make_decode_plan(n_items, num_q_heads, num_kv_heads, head_dim, max_seq_len,
@@ -472,7 +513,8 @@ int32_t tf_attn_decode(const void* q, int64_t q_row_stride, const void* k_pool,
   if (q_row_stride < (int64_t)num_q_heads * head_dim ||
       out_row_stride < (int64_t)num_q_heads * head_dim)
     return fail(TF_ERR_INVALID, "decode: row stride smaller than num_q_heads*head_dim");
-  if (p.total_bytes > 0 && (!workspace || workspace_bytes < p.total_bytes || !aligned16(workspace)))
+  if (p.total_bytes > 0 &&
+      (!workspace || workspace_bytes < p.total_bytes || !aligned16(workspace)))
     return fail(TF_ERR_INVALID, "decode: workspace needs %lld bytes, got %lld",
                 (long long)p.total_bytes, (long long)workspace_bytes);
   const int64_t grid = p.n_units * p.max_splits;
@@ -502,18 +544,74 @@ int32_t tf_attn_decode(const void* q, int64_t q_row_stride, const void* k_pool,
   a.out = static_cast<__bf16*>(out);
   a.out_stride = out_row_stride;
   char* ws = static_cast<char*>(workspace);
-  a.ws_cnt = p.total_bytes ? reinterpret_cast<int32_t*>(ws) : nullptr;
-  a.ws_ml = p.total_bytes ? reinterpret_cast<float*>(ws + p.cnt_bytes) : nullptr;
-  a.ws_o = p.total_bytes ? reinterpret_cast<float*>(ws + p.cnt_bytes + p.ml_bytes) : nullptr;
+  a.ws_ml = p.total_bytes ? reinterpret_cast<float*>(ws) : nullptr;
+  a.ws_o = p.total_bytes ? reinterpret_cast<float*>(ws + p.ml_bytes) : nullptr;
   a.chunk = p.chunk;
   a.max_splits = p.max_splits;
 
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-  if (kv_dtype == TF_DTYPE_FP8_E4M3)
-    hipLaunchKernelGGL(decode_kernel<true>, dim3((unsigned)grid), dim3(kWaves * kWave), 0, s, a);
-  else
-    hipLaunchKernelGGL(decode_kernel<false>, dim3((unsigned)grid), dim3(kWaves * kWave), 0, s, a);
-  return launch_status("tf_attn_decode launch");
+  const dim3 block(kWaves * kWave);
+  const bool fp8 = kv_dtype == TF_DTYPE_FP8_E4M3;
+  if (phases & kPhasePartial) {
+    if (fp8)
+      hipLaunchKernelGGL(decode_kernel<true>, dim3((unsigned)grid), block, 0, s, a);
+    else
+      hipLaunchKernelGGL(decode_kernel<false>, dim3((unsigned)grid), block, 0, s, a);
+    rc = launch_status("tf_attn_decode partial launch");
+    if (rc != TF_OK) return rc;
+  }
+  if ((phases & kPhaseMerge) && p.max_splits > 1) {
+    if (fp8)
+      hipLaunchKernelGGL(decode_merge_kernel<true>, dim3((unsigned)p.n_units), block, 0, s, a);
+    else
+      hipLaunchKernelGGL(decode_merge_kernel<false>, dim3((unsigned)p.n_units), block, 0, s, a);
+    rc = launch_status("tf_attn_decode merge launch");
+  }
+  return rc;
+}
+
+}  // namespace
+}  // namespace tfa
+
+#define TF_DECODE_PARAMS                                                                    \
+  const void *q, int64_t q_row_stride, const void *k_pool, const void *v_pool,            \
+      int64_t pool_slots, int32_t kv_dtype, const float *k_scale, const float *v_scale,    \
+      const int64_t *req_to_token, int64_t rtt_rows, int64_t rtt_row_stride,               \
+      int64_t rtt_cols, const int64_t *req_pool_indices, const int64_t *seq_lens,          \
+      int32_t seq_len_override, const int32_t *items, const int32_t *q_rows,               \
+      int32_t n_items, int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,        \
+      float scale, void *out, int64_t out_row_stride, void *workspace,                     \
+      int64_t workspace_bytes, int32_t max_seq_len, int32_t chunk_tokens,                  \
+      tf_stream_t stream
+#define TF_DECODE_ARGS                                                                      \
+  q, q_row_stride, k_pool, v_pool, pool_slots, kv_dtype, k_scale, v_scale, req_to_token,   \
+      rtt_rows, rtt_row_stride, rtt_cols, req_pool_indices, seq_lens, seq_len_override,    \
+      items, q_rows, n_items, num_q_heads, num_kv_heads, head_dim, scale, out,             \
+      out_row_stride, workspace, workspace_bytes, max_seq_len, chunk_tokens, stream
+
+extern "C" {
+
+int64_t tf_attn_decode_workspace_bytes(int32_t n_items, int32_t num_q_heads,
+                                       int32_t num_kv_heads, int32_t head_dim,
+                                       int32_t max_seq_len, int32_t chunk_tokens) {
+  tfa::clear_error();
+  tfa::DecodePlan p;
+  const int rc = tfa::make_decode_plan(n_items, num_q_heads, num_kv_heads, head_dim,
+                                       max_seq_len, chunk_tokens, &p);
+  if (rc != TF_OK) return rc;
+  return p.total_bytes;
+}
+
+int32_t tf_attn_decode(TF_DECODE_PARAMS) {
+  return tfa::decode_launch(TF_DECODE_ARGS, tfa::kPhasePartial | tfa::kPhaseMerge);
+}
+
+int32_t tf_attn_decode_partial(TF_DECODE_PARAMS) {
+  return tfa::decode_launch(TF_DECODE_ARGS, tfa::kPhasePartial);
+}
+
+int32_t tf_attn_decode_merge(TF_DECODE_PARAMS) {
+  return tfa::decode_launch(TF_DECODE_ARGS, tfa::kPhaseMerge);
 }
 
 }  // extern "C"

@@ -145,7 +145,7 @@ extend_kernel(ExtendArgs a) {
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int w = tid >> 6;
+  const int w = wave_id();
   const int g = lane >> 5;
   const int n = lane & 31;
 

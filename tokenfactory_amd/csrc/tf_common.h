@@ -92,6 +92,12 @@ __device__ __forceinline__ u32x4 e4m3x8_to_bf16x8(uint32_t d0, uint32_t d1) {
   return r;
 }
 
+// Wave index within the workgroup as a scalar (wave-uniform) value, so loops
+// and branches keyed on it compile to scalar control flow.
+__device__ __forceinline__ int wave_id() {
+  return __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+}
+
 // ---------------------------------------------------------------- math
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 

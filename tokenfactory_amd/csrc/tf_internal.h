@@ -25,7 +25,7 @@ struct DecodePlan {
   int32_t n_hgroups;    // ceil(group / 16)
   int32_t gmax;         // min(group, 16)
   int64_t n_units;      // items * kv_heads * n_hgroups
-  int64_t cnt_bytes, ml_bytes, o_bytes, total_bytes;
+  int64_t ml_bytes, o_bytes, total_bytes;  // split partials: (max, sum) and O
 };
 int make_decode_plan(int32_t n_items, int32_t num_q_heads, int32_t num_kv_heads,
                      int32_t head_dim, int32_t max_seq_len, int32_t chunk_tokens,
