@@ -1,0 +1,310 @@
+"""Benchmark of the MI355X full-attention hot path (one GPU).
+
+Headline (``value``): decode attention over the slot-indirected KV pool for a
+64-request step of the 27B hybrid model's full-attention layer at TP=1 -
+batch 64, context lengths uniform in [1k, 8k], 24 q / 4 kv heads, head_dim 256,
+bf16 KV in a 1M-slot pool with randomly scattered slots - as whole-job HBM
+throughput: algorithmic bytes (K/V rows + int64 slot ids + q in + out) divided
+by the time of the step's launches (streaming kernel + split merge), inputs
+resident in HBM. Two independent step instances alternate so the 256 MB
+Infinity Cache cannot serve one step's KV from the previous step.
+
+``roofline`` covers the dominant kernel (the streaming decode kernel), timed
+with HIP events recorded on the stream it is launched on. ``secondary`` holds
+the other serving shapes (prefill/extend with radix prefixes on MFMA, the mixed
+chunked-prefill + decode step, fp8-KV decode at 128k context) with their own
+roofline fractions. ``cpu_baseline`` times the oracle's op-for-op restatement of
+the reference's CPU decode path on a bounded sample of the same step.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--only ...] [--no-cpu]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+REPO = Path(__file__).resolve().parent
+sys.path.insert(0, str(REPO))
+
+HBM_PEAK = 8.0e12          # MI355X HBM3E bytes/s
+MFMA_BF16_PEAK = 2.5e15    # MI355X dense bf16 FLOP/s
+METRIC = ("decode attn HBM GB/s (% peak) + prefill attn TFLOP/s (% MFMA peak), 1 MI355X")
+
+
+def log(msg):
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--only", default="decode,extend,mixed,fp8",
+                    help="comma list of decode,extend,mixed,fp8,copy")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--chunk", type=int, default=0, help="decode split size (0 = auto)")
+    return ap.parse_args()
+
+
+class Timer:
+    """HIP events on the launch stream around selected launches of each step."""
+
+    def __init__(self, torch, stream):
+        self.torch = torch
+        self.stream = stream
+        self.pairs = []
+
+    def mark(self):
+        ev = self.torch.cuda.Event(enable_timing=True)
+        ev.record(self.stream)
+        return ev
+
+    def total_ms(self, pairs):
+        return sum(a.elapsed_time(b) for a, b in pairs)
+
+
+def time_steps(torch, calls, steps, warmup, phases):
+    """Runs ``steps`` timed steps cycling over ``calls``. ``phases`` maps a phase
+    name to the list of call methods to run in that phase; each phase of each
+    step is bracketed by events. Returns (ms_per_step, {phase: ms_per_step})."""
+    stream = torch.cuda.current_stream()
+    for i in range(warmup):
+        for fns in phases.values():
+            for fn in fns(calls[i % len(calls)]):
+                fn()
+    torch.cuda.synchronize()
+    t = Timer(torch, stream)
+    per_phase = {name: [] for name in phases}
+    start = t.mark()
+    for i in range(steps):
+        call = calls[i % len(calls)]
+        for name, fns in phases.items():
+            a = t.mark()
+            for fn in fns(call):
+                fn()
+            per_phase[name].append((a, t.mark()))
+    end = t.mark()
+    torch.cuda.synchronize()
+    total = start.elapsed_time(end) / steps
+    return total, {k: t.total_ms(v) / steps for k, v in per_phase.items()}
+
+
+def bench_decode(torch, workloads, SlotAttentionCall, args):
+    log("building decode_b64 (2 independent instances, 1M-slot pools)")
+    wls = [workloads.decode_b64(device="cuda", seed=11), workloads.decode_b64(device="cuda",
+                                                                              seed=12)]
+    calls = [SlotAttentionCall(w.q, w.k_pool, w.v_pool, w.batch, scaling=w.scale,
+                               chunk_tokens=args.chunk) for w in wls]
+    nbytes = sum(w.decode_bytes() for w in wls) / len(wls)
+    ms, ph = time_steps(torch, calls, args.steps, args.warmup, {
+        "partial": lambda c: [c.run_decode_partial],
+        "merge": lambda c: [c.run_decode_merge],
+    })
+    value = nbytes / (ms * 1e-3)
+    ach = nbytes / (ph["partial"] * 1e-3)
+    res = {
+        "value": value, "ms_per_step": ms, "bytes_per_step": nbytes,
+        "roofline": {"bound": "hbm", "achieved": ach / 1e9, "peak": HBM_PEAK / 1e9,
+                     "unit": "GB/s", "frac": ach / HBM_PEAK, "traffic": None,
+                     "kernel": "decode_kernel<bf16> (tf_attn_decode_partial)",
+                     "kernel_ms": ph["partial"], "merge_ms": ph["merge"]},
+        "workloads": wls,
+    }
+    log(f"decode_b64: {ms*1e3:.1f} us/step, {value/1e9:.0f} GB/s ({value/HBM_PEAK*100:.1f}% "
+        f"of HBM peak); streaming kernel {ph['partial']*1e3:.1f} us "
+        f"({ach/HBM_PEAK*100:.1f}%)")
+    return res
+
+
+def bench_extend(torch, workloads, SlotAttentionCall, args):
+    log("building extend_prefix (16 requests, 4 radix groups)")
+    wl = workloads.extend_prefix(device="cuda")
+    call = SlotAttentionCall(wl.q, wl.k_pool, wl.v_pool, wl.batch, scaling=wl.scale)
+    steps = max(3, args.steps // 5)
+    ms, ph = time_steps(torch, [call], steps, max(1, args.warmup // 5),
+                        {"extend": lambda c: [c.run_extend]})
+    flops = wl.extend_flops()
+    tf = flops / (ph["extend"] * 1e-3)
+    log(f"extend_prefix: {ms*1e3:.1f} us/step, {tf/1e12:.1f} TFLOP/s "
+        f"({tf/MFMA_BF16_PEAK*100:.1f}% of bf16 MFMA peak)")
+    return {"workload": "extend_prefix: 16 requests in 4 radix-prefix groups of 4, prefix "
+                        "U[0,4k] shared per group, new tokens U[512,2k], causal, 24q/4kv, "
+                        "head_dim 256, bf16",
+            "value": tf / 1e12, "unit": "TFLOP/s", "ms_per_step": ms, "steps": steps,
+            "flops_per_step": flops,
+            "roofline": {"bound": "mfma", "achieved": tf / 1e12, "peak": MFMA_BF16_PEAK / 1e12,
+                         "unit": "TFLOP/s", "frac": tf / MFMA_BF16_PEAK,
+                         "kernel": "extend_kernel<bf16>"}}
+
+
+def bench_mixed(torch, workloads, SlotAttentionCall, args):
+    log("building mixed (4 x 2k extend + 128 decode, 2M-slot pool)")
+    wl = workloads.mixed(device="cuda")
+    call = SlotAttentionCall(wl.q, wl.k_pool, wl.v_pool, wl.batch, scaling=wl.scale)
+    steps = max(3, args.steps // 5)
+    ms, ph = time_steps(torch, [call], steps, max(1, args.warmup // 5), {
+        "extend": lambda c: [c.run_extend],
+        "decode": lambda c: [c.run_decode_partial, c.run_decode_merge]})
+    flops, nbytes = wl.extend_flops(), wl.decode_bytes()
+    bound_ms = (flops / MFMA_BF16_PEAK + nbytes / HBM_PEAK) * 1e3
+    log(f"mixed: {ms*1e3:.1f} us/step (extend {ph['extend']*1e3:.1f}, decode "
+        f"{ph['decode']*1e3:.1f}); serial roofline {bound_ms*1e3:.0f} us "
+        f"({bound_ms/ms*100:.1f}%)")
+    return {"workload": "mixed: 4 extend requests of 2048 new tokens on U[0,8k] prefixes + "
+                        "128 decode requests with contexts U[512,16k], 24q/4kv, head_dim 256, "
+                        "bf16, one launch sequence",
+            "value": bound_ms / ms, "unit": "fraction of serial roofline",
+            "ms_per_step": ms, "steps": steps,
+            "extend_ms": ph["extend"], "decode_ms": ph["decode"],
+            "extend_tflops": flops / (ph["extend"] * 1e-3) / 1e12,
+            "decode_gbps": nbytes / (ph["decode"] * 1e-3) / 1e9,
+            "roofline": {"bound": "mfma+hbm (serial)", "achieved": bound_ms / ms, "peak": 1.0,
+                         "unit": "fraction", "frac": bound_ms / ms}}
+
+
+def bench_fp8(torch, workloads, SlotAttentionCall, args):
+    log("building decode_fp8_128k (8 x 128k tokens, fp8-e4m3 KV)")
+    wl = workloads.decode_fp8_128k(device="cuda")
+    call = SlotAttentionCall(wl.q, wl.k_pool, wl.v_pool, wl.batch, scaling=wl.scale,
+                             k_scale=wl.k_scale, v_scale=wl.v_scale)
+    ms, ph = time_steps(torch, [call], args.steps, args.warmup, {
+        "partial": lambda c: [c.run_decode_partial],
+        "merge": lambda c: [c.run_decode_merge]})
+    nbytes = wl.decode_bytes()
+    value = nbytes / (ms * 1e-3)
+    ach = nbytes / (ph["partial"] * 1e-3)
+    log(f"decode_fp8_128k: {ms*1e3:.1f} us/step, {value/1e9:.0f} GB/s "
+        f"({value/HBM_PEAK*100:.1f}%); streaming kernel {ach/HBM_PEAK*100:.1f}%")
+    return {"workload": "decode_fp8_128k: batch 8, 131072-token contexts, 24q/4kv, head_dim "
+                        "256, fp8-e4m3 KV with per-tensor scales amax/448, bf16 queries",
+            "value": value / 1e9, "unit": "GB/s", "ms_per_step": ms, "steps": args.steps,
+            "bytes_per_step": nbytes,
+            "roofline": {"bound": "hbm", "achieved": ach / 1e9, "peak": HBM_PEAK / 1e9,
+                         "unit": "GB/s", "frac": ach / HBM_PEAK,
+                         "kernel": "decode_kernel<fp8>"}}
+
+
+def bench_copy(torch, args):
+    """A plain device copy of known size, the reference point for HBM counters."""
+    n = 1 << 30
+    src = torch.empty(n, dtype=torch.uint8, device="cuda")
+    dst = torch.empty_like(src)
+    ms, _ = time_steps(torch, [None], args.steps, args.warmup,
+                       {"copy": lambda c: [lambda: dst.copy_(src)]})
+    log(f"copy 1 GiB: {ms*1e3:.1f} us, {2*n/(ms*1e-3)/1e9:.0f} GB/s (read+write)")
+    return {"bytes_read": n, "bytes_written": n, "ms": ms}
+
+
+def cpu_baseline(torch, dec_res):
+    """The oracle's restatement of the reference decode branch, fp32, host cores."""
+    from oracle.harness import prepare_host_inputs
+    from oracle.slot_attention import slot_based_attention_ref
+    from tokenfactory_amd.workloads import subset
+    wl = dec_res["workloads"][0]
+    pick = [0, 17, 40, 63]
+    sub = subset(wl, pick)
+    host_args = prepare_host_inputs(sub)
+    cores = min(16, len(os.sched_getaffinity(0)))
+    torch.set_num_threads(cores)
+    fn = lambda: slot_based_attention_ref(*host_args)
+    fn()
+    times = []
+    t_end = time.perf_counter() + 15.0
+    while time.perf_counter() < t_end or len(times) < 3:
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+    times.sort()
+    med = times[len(times) // 2]
+    nbytes = sub.decode_bytes()
+    # The restatement reads fp32 K/V; report the same algorithmic (bf16) bytes as the GPU.
+    log(f"cpu baseline: {med*1e3:.1f} ms per 4-request sample on {cores} threads "
+        f"({nbytes/med/1e9:.2f} GB/s)")
+    cpu = None
+    try:
+        with open("/proc/cpuinfo") as fh:
+            cpu = next((ln.split(":", 1)[1].strip() for ln in fh if "model name" in ln), None)
+    except OSError:
+        pass
+    return {"value": nbytes / med / 1e9, "unit": "GB/s", "cores": cores, "kind": "port",
+            "sample": f"4 of the 64 decode requests (contexts {sub.seq_lens}), fp32 op-for-op "
+                      f"restatement of full_attention.py:215-242 (padded gather, "
+                      f"repeat_interleave, -inf mask, SDPA); median of {len(times)} runs; "
+                      f"same algorithmic bytes as the GPU line",
+            "ms_per_sample": med * 1e3, "cpu_model": cpu}
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build measures one GPU only: the full-attention "
+                                   "path needs no collective at TP=1 (see DESIGN.md for how "
+                                   "it would shard); run with --gpus 1"}))
+        sys.exit(2)
+    import torch
+    if not torch.cuda.is_available():
+        print(json.dumps({"error": "no ROCm GPU visible"}))
+        sys.exit(1)
+    from tokenfactory_amd import _native, workloads
+    from tokenfactory_amd.attention import SlotAttentionCall
+    _native.load()
+    only = set(args.only.split(","))
+    secondary = {}
+    dec = None
+    if "copy" in only:
+        secondary["copy_1gib"] = bench_copy(torch, args)
+    if "decode" in only:
+        dec = bench_decode(torch, workloads, SlotAttentionCall, args)
+    if "extend" in only:
+        secondary["extend_prefix"] = bench_extend(torch, workloads, SlotAttentionCall, args)
+        torch.cuda.empty_cache()
+    if "mixed" in only:
+        secondary["mixed"] = bench_mixed(torch, workloads, SlotAttentionCall, args)
+        torch.cuda.empty_cache()
+    if "fp8" in only:
+        secondary["decode_fp8_128k"] = bench_fp8(torch, workloads, SlotAttentionCall, args)
+        torch.cuda.empty_cache()
+    if dec is None:
+        print(json.dumps({"metric": METRIC, "value": None, "secondary": secondary},
+                         default=float))
+        return
+    traffic_file = REPO / "profiles" / "decode_b64_hbm_traffic.json"
+    if traffic_file.exists():
+        try:
+            dec["roofline"]["traffic"] = json.loads(traffic_file.read_text()).get(
+                "bytes_per_launch")
+        except (ValueError, OSError):
+            pass
+    cpu = None if args.no_cpu else cpu_baseline(torch, dec)
+    line = {
+        "metric": METRIC,
+        "value": dec["value"] / 1e9,
+        "unit": "GB/s",
+        "pct_of_peak": dec["value"] / HBM_PEAK * 100,
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": dec["ms_per_step"],
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1) q/K/V, random scattered slots)",
+        "config": {"workload": "decode_b64: batch 64, contexts U[1k,8k], 24 q / 4 kv heads, "
+                               "head_dim 256, softmax scale 1/16, bf16 KV in a 1M-slot pool "
+                               "with randomly scattered slots (two alternating instances)",
+                   "bytes_per_step": dec["bytes_per_step"], "decode_chunk": args.chunk},
+        "roofline": dec["roofline"],
+        "cpu_baseline": cpu,
+        "secondary": secondary,
+    }
+    print(json.dumps(line, default=float))
+
+
+if __name__ == "__main__":
+    main()

@@ -201,6 +201,38 @@ def build(name: str, seq_lens: List[int], ext_lens: List[int], *, num_q_heads: i
                           "shared_prefix_lens": shared_prefix_lens})
 
 
+def rebatch(wl: Workload, seq_lens, ext_lens, q, rows=None) -> Workload:
+    """A workload sharing ``wl``'s pools and req_to_token table, with new
+    per-request lengths and queries (rows default to the first len(seq_lens)
+    rows of ``wl``)."""
+    import copy
+    rows = list(rows if rows is not None else wl.rows[:len(seq_lens)])
+    dev = wl.q.device
+    t = lambda x: torch.tensor(list(x), dtype=torch.long, device=dev)
+    batch = ForwardBatch(
+        batch_size=len(seq_lens), req_pool_indices=t(rows), seq_lens=t(seq_lens),
+        prefix_lens=t([L - e for L, e in zip(seq_lens, ext_lens)]),
+        extend_lens=list(ext_lens), out_cache_loc=t([0] * sum(ext_lens)),
+        req_to_token=wl.batch.req_to_token, is_prefill=max(ext_lens) > 1,
+        max_seq_len=max(seq_lens), max_extend_len=max(ext_lens),
+        extend_lens_tensor=t(ext_lens), req_pool_indices_list=rows)
+    new = copy.copy(wl)
+    new.q = q
+    new.batch = batch
+    new.seq_lens = list(seq_lens)
+    new.ext_lens = list(ext_lens)
+    new.rows = rows
+    return new
+
+
+def subset(wl: Workload, indices) -> Workload:
+    """The requests ``indices`` of ``wl`` as their own batch (same pools)."""
+    starts = np.cumsum([0] + list(wl.ext_lens))
+    q = torch.cat([wl.q[starts[i]:starts[i + 1]] for i in indices])
+    return rebatch(wl, [wl.seq_lens[i] for i in indices], [wl.ext_lens[i] for i in indices],
+                   q, rows=[wl.rows[i] for i in indices])
+
+
 # ---------------------------------------------------------------- named configs
 
 def decode_cpu_small(device="cpu", seed=7) -> Workload:
