@@ -47,7 +47,8 @@ def parse():
     ap.add_argument("--only", default="decode,extend,mixed,fp8",
                     help="comma list of decode,extend,mixed,fp8,copy")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
-    ap.add_argument("--chunk", type=int, default=0, help="decode split size (0 = auto)")
+    ap.add_argument("--workgroups", type=int, default=0,
+                    help="decode persistent grid size (0 = two per CU)")
     return ap.parse_args()
 
 
@@ -99,7 +100,7 @@ def bench_decode(torch, workloads, SlotAttentionCall, args):
     wls = [workloads.decode_b64(device="cuda", seed=11), workloads.decode_b64(device="cuda",
                                                                               seed=12)]
     calls = [SlotAttentionCall(w.q, w.k_pool, w.v_pool, w.batch, scaling=w.scale,
-                               chunk_tokens=args.chunk) for w in wls]
+                               decode_workgroups=args.workgroups) for w in wls]
     nbytes = sum(w.decode_bytes() for w in wls) / len(wls)
     ms, ph = time_steps(torch, calls, args.steps, args.warmup, {
         "partial": lambda c: [c.run_decode_partial],
@@ -298,7 +299,8 @@ def main():
         "config": {"workload": "decode_b64: batch 64, contexts U[1k,8k], 24 q / 4 kv heads, "
                                "head_dim 256, softmax scale 1/16, bf16 KV in a 1M-slot pool "
                                "with randomly scattered slots (two alternating instances)",
-                   "bytes_per_step": dec["bytes_per_step"], "decode_chunk": args.chunk},
+                   "bytes_per_step": dec["bytes_per_step"],
+                   "decode_workgroups": args.workgroups or "2 per CU"},
         "roofline": dec["roofline"],
         "cpu_baseline": cpu,
         "secondary": secondary,

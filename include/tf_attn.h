@@ -66,7 +66,7 @@ int32_t tf_attn_abi_version(void);
 const char* tf_attn_last_error(void);
 
 /* ------------------------------------------------------------------ decode
- * Split-K decode attention: one new token per request (ext_b == 1).
+ * Decode attention: one new token per request (ext_b == 1).
  * Replaces the pure-decode branch, full_attention.py:215-242, and the
  * ext_len == 1 case of the bsz == 1 branch, full_attention.py:179-213.
  *
@@ -74,14 +74,16 @@ const char* tf_attn_last_error(void);
  * items is NULL) and reads / writes query row q_rows[i] (or items[i] / i when
  * q_rows is NULL) of q and out.
  *
+ * The streaming kernel runs a persistent grid of num_workgroups workgroups
+ * (0 = two per compute unit) that split the (request, kv head, 16-token tile)
+ * work evenly, whatever the length mix; a request's kv head that spans several
+ * workgroups leaves fp32 partials that the merge phase combines.
+ * At most 2048 requests per call.
  * workspace: device scratch of tf_attn_decode_workspace_bytes(...) bytes (no
- * initialisation needed; 0 bytes when every request fits one split).  It holds
- * the fp32 split partials between the two phases.  Calls that overlap in time
- * must not share a workspace.
- * chunk_tokens: context tokens per workgroup (multiple of 64, <= 4096), or 0 to
- * let the library choose from max_seq_len and n_items.
+ * initialisation needed) holding the partials between the two phases.  Calls
+ * that overlap in time must not share a workspace.
  * max_seq_len: an upper bound of every L_b processed (host int, as
- * ForwardBatch.max_seq_len).
+ * ForwardBatch.max_seq_len); kept for the caller's bookkeeping.
  *
  * tf_attn_decode runs both phases.  tf_attn_decode_partial runs the
  * HBM-streaming split kernel only (requests that fit one split get their final
@@ -92,7 +94,7 @@ const char* tf_attn_last_error(void);
  */
 int64_t tf_attn_decode_workspace_bytes(int32_t n_items, int32_t num_q_heads,
                                        int32_t num_kv_heads, int32_t head_dim,
-                                       int32_t max_seq_len, int32_t chunk_tokens);
+                                       int32_t max_seq_len, int32_t num_workgroups);
 
 int32_t tf_attn_decode(const void* q, int64_t q_row_stride,
                        const void* k_pool, const void* v_pool, int64_t pool_slots,
@@ -105,7 +107,7 @@ int32_t tf_attn_decode(const void* q, int64_t q_row_stride,
                        int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
                        float scale, void* out, int64_t out_row_stride,
                        void* workspace, int64_t workspace_bytes,
-                       int32_t max_seq_len, int32_t chunk_tokens, tf_stream_t stream);
+                       int32_t max_seq_len, int32_t num_workgroups, tf_stream_t stream);
 
 int32_t tf_attn_decode_partial(const void* q, int64_t q_row_stride,
                                const void* k_pool, const void* v_pool, int64_t pool_slots,
@@ -118,7 +120,7 @@ int32_t tf_attn_decode_partial(const void* q, int64_t q_row_stride,
                                int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
                                float scale, void* out, int64_t out_row_stride,
                                void* workspace, int64_t workspace_bytes,
-                               int32_t max_seq_len, int32_t chunk_tokens, tf_stream_t stream);
+                               int32_t max_seq_len, int32_t num_workgroups, tf_stream_t stream);
 
 int32_t tf_attn_decode_merge(const void* q, int64_t q_row_stride,
                              const void* k_pool, const void* v_pool, int64_t pool_slots,
@@ -131,7 +133,7 @@ int32_t tf_attn_decode_merge(const void* q, int64_t q_row_stride,
                              int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
                              float scale, void* out, int64_t out_row_stride,
                              void* workspace, int64_t workspace_bytes,
-                             int32_t max_seq_len, int32_t chunk_tokens, tf_stream_t stream);
+                             int32_t max_seq_len, int32_t num_workgroups, tf_stream_t stream);
 
 /* ------------------------------------------------------------------ extend
  * Causal prefill / extend attention over cached prefix + new tokens, bf16

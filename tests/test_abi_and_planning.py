@@ -36,17 +36,18 @@ def test_every_declared_symbol_is_exported_and_bound():
     assert not unbound, unbound
 
 
-def test_decode_workspace_size_and_unsupported_head_dim():
-    assert _native.decode_workspace_bytes(4, 16, 2, 256, 512, 1024) == 0   # one split
-    n = _native.decode_workspace_bytes(64, 24, 4, 256, 8192, 1024)
-    units, splits = 64 * 4, 8
-    assert n >= units * splits * 16 * 256 * 4
+def test_decode_workspace_size_and_unsupported_arguments():
+    # One partial slot per (unit) + one per workgroup: index b + u is unique.
+    n = _native.decode_workspace_bytes(64, 24, 4, 256, 8192, 512)
+    assert n >= (64 * 4 + 512) * 16 * 256 * 4
     with pytest.raises(NotImplementedError):
-        _native.decode_workspace_bytes(4, 16, 2, 128, 512, 0)
+        _native.decode_workspace_bytes(4, 16, 2, 128, 512, 0)       # head_dim 128 not built
+    with pytest.raises(NotImplementedError):
+        _native.decode_workspace_bytes(4096, 16, 2, 256, 512, 0)    # > 2048 requests
     with pytest.raises(ValueError):
-        _native.decode_workspace_bytes(4, 16, 3, 256, 512, 0)
+        _native.decode_workspace_bytes(4, 16, 3, 256, 512, 0)       # 16 % 3 != 0
     with pytest.raises(ValueError):
-        _native.decode_workspace_bytes(4, 16, 2, 256, 512, 100)     # not a multiple of 64
+        _native.decode_workspace_bytes(4, 16, 2, 256, 512, -1)
 
 
 def test_entry_points_reject_bad_arguments_before_launching():

@@ -14,15 +14,16 @@ from tokenfactory_amd import _native, slot_based_attention, workloads
 pytestmark = pytest.mark.gpu
 
 
-def run(wl, chunk=0):
+def run(wl, workgroups=0):
     return slot_based_attention(wl.q, wl.k_pool, wl.v_pool, wl.batch, scaling=wl.scale,
-                                k_scale=wl.k_scale, v_scale=wl.v_scale, chunk_tokens=chunk)
+                                k_scale=wl.k_scale, v_scale=wl.v_scale,
+                                decode_workgroups=workgroups)
 
 
-def check(wl, chunk=0, what=""):
+def check(wl, workgroups=0, what=""):
     print(f"[decode] {what} B={wl.batch.batch_size} L<={wl.batch.max_seq_len} "
-          f"Hq={wl.num_q_heads} Hkv={wl.num_kv_heads} chunk={chunk}", flush=True)
-    out = run(wl, chunk)
+          f"Hq={wl.num_q_heads} Hkv={wl.num_kv_heads} workgroups={workgroups}", flush=True)
+    out = run(wl, workgroups)
     torch.cuda.synchronize()
     return assert_attn_close(out, restatement(wl), what=what)
 
@@ -39,13 +40,24 @@ def test_single_request_lengths(gpu, L):
     check(wl, what=f"bsz1 L={L}")
 
 
-@pytest.mark.parametrize("chunk", [0, 64, 256, 1024])
-def test_multi_split_merge(gpu, chunk):
+@pytest.mark.parametrize("workgroups", [0, 1, 3, 7, 64, 513, 4096])
+def test_balanced_split_and_merge(gpu, workgroups):
+    """Any grid size: one workgroup owning every unit, workgroups straddling unit
+    boundaries, and far more workgroups than tiles (empty ranges)."""
     rng = np.random.default_rng(3)
     lens = rng.integers(1, 3000, size=7).tolist()
     wl = small_case(lens, [1] * 7, hq=24, hkv=4, d=256, seed=4, device=gpu,
                     dtype=torch.bfloat16)
-    check(wl, chunk, what=f"chunk={chunk}")
+    check(wl, workgroups, what=f"workgroups={workgroups}")
+
+
+def test_empty_and_tiny_requests(gpu):
+    """L = 1 units next to long ones; many units per workgroup."""
+    lens = [1, 2, 4000, 1, 17, 33, 1, 900]
+    wl = small_case(lens, [1] * len(lens), hq=24, hkv=4, d=256, seed=8, device=gpu,
+                    dtype=torch.bfloat16)
+    for wg in (0, 5, 40):
+        check(wl, wg, what=f"tiny wg={wg}")
 
 
 def test_workspace_reuse_across_shapes(gpu):
@@ -55,7 +67,7 @@ def test_workspace_reuse_across_shapes(gpu):
                      device=gpu, dtype=torch.bfloat16)
     small = rebatch(big, [2500, 17], [1, 1], big.q[1:3].clone(), rows=big.rows[1:3])
     for wl in (big, small, big, small):
-        check(wl, 128, what="reuse")
+        check(wl, 37, what="reuse")
 
 
 def test_split_phases_compose_to_full_call(gpu):
@@ -63,7 +75,7 @@ def test_split_phases_compose_to_full_call(gpu):
     wl = small_case([2000, 33, 4100], [1, 1, 1], hq=24, hkv=4, d=256, seed=6, device=gpu,
                     dtype=torch.bfloat16)
     call = SlotAttentionCall(wl.q, wl.k_pool, wl.v_pool, wl.batch, scaling=wl.scale,
-                             chunk_tokens=512)
+                             decode_workgroups=29)
     full = call.run().clone()
     call.out.zero_()
     call.run_decode_partial()
@@ -76,21 +88,21 @@ def test_split_phases_compose_to_full_call(gpu):
 def test_group_sizes(gpu, hq, hkv):
     wl = small_case([300, 1, 77, 1500], [1] * 4, hq=hq, hkv=hkv, d=256, seed=hq + hkv,
                     device=gpu, dtype=torch.bfloat16)
-    check(wl, 256, what=f"G={hq // hkv}")
+    check(wl, 24, what=f"G={hq // hkv}")
 
 
 def test_peaky_softmax(gpu):
     """Large-norm queries make the softmax concentrate on few keys."""
     wl = small_case([900, 2049], [1, 1], hq=24, hkv=4, d=256, seed=9, device=gpu,
                     dtype=torch.bfloat16, q_std=6.0)
-    check(wl, 256, what="peaky")
+    check(wl, 24, what="peaky")
 
 
 def test_shared_prefix_rows_give_identical_outputs(gpu):
     wl = small_case([700, 700, 420], [1, 1, 1], hq=24, hkv=4, d=256, seed=10, device=gpu,
                     dtype=torch.bfloat16, groups=[0, 0, 1], prefixes=[700, 400])
     wl.q[1] = wl.q[0]
-    out = run(wl, 128)
+    out = run(wl)
     assert torch.equal(out[0], out[1])
     assert_attn_close(out, restatement(wl), what="shared prefix")
 
@@ -100,7 +112,7 @@ def test_fp8_kv_decode(gpu, lens):
     wl = workloads.build("fp8", lens, [1] * len(lens), num_q_heads=24, num_kv_heads=4,
                          head_dim=256, pool_slots=sum(lens) + 100, device=gpu, seed=31,
                          kv_fp8=True)
-    check(wl, 256, what="fp8")
+    check(wl, 24, what="fp8")
 
 
 def test_decode_rows_via_item_list(gpu):
@@ -124,6 +136,7 @@ def test_full_size_decode_b64_sampled(gpu):
     sub = rebatch(wl, [wl.seq_lens[i] for i in pick], [1] * 4, wl.q[pick].clone(),
                   rows=[wl.rows[i] for i in pick])
     assert_attn_close(out[pick], restatement(sub), what="b64 sample")
-    # With the split size pinned, a request's split boundaries and merge order do
-    # not depend on the rest of the batch, so its output row is bit-identical.
-    assert torch.equal(run(sub, 1024), run(wl, 1024)[pick])
+    # The same rows computed inside a 4-request batch are split differently over
+    # the workgroups; only fp32 summation order may differ.
+    assert_attn_close(run(sub), out[pick], atol=4e-3, rtol=4e-3, norm_rel=4e-3,
+                      what="batch composition")

@@ -12,7 +12,7 @@ from pathlib import Path
 from typing import Optional
 
 LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libtf_attn.so"
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 TF_DTYPE_BF16 = 0
 TF_DTYPE_FP8_E4M3 = 1
@@ -41,7 +41,7 @@ SIGNATURES = {
         _p, _p, _i32,                  # items, q_rows, n_items
         _i32, _i32, _i32, _f32,        # num_q_heads, num_kv_heads, head_dim, scale
         _p, _i64,                      # out, out_row_stride
-        _p, _i64, _i32, _i32,          # workspace, workspace_bytes, max_seq_len, chunk_tokens
+        _p, _i64, _i32, _i32,          # workspace, workspace_bytes, max_seq_len, num_workgroups
         _p,                            # stream
     ]),
     "tf_attn_decode_partial": None,   # same signature as tf_attn_decode
@@ -134,10 +134,10 @@ def call(name: str, *args) -> int:
 
 
 def decode_workspace_bytes(n_items, num_q_heads, num_kv_heads, head_dim, max_seq_len,
-                           chunk_tokens=0) -> int:
+                           num_workgroups=0) -> int:
     lib = load()
     n = lib.tf_attn_decode_workspace_bytes(n_items, num_q_heads, num_kv_heads, head_dim,
-                                           max_seq_len, chunk_tokens)
+                                           max_seq_len, num_workgroups)
     if n < 0:
         msg = lib.tf_attn_last_error().decode(errors="replace")
         if n == TF_ERR_UNSUPPORTED:

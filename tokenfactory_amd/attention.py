@@ -116,7 +116,8 @@ class SlotAttentionCall:
     """
 
     def __init__(self, q, layer_k_buffer, layer_v_buffer, batch, *, scaling=None,
-                 k_scale=None, v_scale=None, chunk_tokens: int = 0, out=None, stream=None):
+                 k_scale=None, v_scale=None, decode_workgroups: int = 0, out=None,
+                 stream=None):
         _check_inputs(q, layer_k_buffer, layer_v_buffer, batch)
         n_tok, n_q, head_dim = q.shape
         n_slots, n_kv, _ = layer_k_buffer.shape
@@ -152,7 +153,7 @@ class SlotAttentionCall:
         self.stream = stream if stream is not None else torch.cuda.current_stream(q.device)
         self.n_q, self.n_kv, self.head_dim = n_q, n_kv, head_dim
         self.scaling = float(scaling)
-        self.chunk_tokens = int(chunk_tokens)
+        self.decode_workgroups = int(decode_workgroups)
         self.max_len = int(batch.max_seq_len)
         rtt = batch.req_to_token
         seq_override = self.max_len if bsz == 1 else 0
@@ -187,7 +188,7 @@ class SlotAttentionCall:
         self.ws = None
         if self.n_dec:
             nbytes = _native.decode_workspace_bytes(self.n_dec, n_q, n_kv, head_dim,
-                                                    self.max_len, self.chunk_tokens)
+                                                    self.max_len, self.decode_workgroups)
             if nbytes:
                 self.ws = _workspace(q.device, self.stream, nbytes)
 
@@ -201,7 +202,7 @@ class SlotAttentionCall:
                      self.n_q, self.n_kv, self.head_dim, self.scaling,
                      self.out.data_ptr(), self.out.stride(0),
                      _ptr(ws), 0 if ws is None else ws.numel(), self.max_len,
-                     self.chunk_tokens, self.stream.cuda_stream)
+                     self.decode_workgroups, self.stream.cuda_stream)
 
     def run_extend(self) -> None:
         if self.n_work:
@@ -231,19 +232,19 @@ def slot_based_attention(
     scaling: Optional[float] = None,
     k_scale: Optional[torch.Tensor] = None,
     v_scale: Optional[torch.Tensor] = None,
-    chunk_tokens: int = 0,
+    decode_workgroups: int = 0,
     out: Optional[torch.Tensor] = None,
 ) -> torch.Tensor:
     """Attention of ``q [T, Hq, D]`` over one layer's slot pool; returns ``[T, Hq, D]``.
 
     ``scaling`` defaults to ``head_dim ** -0.5`` (``full_attention.py:40``).
     ``k_scale`` / ``v_scale`` (fp32 device scalars) are required for a
-    ``float8_e4m3fn`` pool. ``chunk_tokens`` overrides the decode split size
-    (0 = automatic).
+    ``float8_e4m3fn`` pool. ``decode_workgroups`` overrides the size of the
+    decode kernel's persistent grid (0 = two workgroups per compute unit).
     """
     call = SlotAttentionCall(q, layer_k_buffer, layer_v_buffer, batch, scaling=scaling,
-                             k_scale=k_scale, v_scale=v_scale, chunk_tokens=chunk_tokens,
-                             out=out)
+                             k_scale=k_scale, v_scale=v_scale,
+                             decode_workgroups=decode_workgroups, out=out)
     return call.run()
 
 

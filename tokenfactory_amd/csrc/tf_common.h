@@ -27,6 +27,10 @@ constexpr float kLog2e = 1.4426950408889634f;
 __device__ __forceinline__ u32x4 ld_g16(const void* p) {
   return *reinterpret_cast<const u32x4*>(p);
 }
+// Streaming (nontemporal) 16-byte load for data read exactly once.
+__device__ __forceinline__ u32x4 ld_nt16(const void* p) {
+  return __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+}
 __device__ __forceinline__ u32x2 ld_g8(const void* p) {
   return *reinterpret_cast<const u32x2*>(p);
 }

@@ -18,17 +18,16 @@ int launch_status(const char* what);
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 inline bool aligned8(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 7u) == 0; }
 
-// Decode split plan shared by the launcher and the workspace-size query.
+// Decode plan shared by the launcher and the workspace-size query.
 struct DecodePlan {
-  int32_t chunk;        // context tokens per workgroup
-  int32_t max_splits;   // ceil(max_seq_len / chunk)
+  int32_t n_blocks;     // workgroups of the streaming kernel (2 per CU by default)
   int32_t n_hgroups;    // ceil(group / 16)
   int32_t gmax;         // min(group, 16)
   int64_t n_units;      // items * kv_heads * n_hgroups
   int64_t ml_bytes, o_bytes, total_bytes;  // split partials: (max, sum) and O
 };
 int make_decode_plan(int32_t n_items, int32_t num_q_heads, int32_t num_kv_heads,
-                     int32_t head_dim, int32_t max_seq_len, int32_t chunk_tokens,
+                     int32_t head_dim, int32_t max_seq_len, int32_t num_workgroups,
                      DecodePlan* plan);
 
 }  // namespace tfa
