@@ -48,51 +48,45 @@ def parse():
                     help="comma list of decode,extend,mixed,fp8,copy")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--workgroups", type=int, default=0,
-                    help="decode persistent grid size (0 = two per CU)")
+                    help="decode persistent grid size (0 = one per CU)")
     return ap.parse_args()
 
 
-class Timer:
-    """HIP events on the launch stream around selected launches of each step."""
-
-    def __init__(self, torch, stream):
-        self.torch = torch
-        self.stream = stream
-        self.pairs = []
-
-    def mark(self):
-        ev = self.torch.cuda.Event(enable_timing=True)
-        ev.record(self.stream)
-        return ev
-
-    def total_ms(self, pairs):
-        return sum(a.elapsed_time(b) for a, b in pairs)
+def _event(torch, stream):
+    ev = torch.cuda.Event(enable_timing=True)
+    ev.record(stream)
+    return ev
 
 
-def time_steps(torch, calls, steps, warmup, phases):
-    """Runs ``steps`` timed steps cycling over ``calls``. ``phases`` maps a phase
-    name to the list of call methods to run in that phase; each phase of each
-    step is bracketed by events. Returns (ms_per_step, {phase: ms_per_step})."""
+def time_steps(torch, calls, steps, warmup, step_fns):
+    """Whole-step time: ``warmup`` untimed steps, then ``steps`` steps cycling over
+    ``calls`` between one pair of HIP events on the launch stream (no event in
+    between, so nothing idles the GPU inside the timed region). Returns ms/step."""
     stream = torch.cuda.current_stream()
     for i in range(warmup):
-        for fns in phases.values():
-            for fn in fns(calls[i % len(calls)]):
-                fn()
+        for fn in step_fns(calls[i % len(calls)]):
+            fn()
     torch.cuda.synchronize()
-    t = Timer(torch, stream)
-    per_phase = {name: [] for name in phases}
-    start = t.mark()
+    start = _event(torch, stream)
     for i in range(steps):
-        call = calls[i % len(calls)]
-        for name, fns in phases.items():
-            a = t.mark()
-            for fn in fns(call):
-                fn()
-            per_phase[name].append((a, t.mark()))
-    end = t.mark()
+        for fn in step_fns(calls[i % len(calls)]):
+            fn()
+    end = _event(torch, stream)
     torch.cuda.synchronize()
-    total = start.elapsed_time(end) / steps
-    return total, {k: t.total_ms(v) / steps for k, v in per_phase.items()}
+    return start.elapsed_time(end) / steps
+
+
+def time_kernel(torch, calls, steps, launch):
+    """Average duration of one kernel: every launch bracketed by HIP events
+    recorded on the stream the kernel is launched on. Returns ms/launch."""
+    stream = torch.cuda.current_stream()
+    pairs = []
+    for i in range(steps):
+        a = _event(torch, stream)
+        launch(calls[i % len(calls)])
+        pairs.append((a, _event(torch, stream)))
+    torch.cuda.synchronize()
+    return sum(a.elapsed_time(b) for a, b in pairs) / steps
 
 
 def bench_decode(torch, workloads, SlotAttentionCall, args):
@@ -102,23 +96,22 @@ def bench_decode(torch, workloads, SlotAttentionCall, args):
     calls = [SlotAttentionCall(w.q, w.k_pool, w.v_pool, w.batch, scaling=w.scale,
                                decode_workgroups=args.workgroups) for w in wls]
     nbytes = sum(w.decode_bytes() for w in wls) / len(wls)
-    ms, ph = time_steps(torch, calls, args.steps, args.warmup, {
-        "partial": lambda c: [c.run_decode_partial],
-        "merge": lambda c: [c.run_decode_merge],
-    })
+    ms = time_steps(torch, calls, args.steps, args.warmup, lambda c: [c.run])
+    k_ms = time_kernel(torch, calls, args.steps, lambda c: c.run_decode_partial())
+    m_ms = time_kernel(torch, calls, args.steps, lambda c: c.run_decode_merge())
     value = nbytes / (ms * 1e-3)
-    ach = nbytes / (ph["partial"] * 1e-3)
+    ach = nbytes / (k_ms * 1e-3)
     res = {
         "value": value, "ms_per_step": ms, "bytes_per_step": nbytes,
         "roofline": {"bound": "hbm", "achieved": ach / 1e9, "peak": HBM_PEAK / 1e9,
                      "unit": "GB/s", "frac": ach / HBM_PEAK, "traffic": None,
                      "kernel": "decode_kernel<bf16> (tf_attn_decode_partial)",
-                     "kernel_ms": ph["partial"], "merge_ms": ph["merge"]},
+                     "kernel_ms": k_ms, "merge_kernel_ms": m_ms},
         "workloads": wls,
     }
     log(f"decode_b64: {ms*1e3:.1f} us/step, {value/1e9:.0f} GB/s ({value/HBM_PEAK*100:.1f}% "
-        f"of HBM peak); streaming kernel {ph['partial']*1e3:.1f} us "
-        f"({ach/HBM_PEAK*100:.1f}%)")
+        f"of HBM peak); streaming kernel {k_ms*1e3:.1f} us ({ach/HBM_PEAK*100:.1f}%), "
+        f"merge kernel {m_ms*1e3:.1f} us")
     return res
 
 
@@ -127,17 +120,17 @@ def bench_extend(torch, workloads, SlotAttentionCall, args):
     wl = workloads.extend_prefix(device="cuda")
     call = SlotAttentionCall(wl.q, wl.k_pool, wl.v_pool, wl.batch, scaling=wl.scale)
     steps = max(3, args.steps // 5)
-    ms, ph = time_steps(torch, [call], steps, max(1, args.warmup // 5),
-                        {"extend": lambda c: [c.run_extend]})
+    ms = time_steps(torch, [call], steps, max(1, args.warmup // 5), lambda c: [c.run])
+    k_ms = time_kernel(torch, [call], steps, lambda c: c.run_extend())
     flops = wl.extend_flops()
-    tf = flops / (ph["extend"] * 1e-3)
+    tf = flops / (k_ms * 1e-3)
     log(f"extend_prefix: {ms*1e3:.1f} us/step, {tf/1e12:.1f} TFLOP/s "
         f"({tf/MFMA_BF16_PEAK*100:.1f}% of bf16 MFMA peak)")
     return {"workload": "extend_prefix: 16 requests in 4 radix-prefix groups of 4, prefix "
                         "U[0,4k] shared per group, new tokens U[512,2k], causal, 24q/4kv, "
                         "head_dim 256, bf16",
-            "value": tf / 1e12, "unit": "TFLOP/s", "ms_per_step": ms, "steps": steps,
-            "flops_per_step": flops,
+            "value": flops / (ms * 1e-3) / 1e12, "unit": "TFLOP/s", "ms_per_step": ms,
+            "steps": steps, "flops_per_step": flops, "kernel_ms": k_ms,
             "roofline": {"bound": "mfma", "achieved": tf / 1e12, "peak": MFMA_BF16_PEAK / 1e12,
                          "unit": "TFLOP/s", "frac": tf / MFMA_BF16_PEAK,
                          "kernel": "extend_kernel<bf16>"}}
@@ -148,20 +141,20 @@ def bench_mixed(torch, workloads, SlotAttentionCall, args):
     wl = workloads.mixed(device="cuda")
     call = SlotAttentionCall(wl.q, wl.k_pool, wl.v_pool, wl.batch, scaling=wl.scale)
     steps = max(3, args.steps // 5)
-    ms, ph = time_steps(torch, [call], steps, max(1, args.warmup // 5), {
-        "extend": lambda c: [c.run_extend],
-        "decode": lambda c: [c.run_decode_partial, c.run_decode_merge]})
+    ms = time_steps(torch, [call], steps, max(1, args.warmup // 5), lambda c: [c.run])
+    ph = {"extend": time_kernel(torch, [call], steps, lambda c: c.run_extend()),
+          "decode": time_kernel(torch, [call], steps, lambda c: c.run_decode_partial())}
     flops, nbytes = wl.extend_flops(), wl.decode_bytes()
     bound_ms = (flops / MFMA_BF16_PEAK + nbytes / HBM_PEAK) * 1e3
-    log(f"mixed: {ms*1e3:.1f} us/step (extend {ph['extend']*1e3:.1f}, decode "
-        f"{ph['decode']*1e3:.1f}); serial roofline {bound_ms*1e3:.0f} us "
+    log(f"mixed: {ms*1e3:.1f} us/step (extend kernel {ph['extend']*1e3:.1f}, decode streaming "
+        f"kernel {ph['decode']*1e3:.1f}); serial roofline {bound_ms*1e3:.0f} us "
         f"({bound_ms/ms*100:.1f}%)")
     return {"workload": "mixed: 4 extend requests of 2048 new tokens on U[0,8k] prefixes + "
                         "128 decode requests with contexts U[512,16k], 24q/4kv, head_dim 256, "
                         "bf16, one launch sequence",
             "value": bound_ms / ms, "unit": "fraction of serial roofline",
             "ms_per_step": ms, "steps": steps,
-            "extend_ms": ph["extend"], "decode_ms": ph["decode"],
+            "extend_kernel_ms": ph["extend"], "decode_kernel_ms": ph["decode"],
             "extend_tflops": flops / (ph["extend"] * 1e-3) / 1e12,
             "decode_gbps": nbytes / (ph["decode"] * 1e-3) / 1e9,
             "roofline": {"bound": "mfma+hbm (serial)", "achieved": bound_ms / ms, "peak": 1.0,
@@ -173,18 +166,17 @@ def bench_fp8(torch, workloads, SlotAttentionCall, args):
     wl = workloads.decode_fp8_128k(device="cuda")
     call = SlotAttentionCall(wl.q, wl.k_pool, wl.v_pool, wl.batch, scaling=wl.scale,
                              k_scale=wl.k_scale, v_scale=wl.v_scale)
-    ms, ph = time_steps(torch, [call], args.steps, args.warmup, {
-        "partial": lambda c: [c.run_decode_partial],
-        "merge": lambda c: [c.run_decode_merge]})
+    ms = time_steps(torch, [call], args.steps, args.warmup, lambda c: [c.run])
+    k_ms = time_kernel(torch, [call], args.steps, lambda c: c.run_decode_partial())
     nbytes = wl.decode_bytes()
     value = nbytes / (ms * 1e-3)
-    ach = nbytes / (ph["partial"] * 1e-3)
+    ach = nbytes / (k_ms * 1e-3)
     log(f"decode_fp8_128k: {ms*1e3:.1f} us/step, {value/1e9:.0f} GB/s "
         f"({value/HBM_PEAK*100:.1f}%); streaming kernel {ach/HBM_PEAK*100:.1f}%")
     return {"workload": "decode_fp8_128k: batch 8, 131072-token contexts, 24q/4kv, head_dim "
                         "256, fp8-e4m3 KV with per-tensor scales amax/448, bf16 queries",
             "value": value / 1e9, "unit": "GB/s", "ms_per_step": ms, "steps": args.steps,
-            "bytes_per_step": nbytes,
+            "bytes_per_step": nbytes, "kernel_ms": k_ms,
             "roofline": {"bound": "hbm", "achieved": ach / 1e9, "peak": HBM_PEAK / 1e9,
                          "unit": "GB/s", "frac": ach / HBM_PEAK,
                          "kernel": "decode_kernel<fp8>"}}
@@ -195,8 +187,8 @@ def bench_copy(torch, args):
     n = 1 << 30
     src = torch.empty(n, dtype=torch.uint8, device="cuda")
     dst = torch.empty_like(src)
-    ms, _ = time_steps(torch, [None], args.steps, args.warmup,
-                       {"copy": lambda c: [lambda: dst.copy_(src)]})
+    ms = time_steps(torch, [None], args.steps, args.warmup,
+                    lambda c: [lambda: dst.copy_(src)])
     log(f"copy 1 GiB: {ms*1e3:.1f} us, {2*n/(ms*1e-3)/1e9:.0f} GB/s (read+write)")
     return {"bytes_read": n, "bytes_written": n, "ms": ms}
 
@@ -300,7 +292,7 @@ def main():
                                "head_dim 256, softmax scale 1/16, bf16 KV in a 1M-slot pool "
                                "with randomly scattered slots (two alternating instances)",
                    "bytes_per_step": dec["bytes_per_step"],
-                   "decode_workgroups": args.workgroups or "2 per CU"},
+                   "decode_workgroups": args.workgroups or "1 per CU"},
         "roofline": dec["roofline"],
         "cpu_baseline": cpu,
         "secondary": secondary,

@@ -75,7 +75,7 @@ const char* tf_attn_last_error(void);
  * q_rows is NULL) of q and out.
  *
  * The streaming kernel runs a persistent grid of num_workgroups workgroups
- * (0 = two per compute unit) that split the (request, kv head, 16-token tile)
+ * (0 = one per compute unit) that split the (request, kv head, 16-token tile)
  * work evenly, whatever the length mix; a request's kv head that spans several
  * workgroups leaves fp32 partials that the merge phase combines.
  * At most 2048 requests per call.

@@ -99,12 +99,18 @@ def test_peaky_softmax(gpu):
 
 
 def test_shared_prefix_rows_give_identical_outputs(gpu):
+    """Two requests on one radix prefix with the same query.  The persistent grid
+    may cut them at different tile boundaries, so only the fp32 summation order
+    of their splits may differ; with one workgroup per request they are equal."""
     wl = small_case([700, 700, 420], [1, 1, 1], hq=24, hkv=4, d=256, seed=10, device=gpu,
                     dtype=torch.bfloat16, groups=[0, 0, 1], prefixes=[700, 400])
     wl.q[1] = wl.q[0]
     out = run(wl)
-    assert torch.equal(out[0], out[1])
+    assert_attn_close(out[1], out[0], atol=4e-3, rtol=4e-3, norm_rel=4e-3,
+                      what="shared prefix rows")
     assert_attn_close(out, restatement(wl), what="shared prefix")
+    one = run(wl, workgroups=1)
+    assert torch.equal(one[0], one[1])
 
 
 @pytest.mark.parametrize("lens", [[5, 700, 64], [4096, 33]])

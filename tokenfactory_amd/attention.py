@@ -240,7 +240,7 @@ def slot_based_attention(
     ``scaling`` defaults to ``head_dim ** -0.5`` (``full_attention.py:40``).
     ``k_scale`` / ``v_scale`` (fp32 device scalars) are required for a
     ``float8_e4m3fn`` pool. ``decode_workgroups`` overrides the size of the
-    decode kernel's persistent grid (0 = two workgroups per compute unit).
+    decode kernel's persistent grid (0 = one workgroup per compute unit).
     """
     call = SlotAttentionCall(q, layer_k_buffer, layer_v_buffer, batch, scaling=scaling,
                              k_scale=k_scale, v_scale=v_scale,

@@ -12,16 +12,18 @@
 // (32 per wave), so all G heads of a GQA group share every K/V tile.
 // Row (t, h) attends to context positions 0 .. P + t, P = L - ext.
 //
-// Per 32-key tile the workgroup
-//   * gathers the 32 K rows (slot ids from req_to_token) into LDS row-major,
-//   * gathers the 32 V rows, transposes 4x8 blocks in registers and stores V^T
-//     (dim-major, keys in the order the PV operand wants) into LDS,
-// and each wave computes, with v_mfma_f32_32x32x16_bf16,
-//   S^T[key, row] = K * Q^T   (Q^T register-resident, K from LDS),
-//   online softmax per row (the 32 keys of a row live in lanes n and n + 32),
-//   O^T[dim, row] += V^T * P^T (V^T from LDS, P^T from the S^T registers),
-// so each lane owns one row: its max, sum and 128 of its output dims.
-// The next tile's global loads are issued before the current tile's MFMAs.
+// Per 64-key tile (LDS double-buffered, one barrier per tile):
+//   * the next tile's K and V rows are gathered with coalesced 16-byte loads
+//     (slot ids come from an LDS slot buffer refilled 1024 keys at a time)
+//     before the current tile's MFMAs are issued;
+//   * K lands in LDS row-major with chunk c of key k at k*32 + (c ^ (k & 31));
+//     V is transposed in registers (8 keys x 8 dims per thread) and lands as
+//     V^T rows of 64 keys in the order the PV operand wants, chunk-swizzled;
+//   * each wave computes, with v_mfma_f32_32x32x16_bf16,
+//       S^T[key, row] = K * Q^T   (Q^T register-resident, K from LDS),
+//       the online softmax per row (a row's 64 keys live in lanes n and n + 32),
+//       O^T[dim, row] += V^T * P^T (V^T from LDS, P^T straight from S^T),
+//     so each lane owns one row: its max, sum and 128 of its output dims.
 #include <math.h>
 
 #include "tf_common.h"
@@ -32,12 +34,13 @@ namespace {
 
 constexpr int kD = 256;
 constexpr int kWaves = 4;
+constexpr int kThreads = kWaves * kWave;
 constexpr int kRowsPerWave = 32;
-constexpr int kBN = 32;                    // keys per tile
-constexpr int kKStride = 2 * kD + 16;      // LDS bytes per K row (padded)
-constexpr int kVStride = 2 * kBN + 16;     // LDS bytes per V^T row (padded)
-constexpr int kKTile = kBN * kKStride;     // 16896
-constexpr int kVTile = kD * kVStride;      // 20480
+constexpr int kBN = 64;                     // keys per tile
+constexpr int kKChunks = 32;                // 16-byte chunks per K row (512 B)
+constexpr int kVChunks = kBN / 8;           // 16-byte chunks per V^T row (64 keys)
+constexpr int kSlotChunk = 1024;            // keys per slot-buffer refill
+constexpr int kTilesPerSlotChunk = kSlotChunk / kBN;
 
 struct ExtendArgs {
   const __bf16* q;
@@ -59,89 +62,113 @@ struct ExtendArgs {
   int64_t out_stride;
 };
 
-// Key position (within a 32-key tile) held at V^T LDS position `pos`:
-// within each 16-key half, 4-key blocks [0,1,2,3] sit at [0,2,1,3].
-__device__ __forceinline__ int vt_pos_block(int key_block) {
-  const int half = key_block >> 2;
-  const int q = key_block & 3;
-  return 4 * half + (((q & 1) << 1) | (q >> 1));
+struct ExtendSmem {
+  u32x4 k[2][kBN * kKChunks];      // 2 x 32 KB
+  u32x4 vt[2][kD * kVChunks];      // 2 x 32 KB
+  int32_t slots[2][kSlotChunk];    // 2 x 4 KB
+};
+
+// Key (0..63 within the tile) stored at V^T position p: within each 16-key
+// group st, position 8g + j holds key 16st + 8(j/4) + 4g + (j%4), the order of
+// the P^T operand taken from the S^T accumulator layout.
+__device__ __forceinline__ int key_at_pos(int p) {
+  const int st = p >> 4, g = (p >> 3) & 1, j = p & 7;
+  return 16 * st + 8 * (j >> 2) + 4 * g + (j & 3);
 }
 
+__device__ __forceinline__ int vt_swz(int row) { return (row ^ (row >> 3)) & 7; }
+
+// Registers holding one tile's gathered rows for this thread.
+//  K: key 8i + tid/32 (i = 0..7), chunk tid%32 (16 bytes of 32 dims; fp8 half rows)
+//  V: keys key_at_pos(8pc + j) (pc = tid/32, j = 0..7), dims 8c..8c+7 (c = tid%32)
 template <bool FP8>
 struct TileRegs {
-  // K: bf16 -> 4 x 16B chunks; fp8 -> 2 x 16B chunks (16 e4m3 each).
-  u32x4 k[FP8 ? 2 : 4];
-  // V: 4 keys x 8 dims: bf16 16B per key; fp8 8B per key (stored in .xy).
-  u32x4 v[4];
+  u32x4 k[8];
+  u32x4 v[8];   // fp8: 8 bytes per key in .xy
 };
 
 template <bool FP8>
-__device__ __forceinline__ void load_tile(const ExtendArgs& a, const int64_t* rtt, int L, int hk,
-                                          int k0, int tid, TileRegs<FP8>& r) {
+__device__ __forceinline__ void issue_tile(const ExtendArgs& a, const int32_t* slots, int key0,
+                                           int kend, int hk, int tid, TileRegs<FP8>& r) {
   constexpr int kRowBytes = FP8 ? kD : 2 * kD;
   const int64_t slot_bytes = (int64_t)a.hkv * kRowBytes;
   const uint8_t* kb = a.k_pool + (int64_t)hk * kRowBytes;
   const uint8_t* vb = a.v_pool + (int64_t)hk * kRowBytes;
-  const int last = L - 1;
-#pragma unroll
-  for (int it = 0; it < (FP8 ? 2 : 4); ++it) {
-    const int key = FP8 ? (it * 16 + (tid >> 4)) : (it * 8 + (tid >> 5));
-    const int c = FP8 ? (tid & 15) : (tid & 31);
-    const int64_t slot = clamp_i64(rtt[min(k0 + key, last)], 0, a.pool_slots - 1);
-    r.k[it] = ld_g16(kb + slot * slot_bytes + 16 * c);
-  }
-  const int kg = tid >> 5;
   const int c = tid & 31;
+  const int grp = tid >> 5;
+  // Keys past the needed range read the last needed key (valid rows; masked).
+  // Key k's slot id sits at slots[k % 2048] (two 1024-key halves).
+  const int last = kend - 1;
 #pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    const int64_t slot = clamp_i64(rtt[min(k0 + 4 * kg + e, last)], 0, a.pool_slots - 1);
-    const uint8_t* vp = vb + slot * slot_bytes;
+  for (int i = 0; i < 8; ++i) {
+    const int key = min(key0 + 8 * i + grp, last);
+    const int64_t s = slots[key & (2 * kSlotChunk - 1)];
     if (FP8) {
-      const u32x2 x = ld_g8(vp + 8 * c);
-      r.v[e] = u32x4{x[0], x[1], 0u, 0u};
+      // fp8 rows are 256 B: chunk c covers dims 16(c/2) .. in two halves of 8 B.
+      const u32x2 x = ld_g8(kb + s * slot_bytes + 8 * c);
+      r.k[i] = u32x4{x[0], x[1], 0u, 0u};
     } else {
-      r.v[e] = ld_g16(vp + 16 * c);
+      r.k[i] = ld_g16(kb + s * slot_bytes + 16 * c);
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const int key = min(key0 + key_at_pos(8 * grp + j), last);
+    const int64_t s = slots[key & (2 * kSlotChunk - 1)];
+    if (FP8) {
+      const u32x2 x = ld_g8(vb + s * slot_bytes + 8 * c);
+      r.v[j] = u32x4{x[0], x[1], 0u, 0u};
+    } else {
+      r.v[j] = ld_g16(vb + s * slot_bytes + 16 * c);
     }
   }
 }
 
 template <bool FP8>
-__device__ __forceinline__ void store_tile(char* kt, char* vt, int tid, const TileRegs<FP8>& r) {
-#pragma unroll
-  for (int it = 0; it < (FP8 ? 2 : 4); ++it) {
-    if (FP8) {
-      const int key = it * 16 + (tid >> 4);
-      const int c = tid & 15;
-      char* p = kt + key * kKStride + 32 * c;
-      st_s16(p, e4m3x8_to_bf16x8(r.k[it][0], r.k[it][1]));
-      st_s16(p + 16, e4m3x8_to_bf16x8(r.k[it][2], r.k[it][3]));
-    } else {
-      const int key = it * 8 + (tid >> 5);
-      const int c = tid & 31;
-      st_s16(kt + key * kKStride + 16 * c, r.k[it]);
-    }
-  }
-  const int kg = tid >> 5;
+__device__ __forceinline__ void store_tile(u32x4* ks, u32x4* vts, int tid,
+                                           const TileRegs<FP8>& r) {
   const int c = tid & 31;
-  u32x4 v[4];
+  const int grp = tid >> 5;
 #pragma unroll
-  for (int e = 0; e < 4; ++e) v[e] = FP8 ? e4m3x8_to_bf16x8(r.v[e][0], r.v[e][1]) : r.v[e];
-  char* base = vt + 8 * vt_pos_block(kg);
+  for (int i = 0; i < 8; ++i) {
+    const int key = 8 * i + grp;
+    u32x4 v = r.k[i];
+    if (FP8) {
+      // 8 fp8 = dims 8c..8c+7 -> one bf16 chunk (chunk index c).
+      v = e4m3x8_to_bf16x8(r.k[i][0], r.k[i][1]);
+    }
+    ks[key * kKChunks + (c ^ (key & 31))] = v;
+  }
+  // V: 8 keys (position chunk grp) x 8 dims (8c .. 8c+7) -> 8 V^T rows.
+  u32x4 in[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) in[j] = FP8 ? e4m3x8_to_bf16x8(r.v[j][0], r.v[j][1]) : r.v[j];
 #pragma unroll
   for (int d = 0; d < 8; ++d) {
-    const int dw = d >> 1;
-    const int hi = d & 1;
-    const u32x2 x = {pair_sel(v[1][dw], v[0][dw], hi), pair_sel(v[3][dw], v[2][dw], hi)};
-    st_s8(base + (8 * c + d) * kVStride, x);
+    const int dw = d >> 1, hi = d & 1;
+    u32x4 o;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) o[w] = pair_sel(in[2 * w + 1][dw], in[2 * w][dw], hi);
+    const int row = 8 * c + d;
+    vts[row * kVChunks + (grp ^ vt_swz(row))] = o;
+  }
+}
+
+// Refills slot buffer (chunk & 1) with the slot ids of keys
+// [chunk*1024, chunk*1024 + 1024) clamped to the needed range.
+__device__ __forceinline__ void stage_slots(const ExtendArgs& a, const int64_t* rtt, int chunk,
+                                            int kend, int tid, int32_t* buf) {
+  const int k0 = chunk * kSlotChunk;
+  for (int i = tid; i < kSlotChunk; i += kThreads) {
+    const int key = min(k0 + i, kend - 1);
+    buf[i] = (int32_t)clamp_i64(rtt[key], 0, a.pool_slots - 1);
   }
 }
 
 template <bool FP8>
-__global__ void __launch_bounds__(kWaves * kWave)
+__global__ void __launch_bounds__(kThreads)
 extend_kernel(ExtendArgs a) {
-  __shared__ __attribute__((aligned(16))) char smem[kKTile + kVTile];
-  char* kt = smem;
-  char* vt = smem + kKTile;
+  __shared__ __attribute__((aligned(16))) ExtendSmem sm;
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -176,7 +203,8 @@ extend_kernel(ExtendArgs a) {
 
   // Block / wave key extents.
   const int blk_last_row = min(row0 + kWaves * kRowsPerWave, rows_total) - 1;
-  const int kend = P + blk_last_row / G + 1;  // keys [0, kend) are needed
+  const int kend = min(L, P + blk_last_row / G + 1);   // keys [0, kend) are needed
+  if (kend <= 0) return;
   const int n_tiles = (kend + kBN - 1) / kBN;
   const int w_first = row0 + kRowsPerWave * w;
   const int w_last = min(w_first + kRowsPerWave, rows_total) - 1;
@@ -188,13 +216,13 @@ extend_kernel(ExtendArgs a) {
   const float vscale = FP8 ? a.v_scale[0] : 1.f;
   const float sl2 = a.scale_log2 * kscale;
 
-  // Q^T fragments: lane (g, n) holds q[row n][16 kk + 8 g .. +8].
+  // Q^T fragments: lane (g, n) holds q[row n][16 kk + 8 g .. +8].  Padding
+  // lanes (row_ok false) load a valid row and never write their result.
   u32x4 qf[16];
   {
     const __bf16* qp = a.q + (int64_t)(q_start + t) * a.q_stride + (int64_t)(hk * G + h) * kD;
 #pragma unroll
-    for (int kk = 0; kk < 16; ++kk)
-      qf[kk] = row_ok ? ld_g16(qp + 16 * kk + 8 * g) : u32x4{0u, 0u, 0u, 0u};
+    for (int kk = 0; kk < 16; ++kk) qf[kk] = ld_g16(qp + 16 * kk + 8 * g);
   }
 
   float m = -INFINITY;
@@ -203,67 +231,96 @@ extend_kernel(ExtendArgs a) {
 #pragma unroll
   for (int i = 0; i < 8; ++i) acc[i] = f32x16{};
 
+  // ---- prologue: slots of chunk 0, tile 0 into stage 0
+  stage_slots(a, rtt, 0, kend, tid, sm.slots[0]);
+  __syncthreads();
   TileRegs<FP8> regs;
-  load_tile<FP8>(a, rtt, L, hk, 0, tid, regs);
+  issue_tile<FP8>(a, &sm.slots[0][0], 0, kend, hk, tid, regs);
+  store_tile<FP8>(sm.k[0], sm.vt[0], tid, regs);
+  __syncthreads();
 
   for (int tile = 0; tile < n_tiles; ++tile) {
     const int k0 = tile * kBN;
-    __syncthreads();  // previous tile's LDS reads are done
-    store_tile<FP8>(kt, vt, tid, regs);
+    const int st = tile & 1;
+    const bool has_next = tile + 1 < n_tiles;
+    // Refill the other slot buffer half-way through a slot chunk (visible to
+    // every thread after this tile's barrier, long before it is needed).
+    if ((tile % kTilesPerSlotChunk) == kTilesPerSlotChunk / 2 &&
+        (tile / kTilesPerSlotChunk + 1) * kSlotChunk < kend) {
+      const int nc = tile / kTilesPerSlotChunk + 1;
+      stage_slots(a, rtt, nc, kend, tid, sm.slots[nc & 1]);
+    }
+    if (has_next) issue_tile<FP8>(a, &sm.slots[0][0], k0 + kBN, kend, hk, tid, regs);
+    __builtin_amdgcn_sched_barrier(0);
+
+    if (wave_active && k0 < w_kend) {
+      const u32x4* ks = sm.k[st];
+      const u32x4* vts = sm.vt[st];
+      // ---- S^T = K Q^T: two 32-key halves; lane holds keys 8(r/4) + 4g + r%4
+      f32x16 s[2];
+#pragma unroll
+      for (int hh = 0; hh < 2; ++hh) {
+        s[hh] = f32x16{};
+        const int key = 32 * hh + n;
+#pragma unroll
+        for (int kk = 0; kk < 16; ++kk)
+          s[hh] = mfma_32x32x16(ks[key * kKChunks + ((2 * kk + g) ^ (key & 31))], qf[kk], s[hh]);
+      }
+      const bool need_mask = (k0 + kBN) > w_full;
+      float mx = -INFINITY;
+#pragma unroll
+      for (int hh = 0; hh < 2; ++hh) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          float v = s[hh][r] * sl2;
+          if (need_mask) {
+            const int key = k0 + 32 * hh + 8 * (r >> 2) + 4 * g + (r & 3);
+            if (key > limit) v = -INFINITY;
+          }
+          s[hh][r] = v;
+          mx = fmaxf(mx, v);
+        }
+      }
+      mx = wave_max_xor(mx, 32);
+      const float mnew = fmaxf(m, mx);
+      const float alpha = fast_exp2(m - mnew);
+      float psum = 0.f;
+#pragma unroll
+      for (int hh = 0; hh < 2; ++hh) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          s[hh][r] = fast_exp2(s[hh][r] - mnew);
+          psum += s[hh][r];
+        }
+      }
+      l = l * alpha + psum;
+      m = mnew;
+      if (__ballot(alpha != 1.f)) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) acc[i] *= alpha;
+      }
+
+      // ---- O^T += V^T P^T over four 16-key steps
+      u32x4 pt[4];
+#pragma unroll
+      for (int q4 = 0; q4 < 4; ++q4) {
+        const int hh = q4 >> 1, o = 8 * (q4 & 1);
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+          pt[q4][k] = pack_bf16(s[hh][o + 2 * k], s[hh][o + 2 * k + 1]);
+      }
+#pragma unroll
+      for (int mt = 0; mt < 8; ++mt) {
+        const int row = 32 * mt + n;
+#pragma unroll
+        for (int q4 = 0; q4 < 4; ++q4)
+          acc[mt] = mfma_32x32x16(vts[row * kVChunks + ((2 * q4 + g) ^ vt_swz(row))], pt[q4],
+                                  acc[mt]);
+      }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    if (has_next) store_tile<FP8>(sm.k[st ^ 1], sm.vt[st ^ 1], tid, regs);
     __syncthreads();
-    if (tile + 1 < n_tiles) load_tile<FP8>(a, rtt, L, hk, k0 + kBN, tid, regs);
-
-    if (!wave_active || k0 >= w_kend) continue;
-
-    // ---- S^T = K Q^T : lane holds keys 8(r/4) + 4g + r%4 of row n
-    f32x16 s = {};
-#pragma unroll
-    for (int kk = 0; kk < 16; ++kk) {
-      const u32x4 kf = ld_s16(kt + n * kKStride + 32 * kk + 16 * g);
-      s = mfma_32x32x16(kf, qf[kk], s);
-    }
-    const bool need_mask = (k0 + kBN) > w_full;
-    float mx = -INFINITY;
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      float v = s[r] * sl2;
-      if (need_mask) {
-        const int key = k0 + 8 * (r >> 2) + 4 * g + (r & 3);
-        if (key > limit) v = -INFINITY;
-      }
-      s[r] = v;
-      mx = fmaxf(mx, v);
-    }
-    mx = wave_max_xor(mx, 32);
-    const float mnew = fmaxf(m, mx);
-    const float alpha = fast_exp2(m - mnew);
-    float psum = 0.f;
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      s[r] = fast_exp2(s[r] - mnew);
-      psum += s[r];
-    }
-    l = l * alpha + psum;
-    m = mnew;
-    if (__ballot(alpha != 1.f)) {
-#pragma unroll
-      for (int i = 0; i < 8; ++i) acc[i] *= alpha;
-    }
-
-    // ---- O^T += V^T P^T
-    u32x4 pt[2];
-#pragma unroll
-    for (int st = 0; st < 2; ++st)
-#pragma unroll
-      for (int k = 0; k < 4; ++k) pt[st][k] = pack_bf16(s[8 * st + 2 * k], s[8 * st + 2 * k + 1]);
-#pragma unroll
-    for (int mt = 0; mt < 8; ++mt) {
-#pragma unroll
-      for (int st = 0; st < 2; ++st) {
-        const u32x4 vf = ld_s16(vt + (32 * mt + n) * kVStride + 32 * st + 16 * g);
-        acc[mt] = mfma_32x32x16(vf, pt[st], acc[mt]);
-      }
-    }
   }
 
   if (!row_ok) return;
@@ -344,8 +401,8 @@ extern "C" int32_t tf_attn_extend(const void* q, int64_t q_row_stride, const voi
 
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   if (kv_dtype == TF_DTYPE_FP8_E4M3)
-    hipLaunchKernelGGL(extend_kernel<true>, dim3((unsigned)n_work), dim3(kWaves * kWave), 0, s, a);
+    hipLaunchKernelGGL(extend_kernel<true>, dim3((unsigned)n_work), dim3(kThreads), 0, s, a);
   else
-    hipLaunchKernelGGL(extend_kernel<false>, dim3((unsigned)n_work), dim3(kWaves * kWave), 0, s, a);
+    hipLaunchKernelGGL(extend_kernel<false>, dim3((unsigned)n_work), dim3(kThreads), 0, s, a);
   return launch_status("tf_attn_extend launch");
 }

@@ -20,7 +20,7 @@ inline bool aligned8(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 7
 
 // Decode plan shared by the launcher and the workspace-size query.
 struct DecodePlan {
-  int32_t n_blocks;     // workgroups of the streaming kernel (2 per CU by default)
+  int32_t n_blocks;     // workgroups of the streaming kernel (1 per CU by default)
   int32_t n_hgroups;    // ceil(group / 16)
   int32_t gmax;         // min(group, 16)
   int64_t n_units;      // items * kv_heads * n_hgroups
