@@ -12,19 +12,30 @@
 // (32 per wave), so all G heads of a GQA group share every K/V tile.
 // Row (t, h) attends to context positions 0 .. P + t, P = L - ext.
 //
-// Per 64-key tile (LDS double-buffered, one barrier per tile):
-//   * the next tile's K and V rows are gathered with coalesced 16-byte loads
-//     (slot ids come from an LDS slot buffer refilled 1024 keys at a time)
-//     before the current tile's MFMAs are issued;
-//   * K lands in LDS row-major with chunk c of key k at k*32 + (c ^ (k & 31));
-//     V is transposed in registers (8 keys x 8 dims per thread) and lands as
-//     V^T rows of 64 keys in the order the PV operand wants, chunk-swizzled;
-//   * each wave computes, with v_mfma_f32_32x32x16_bf16,
-//       S^T[key, row] = K * Q^T   (Q^T register-resident, K from LDS),
-//       the online softmax per row (a row's 64 keys live in lanes n and n + 32),
-//       O^T[dim, row] += V^T * P^T (V^T from LDS, P^T straight from S^T),
-//     so each lane owns one row: its max, sum and 128 of its output dims.
+// Each wave computes, per 64-key tile j, with v_mfma_f32_32x32x16_bf16:
+//   S^T[key, row] = K Q^T        (Q^T register-resident, K from LDS)
+//   online softmax of S^T        (a row's 64 scores live in lanes n and n + 32)
+//   O^T[dim, row] += V^T P^T     (V^T from LDS, P^T packed straight from S^T)
+// so each lane owns one row: its max, sum and 128 of its output dims.
+//
+// Software pipeline (one barrier per tile, no wave-dependent branches around
+// the accumulator so it stays in AGPRs):
+//   * the QK^T MFMAs of tile j + 1 are issued next to the softmax of tile j,
+//     and the exps of tile j next to its PV MFMAs, so VALU work hides under
+//     matrix-core time;
+//   * tile j + 2 is gathered from HBM into registers while tile j is computed
+//     (slot ids come from an LDS slot buffer refilled 1024 keys at a time, so
+//     no load waits on a dependent slot lookup in global memory);
+//   * K lands in LDS row-major with a 16-byte pad per key row, V is transposed
+//     in registers and lands as V^T rows of 64 keys, chunk-swizzled; both are
+//     double-buffered (K(j+2) overwrites K(j) during PV(j); V(j+2) is written
+//     at the start of the next tile, after every wave has finished PV(j)).
+//   * The running max is raised lazily: the accumulator is rescaled only when
+//     some row's max grows by more than 2^8, otherwise the old max stays the
+//     reference point (exact in exact arithmetic; p <= 2^8 fits bf16's range).
 #include <math.h>
+
+#include <type_traits>
 
 #include "tf_common.h"
 #include "tf_internal.h"
@@ -36,11 +47,15 @@ constexpr int kD = 256;
 constexpr int kWaves = 4;
 constexpr int kThreads = kWaves * kWave;
 constexpr int kRowsPerWave = 32;
-constexpr int kBN = 64;                     // keys per tile
-constexpr int kKChunks = 32;                // 16-byte chunks per K row (512 B)
-constexpr int kVChunks = kBN / 8;           // 16-byte chunks per V^T row (64 keys)
-constexpr int kSlotChunk = 1024;            // keys per slot-buffer refill
+constexpr int kBN = 64;                         // keys per tile
+constexpr int kKStride = 2 * kD + 16;           // bytes per K row in LDS (padded)
+constexpr int kKStage = kBN * kKStride;         // 33792
+constexpr int kVtStride = 2 * kBN;              // bytes per V^T row (64 keys)
+constexpr int kVtStage = kD * kVtStride;        // 32768
+constexpr int kSlotChunk = 1024;                // keys per slot-buffer refill
+constexpr int kSlotMask = 2 * kSlotChunk - 1;
 constexpr int kTilesPerSlotChunk = kSlotChunk / kBN;
+constexpr float kRescaleLog2 = 8.f;             // lazy-rescale threshold (log2 units)
 
 struct ExtendArgs {
   const __bf16* q;
@@ -62,113 +77,181 @@ struct ExtendArgs {
   int64_t out_stride;
 };
 
-struct ExtendSmem {
-  u32x4 k[2][kBN * kKChunks];      // 2 x 32 KB
-  u32x4 vt[2][kD * kVChunks];      // 2 x 32 KB
-  int32_t slots[2][kSlotChunk];    // 2 x 4 KB
+struct __attribute__((aligned(16))) ExtendSmem {
+  uint8_t k[2 * kKStage];          // 66 KB
+  uint8_t vt[2 * kVtStage];        // 64 KB
+  int32_t slots[2 * kSlotChunk];   // 8 KB: key k's slot id at slots[k % 2048]
 };
 
-// Key (0..63 within the tile) stored at V^T position p: within each 16-key
-// group st, position 8g + j holds key 16st + 8(j/4) + 4g + (j%4), the order of
-// the P^T operand taken from the S^T accumulator layout.
-__device__ __forceinline__ int key_at_pos(int p) {
-  const int st = p >> 4, g = (p >> 3) & 1, j = p & 7;
-  return 16 * st + 8 * (j >> 2) + 4 * g + (j & 3);
-}
-
-__device__ __forceinline__ int vt_swz(int row) { return (row ^ (row >> 3)) & 7; }
-
-// Registers holding one tile's gathered rows for this thread.
-//  K: key 8i + tid/32 (i = 0..7), chunk tid%32 (16 bytes of 32 dims; fp8 half rows)
-//  V: keys key_at_pos(8pc + j) (pc = tid/32, j = 0..7), dims 8c..8c+7 (c = tid%32)
+// One tile's gathered rows for this thread: the 8 keys run0 + {0..3, 8..11}
+// (run0 = 16 (grp / 2) + 4 (grp % 2), grp = tid / 32), 16 bytes each (chunk
+// tid % 32 of the head row: dims 8c .. 8c + 7; fp8 rows keep 8 bytes in .xy).
+// Those 8 keys are exactly V^T positions 8 grp .. 8 grp + 7 (see pv_tile).
 template <bool FP8>
 struct TileRegs {
   u32x4 k[8];
-  u32x4 v[8];   // fp8: 8 bytes per key in .xy
+  u32x4 v[8];
 };
 
+__device__ __forceinline__ int run_key(int j) { return 8 * (j >> 2) + (j & 3); }
+
 template <bool FP8>
-__device__ __forceinline__ void issue_tile(const ExtendArgs& a, const int32_t* slots, int key0,
-                                           int kend, int hk, int tid, TileRegs<FP8>& r) {
-  constexpr int kRowBytes = FP8 ? kD : 2 * kD;
-  const int64_t slot_bytes = (int64_t)a.hkv * kRowBytes;
-  const uint8_t* kb = a.k_pool + (int64_t)hk * kRowBytes;
-  const uint8_t* vb = a.v_pool + (int64_t)hk * kRowBytes;
-  const int c = tid & 31;
-  const int grp = tid >> 5;
-  // Keys past the needed range read the last needed key (valid rows; masked).
-  // Key k's slot id sits at slots[k % 2048] (two 1024-key halves).
-  const int last = kend - 1;
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const int key = min(key0 + 8 * i + grp, last);
-    const int64_t s = slots[key & (2 * kSlotChunk - 1)];
-    if (FP8) {
-      // fp8 rows are 256 B: chunk c covers dims 16(c/2) .. in two halves of 8 B.
-      const u32x2 x = ld_g8(kb + s * slot_bytes + 8 * c);
-      r.k[i] = u32x4{x[0], x[1], 0u, 0u};
-    } else {
-      r.k[i] = ld_g16(kb + s * slot_bytes + 16 * c);
-    }
-  }
+__device__ __forceinline__ void gather_tile(const int32_t* slots, const uint8_t* kb,
+                                            const uint8_t* vb, int64_t slot_bytes, int key0,
+                                            int run0, TileRegs<FP8>& r) {
+  const u32x4 s0 = *reinterpret_cast<const u32x4*>(slots + ((key0 + run0) & kSlotMask));
+  const u32x4 s1 = *reinterpret_cast<const u32x4*>(slots + ((key0 + run0 + 8) & kSlotMask));
 #pragma unroll
   for (int j = 0; j < 8; ++j) {
-    const int key = min(key0 + key_at_pos(8 * grp + j), last);
-    const int64_t s = slots[key & (2 * kSlotChunk - 1)];
+    const uint32_t slot = j < 4 ? s0[j] : s1[j - 4];
+    const int64_t off = (int64_t)slot * slot_bytes;
     if (FP8) {
-      const u32x2 x = ld_g8(vb + s * slot_bytes + 8 * c);
-      r.v[j] = u32x4{x[0], x[1], 0u, 0u};
+      const u32x2 x = ld_g8(kb + off);
+      const u32x2 y = ld_g8(vb + off);
+      r.k[j] = u32x4{x[0], x[1], 0u, 0u};
+      r.v[j] = u32x4{y[0], y[1], 0u, 0u};
     } else {
-      r.v[j] = ld_g16(vb + s * slot_bytes + 16 * c);
+      r.k[j] = ld_g16(kb + off);
+      r.v[j] = ld_g16(vb + off);
     }
   }
 }
 
 template <bool FP8>
-__device__ __forceinline__ void store_tile(u32x4* ks, u32x4* vts, int tid,
-                                           const TileRegs<FP8>& r) {
-  const int c = tid & 31;
-  const int grp = tid >> 5;
+__device__ __forceinline__ void store_k(uint8_t* kst, int run0, int c, const TileRegs<FP8>& r) {
+  uint8_t* p = kst + run0 * kKStride + 16 * c;
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const int key = 8 * i + grp;
-    u32x4 v = r.k[i];
-    if (FP8) {
-      // 8 fp8 = dims 8c..8c+7 -> one bf16 chunk (chunk index c).
-      v = e4m3x8_to_bf16x8(r.k[i][0], r.k[i][1]);
-    }
-    ks[key * kKChunks + (c ^ (key & 31))] = v;
-  }
-  // V: 8 keys (position chunk grp) x 8 dims (8c .. 8c+7) -> 8 V^T rows.
+  for (int j = 0; j < 8; ++j)
+    st_s16(p + run_key(j) * kKStride, FP8 ? e4m3x8_to_bf16x8(r.k[j][0], r.k[j][1]) : r.k[j]);
+}
+
+// V^T row `dim` holds the tile's 64 keys in 8 chunks of 8 positions; chunk pc
+// is stored at chunk pc ^ swz(dim), swz(dim) = (dim ^ (dim >> 3)) & 7, which
+// keeps both these writes and the PV reads free of bank conflicts.
+template <bool FP8>
+__device__ __forceinline__ void store_vt(uint8_t* vst, int grp, int c, const TileRegs<FP8>& r) {
   u32x4 in[8];
 #pragma unroll
   for (int j = 0; j < 8; ++j) in[j] = FP8 ? e4m3x8_to_bf16x8(r.v[j][0], r.v[j][1]) : r.v[j];
+  const int y = (grp ^ c) & 7;
+  uint8_t* p = vst + 8 * c * kVtStride;
 #pragma unroll
   for (int d = 0; d < 8; ++d) {
-    const int dw = d >> 1, hi = d & 1;
     u32x4 o;
 #pragma unroll
-    for (int w = 0; w < 4; ++w) o[w] = pair_sel(in[2 * w + 1][dw], in[2 * w][dw], hi);
-    const int row = 8 * c + d;
-    vts[row * kVChunks + (grp ^ vt_swz(row))] = o;
+    for (int w = 0; w < 4; ++w) o[w] = pair_sel(in[2 * w + 1][d >> 1], in[2 * w][d >> 1], d & 1);
+    st_s16(p + d * kVtStride + 16 * (y ^ d), o);
   }
 }
 
-// Refills slot buffer (chunk & 1) with the slot ids of keys
-// [chunk*1024, chunk*1024 + 1024) clamped to the needed range.
+// Refills slot-buffer half (chunk & 1) with the slot ids of keys
+// [chunk * 1024, chunk * 1024 + 1024), clamped to the needed range [0, kend).
 __device__ __forceinline__ void stage_slots(const ExtendArgs& a, const int64_t* rtt, int chunk,
-                                            int kend, int tid, int32_t* buf) {
+                                            int kend, int tid, int32_t* slots) {
   const int k0 = chunk * kSlotChunk;
+  int32_t* buf = slots + (chunk & 1) * kSlotChunk;
   for (int i = tid; i < kSlotChunk; i += kThreads) {
     const int key = min(k0 + i, kend - 1);
     buf[i] = (int32_t)clamp_i64(rtt[key], 0, a.pool_slots - 1);
   }
 }
 
+// S^T (64 keys x 32 rows) = K_tile Q^T: s[hh][r] is key 32 hh + 8 (r / 4) + 4 g + r % 4.
+__device__ __forceinline__ void qk_tile(const uint8_t* kst, int kread, const u32x4 (&qf)[16],
+                                        f32x16 (&s)[2]) {
+  s[0] = f32x16{};
+  s[1] = f32x16{};
+#pragma unroll
+  for (int kk = 0; kk < 16; ++kk) {
+#pragma unroll
+    for (int hh = 0; hh < 2; ++hh)
+      s[hh] = mfma_32x32x16(ld_s16(kst + kread + hh * 32 * kKStride + 32 * kk), qf[kk], s[hh]);
+  }
+}
+
+// Online softmax of one tile's scores (raw, unscaled) for this lane's row;
+// leaves P^T packed as the B operands of the four 16-key PV steps.  Returns
+// true (wave-uniform) when the accumulator must be multiplied by alpha.
+// Sets the scores of keys past this lane's last visible key to -inf.
+__device__ __forceinline__ void mask_tile(f32x16 (&s)[2], int k0, int g, int limit) {
+#pragma unroll
+  for (int hh = 0; hh < 2; ++hh)
+#pragma unroll
+    for (int r = 0; r < 16; ++r)
+      if (k0 + 32 * hh + 8 * (r >> 2) + 4 * g + (r & 3) > limit) s[hh][r] = -INFINITY;
+}
+
+// Online softmax of one tile's scores (raw, unscaled) for this lane's row;
+// leaves P^T packed as the B operands of the four 16-key PV steps.  Returns
+// true (wave-uniform) when the accumulator must be multiplied by alpha.
+__device__ __forceinline__ bool softmax_tile(f32x16 (&s)[2], float& m, float& l, float sl2,
+                                             u32x4 (&pt)[4], float& alpha) {
+  float mx = s[0][0];
+#pragma unroll
+  for (int r = 1; r < 16; ++r) mx = fmaxf(mx, s[0][r]);
+#pragma unroll
+  for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[1][r]);
+  mx = wave_max_xor(mx, 32);
+  // Raise the reference max only when some row of the wave outgrew it by 2^8.
+  const bool grow = (mx - m) * sl2 > kRescaleLog2;
+  const bool any = __ballot(grow) != 0;
+  const float mnew = any ? fmaxf(m, mx) : m;
+  alpha = any ? fast_exp2((m - mnew) * sl2) : 1.f;
+  const float moff = mnew == -INFINITY ? 0.f : mnew * sl2;
+  float psum = 0.f;
+#pragma unroll
+  for (int hh = 0; hh < 2; ++hh)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const float p = fast_exp2(fmaf(s[hh][r], sl2, -moff));
+      s[hh][r] = p;
+      psum += p;
+    }
+  l = l * alpha + psum;
+  m = mnew;
+#pragma unroll
+  for (int q4 = 0; q4 < 4; ++q4) {
+    const int hh = q4 >> 1, o = 8 * (q4 & 1);
+#pragma unroll
+    for (int k = 0; k < 4; ++k) pt[q4][k] = pack_bf16(s[hh][o + 2 * k], s[hh][o + 2 * k + 1]);
+  }
+  return any;
+}
+
+// O^T += V^T P^T.  A operand of step q4 for output dims 32 mt + n: V^T row
+// 32 mt + n, positions 16 q4 + 8 g .. +8, i.e. keys 16 q4 + 8 (j / 4) + 4 g + j % 4
+// (the order in which P^T leaves the S^T accumulator).
+__device__ __forceinline__ void pv_tile(const uint8_t* vst, const int (&vb)[4][2],
+                                        const u32x4 (&pt)[4], f32x16 (&acc)[8]) {
+#pragma unroll
+  for (int q4 = 0; q4 < 4; ++q4)
+#pragma unroll
+    for (int mt = 0; mt < 8; ++mt)
+      acc[mt] = mfma_32x32x16(ld_s16(vst + vb[q4][mt & 1] + 32 * kVtStride * mt), pt[q4],
+                              acc[mt]);
+}
+
+// Multiplies an accumulator tile held in AGPRs by a per-lane factor one
+// register at a time, so the tile never has to live in VGPRs.
+__device__ __forceinline__ void scale_acc(f32x16& x, float f) {
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    float e = x[i];
+    float tmp;
+    asm volatile(
+        "v_accvgpr_read_b32 %1, %0\n\t"
+        "v_mul_f32 %1, %1, %2\n\t"
+        "v_accvgpr_write_b32 %0, %1"
+        : "+a"(e), "=&v"(tmp)
+        : "v"(f));
+    x[i] = e;
+  }
+}
+
 template <bool FP8>
 __global__ void __launch_bounds__(kThreads)
 extend_kernel(ExtendArgs a) {
-  __shared__ __attribute__((aligned(16))) ExtendSmem sm;
+  __shared__ ExtendSmem sm;
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -194,30 +277,50 @@ extend_kernel(ExtendArgs a) {
   const int64_t rrow = clamp_i64(a.rpi[b], 0, a.rtt_rows - 1);
   const int64_t* rtt = a.rtt + rrow * a.rtt_stride;
 
-  // This lane's row.
+  // This lane's row; padding lanes (row_ok false) compute a valid duplicate row
+  // and never write it.
   const int rho = row0 + kRowsPerWave * w + n;
   const bool row_ok = rho < rows_total;
   const int t = row_ok ? rho / G : ext - 1;
   const int h = row_ok ? rho - t * G : 0;
   const int limit = P + t;  // last visible key
 
-  // Block / wave key extents.
+  // Keys [0, kend) are needed by the block; keys below w_full are visible to
+  // every row of this wave.
   const int blk_last_row = min(row0 + kWaves * kRowsPerWave, rows_total) - 1;
-  const int kend = min(L, P + blk_last_row / G + 1);   // keys [0, kend) are needed
+  const int kend = min(L, P + blk_last_row / G + 1);
   if (kend <= 0) return;
   const int n_tiles = (kend + kBN - 1) / kBN;
+  // Every wave runs all n_tiles tiles (keys past a row's limit are masked, and
+  // key 0 is visible to every row, so each row's max is finite after tile 0).
   const int w_first = row0 + kRowsPerWave * w;
-  const int w_last = min(w_first + kRowsPerWave, rows_total) - 1;
-  const bool wave_active = w_first < rows_total;
-  const int w_kend = wave_active ? P + w_last / G + 1 : 0;
-  const int w_full = wave_active ? P + w_first / G + 1 : 0;  // keys < w_full: no mask
+  const int w_full = w_first < rows_total ? P + w_first / G + 1 : 0;
 
   const float kscale = FP8 ? a.k_scale[0] : 1.f;
   const float vscale = FP8 ? a.v_scale[0] : 1.f;
   const float sl2 = a.scale_log2 * kscale;
 
-  // Q^T fragments: lane (g, n) holds q[row n][16 kk + 8 g .. +8].  Padding
-  // lanes (row_ok false) load a valid row and never write their result.
+  // Gather mapping.
+  const int grp = tid >> 5;
+  const int c = tid & 31;
+  const int run0 = 16 * (grp >> 1) + 4 * (grp & 1);
+  constexpr int kRowBytes = FP8 ? kD : 2 * kD;
+  const int64_t slot_bytes = (int64_t)a.hkv * kRowBytes;
+  const uint8_t* kb = a.k_pool + (int64_t)hk * kRowBytes + (FP8 ? 8 : 16) * c;
+  const uint8_t* vb = a.v_pool + (int64_t)hk * kRowBytes + (FP8 ? 8 : 16) * c;
+
+  // LDS read offsets of this lane.
+  const int kread = n * kKStride + 16 * g;
+  int vbo[4][2];
+  {
+    const int z = (n ^ (n >> 3)) & 7;
+#pragma unroll
+    for (int q4 = 0; q4 < 4; ++q4)
+#pragma unroll
+      for (int p = 0; p < 2; ++p) vbo[q4][p] = n * kVtStride + 16 * (((2 * q4 + g) ^ z ^ (4 * p)) & 7);
+  }
+
+  // Q^T fragments: lane (g, n) holds q[row n][16 kk + 8 g .. +8].
   u32x4 qf[16];
   {
     const __bf16* qp = a.q + (int64_t)(q_start + t) * a.q_stride + (int64_t)(hk * G + h) * kD;
@@ -231,95 +334,60 @@ extend_kernel(ExtendArgs a) {
 #pragma unroll
   for (int i = 0; i < 8; ++i) acc[i] = f32x16{};
 
-  // ---- prologue: slots of chunk 0, tile 0 into stage 0
-  stage_slots(a, rtt, 0, kend, tid, sm.slots[0]);
+  uint8_t* const kst0 = sm.k;
+  uint8_t* const kst1 = sm.k + kKStage;
+  uint8_t* const vst0 = sm.vt;
+  uint8_t* const vst1 = sm.vt + kVtStage;
+
+  // ---- prologue: K(0), V(0), K(1) in LDS; V(1) in registers; S(0) computed.
+  // With a single tile the unused K(1) / V(1) stages are simply never read.
+  stage_slots(a, rtt, 0, kend, tid, sm.slots);
   __syncthreads();
   TileRegs<FP8> regs;
-  issue_tile<FP8>(a, &sm.slots[0][0], 0, kend, hk, tid, regs);
-  store_tile<FP8>(sm.k[0], sm.vt[0], tid, regs);
+  gather_tile<FP8>(sm.slots, kb, vb, slot_bytes, 0, run0, regs);
+  store_k<FP8>(kst0, run0, c, regs);
+  store_vt<FP8>(vst0, grp, c, regs);
+  if (n_tiles > 1) {
+    gather_tile<FP8>(sm.slots, kb, vb, slot_bytes, kBN, run0, regs);
+    store_k<FP8>(kst1, run0, c, regs);
+  }
   __syncthreads();
 
-  for (int tile = 0; tile < n_tiles; ++tile) {
-    const int k0 = tile * kBN;
-    const int st = tile & 1;
-    const bool has_next = tile + 1 < n_tiles;
-    // Refill the other slot buffer half-way through a slot chunk (visible to
-    // every thread after this tile's barrier, long before it is needed).
-    if ((tile % kTilesPerSlotChunk) == kTilesPerSlotChunk / 2 &&
-        (tile / kTilesPerSlotChunk + 1) * kSlotChunk < kend) {
-      const int nc = tile / kTilesPerSlotChunk + 1;
-      stage_slots(a, rtt, nc, kend, tid, sm.slots[nc & 1]);
-    }
-    if (has_next) issue_tile<FP8>(a, &sm.slots[0][0], k0 + kBN, kend, hk, tid, regs);
-    __builtin_amdgcn_sched_barrier(0);
+  f32x16 sa[2];
+  qk_tile(kst0, kread, qf, sa);
 
-    if (wave_active && k0 < w_kend) {
-      const u32x4* ks = sm.k[st];
-      const u32x4* vts = sm.vt[st];
-      // ---- S^T = K Q^T: two 32-key halves; lane holds keys 8(r/4) + 4g + r%4
-      f32x16 s[2];
-#pragma unroll
-      for (int hh = 0; hh < 2; ++hh) {
-        s[hh] = f32x16{};
-        const int key = 32 * hh + n;
-#pragma unroll
-        for (int kk = 0; kk < 16; ++kk)
-          s[hh] = mfma_32x32x16(ks[key * kKChunks + ((2 * kk + g) ^ (key & 31))], qf[kk], s[hh]);
-      }
-      const bool need_mask = (k0 + kBN) > w_full;
-      float mx = -INFINITY;
-#pragma unroll
-      for (int hh = 0; hh < 2; ++hh) {
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          float v = s[hh][r] * sl2;
-          if (need_mask) {
-            const int key = k0 + 32 * hh + 8 * (r >> 2) + 4 * g + (r & 3);
-            if (key > limit) v = -INFINITY;
-          }
-          s[hh][r] = v;
-          mx = fmaxf(mx, v);
-        }
-      }
-      mx = wave_max_xor(mx, 32);
-      const float mnew = fmaxf(m, mx);
-      const float alpha = fast_exp2(m - mnew);
-      float psum = 0.f;
-#pragma unroll
-      for (int hh = 0; hh < 2; ++hh) {
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          s[hh][r] = fast_exp2(s[hh][r] - mnew);
-          psum += s[hh][r];
-        }
-      }
-      l = l * alpha + psum;
-      m = mnew;
-      if (__ballot(alpha != 1.f)) {
-#pragma unroll
-        for (int i = 0; i < 8; ++i) acc[i] *= alpha;
-      }
+  // One pipelined step per tile: tile j's softmax + PV, tile j + 1's QK^T,
+  // tile j + 2's gather.  Past the last tile the same steps run on the last
+  // tile's slots (already staged, so every load stays inside the pool) and
+  // their results are never read.
+  for (int j = 0; j < n_tiles; ++j) {
+    const int odd = j & 1;
+    uint8_t* const k_this = odd ? kst1 : kst0;   // K(j) stage, gets K(j + 2)
+    uint8_t* const k_next = odd ? kst0 : kst1;   // K(j + 1)
+    uint8_t* const v_this = odd ? vst1 : vst0;   // V(j)
+    uint8_t* const v_next = odd ? vst0 : vst1;   // V(j + 1), written now
 
-      // ---- O^T += V^T P^T over four 16-key steps
-      u32x4 pt[4];
+    if ((j % kTilesPerSlotChunk) == kTilesPerSlotChunk / 2 &&
+        (j / kTilesPerSlotChunk + 1) * kSlotChunk < kend)
+      stage_slots(a, rtt, j / kTilesPerSlotChunk + 1, kend, tid, sm.slots);
+    store_vt<FP8>(v_next, grp, c, regs);
+    gather_tile<FP8>(sm.slots, kb, vb, slot_bytes, min(j + 2, n_tiles - 1) * kBN, run0, regs);
+
+    const int k0 = j * kBN;
+    if (k0 + kBN > w_full) mask_tile(sa, k0, g, limit);
+    f32x16 sn[2];
+    qk_tile(k_next, kread, qf, sn);
+    u32x4 pt[4];
+    float alpha;
+    const bool rescale = softmax_tile(sa, m, l, sl2, pt, alpha);
+    if (rescale) {
 #pragma unroll
-      for (int q4 = 0; q4 < 4; ++q4) {
-        const int hh = q4 >> 1, o = 8 * (q4 & 1);
-#pragma unroll
-        for (int k = 0; k < 4; ++k)
-          pt[q4][k] = pack_bf16(s[hh][o + 2 * k], s[hh][o + 2 * k + 1]);
-      }
-#pragma unroll
-      for (int mt = 0; mt < 8; ++mt) {
-        const int row = 32 * mt + n;
-#pragma unroll
-        for (int q4 = 0; q4 < 4; ++q4)
-          acc[mt] = mfma_32x32x16(vts[row * kVChunks + ((2 * q4 + g) ^ vt_swz(row))], pt[q4],
-                                  acc[mt]);
-      }
+      for (int i = 0; i < 8; ++i) scale_acc(acc[i], alpha);
     }
-    __builtin_amdgcn_sched_barrier(0);
-    if (has_next) store_tile<FP8>(sm.k[st ^ 1], sm.vt[st ^ 1], tid, regs);
+    pv_tile(v_this, vbo, pt, acc);
+    sa[0] = sn[0];
+    sa[1] = sn[1];
+    store_k<FP8>(k_this, run0, c, regs);
     __syncthreads();
   }
 
