@@ -86,7 +86,7 @@ struct __attribute__((aligned(16))) ExtendSmem {
 // One tile's gathered rows for this thread: the 8 keys run0 + {0..3, 8..11}
 // (run0 = 16 (grp / 2) + 4 (grp % 2), grp = tid / 32), 16 bytes each (chunk
 // tid % 32 of the head row: dims 8c .. 8c + 7; fp8 rows keep 8 bytes in .xy).
-// Those 8 keys are exactly V^T positions 8 grp .. 8 grp + 7 (see pv_tile).
+// Those 8 keys are exactly V^T positions 8 grp .. 8 grp + 7 (see exp_pv_tile).
 template <bool FP8>
 struct TileRegs {
   u32x4 k[8];
@@ -97,22 +97,32 @@ __device__ __forceinline__ int run_key(int j) { return 8 * (j >> 2) + (j & 3); }
 
 template <bool FP8>
 __device__ __forceinline__ void gather_tile(const int32_t* slots, const uint8_t* kb,
-                                            const uint8_t* vb, int64_t slot_bytes, int key0,
-                                            int run0, TileRegs<FP8>& r) {
+                                            const uint8_t* vb, uint32_t lane_off,
+                                            int64_t slot_bytes, int key0, int run0,
+                                            TileRegs<FP8>& r) {
   const u32x4 s0 = *reinterpret_cast<const u32x4*>(slots + ((key0 + run0) & kSlotMask));
   const u32x4 s1 = *reinterpret_cast<const u32x4*>(slots + ((key0 + run0 + 8) & kSlotMask));
+  int64_t off[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) off[j] = (int64_t)(j < 4 ? s0[j] : s1[j - 4]) * slot_bytes + lane_off;
+  // K rows first: store_k consumes them a whole tile earlier than store_vt
+  // consumes the V rows.
 #pragma unroll
   for (int j = 0; j < 8; ++j) {
-    const uint32_t slot = j < 4 ? s0[j] : s1[j - 4];
-    const int64_t off = (int64_t)slot * slot_bytes;
     if (FP8) {
-      const u32x2 x = ld_g8(kb + off);
-      const u32x2 y = ld_g8(vb + off);
+      const u32x2 x = ld_g8(kb + off[j]);
       r.k[j] = u32x4{x[0], x[1], 0u, 0u};
+    } else {
+      r.k[j] = ld_g16(kb + off[j]);
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    if (FP8) {
+      const u32x2 y = ld_g8(vb + off[j]);
       r.v[j] = u32x4{y[0], y[1], 0u, 0u};
     } else {
-      r.k[j] = ld_g16(kb + off);
-      r.v[j] = ld_g16(vb + off);
+      r.v[j] = ld_g16(vb + off[j]);
     }
   }
 }
@@ -144,34 +154,63 @@ __device__ __forceinline__ void store_vt(uint8_t* vst, int grp, int c, const Til
   }
 }
 
-// Refills slot-buffer half (chunk & 1) with the slot ids of keys
-// [chunk * 1024, chunk * 1024 + 1024), clamped to the needed range [0, kend).
-__device__ __forceinline__ void stage_slots(const ExtendArgs& a, const int64_t* rtt, int chunk,
-                                            int kend, int tid, int32_t* slots) {
+// Slot ids of keys [chunk * 1024, chunk * 1024 + 1024) clamped to the needed
+// range [0, kend): loaded into registers (4 per thread) a few tiles before
+// they are written to slot-buffer half (chunk & 1), so the req_to_token read
+// latency hides under compute.
+struct SlotPrefetch {
+  int64_t v[kSlotChunk / kThreads];
+};
+
+__device__ __forceinline__ void slot_load(const int64_t* rtt, int chunk, int kend, int tid,
+                                          SlotPrefetch& p) {
   const int k0 = chunk * kSlotChunk;
+#pragma unroll
+  for (int i = 0; i < kSlotChunk / kThreads; ++i) p.v[i] = rtt[min(k0 + tid + i * kThreads, kend - 1)];
+}
+
+__device__ __forceinline__ void slot_store(const SlotPrefetch& p, int chunk, int tid,
+                                           int64_t pool_slots, int32_t* slots) {
   int32_t* buf = slots + (chunk & 1) * kSlotChunk;
-  for (int i = tid; i < kSlotChunk; i += kThreads) {
-    const int key = min(k0 + i, kend - 1);
-    buf[i] = (int32_t)clamp_i64(rtt[key], 0, a.pool_slots - 1);
-  }
+#pragma unroll
+  for (int i = 0; i < kSlotChunk / kThreads; ++i)
+    buf[tid + i * kThreads] = (int32_t)clamp_i64(p.v[i], 0, pool_slots - 1);
 }
 
 // S^T (64 keys x 32 rows) = K_tile Q^T: s[hh][r] is key 32 hh + 8 (r / 4) + 4 g + r % 4.
+// K fragments are read kQkAhead steps ahead of the MFMAs that consume them.
+constexpr int kQkAhead = 3;
 __device__ __forceinline__ void qk_tile(const uint8_t* kst, int kread, const u32x4 (&qf)[16],
                                         f32x16 (&s)[2]) {
+  u32x4 fr[kQkAhead + 1][2];
+#pragma unroll
+  for (int p = 0; p < kQkAhead; ++p)
+#pragma unroll
+    for (int hh = 0; hh < 2; ++hh) fr[p][hh] = ld_s16(kst + kread + hh * 32 * kKStride + 32 * p);
   s[0] = f32x16{};
   s[1] = f32x16{};
 #pragma unroll
   for (int kk = 0; kk < 16; ++kk) {
+    if (kk + kQkAhead < 16) {
 #pragma unroll
-    for (int hh = 0; hh < 2; ++hh)
-      s[hh] = mfma_32x32x16(ld_s16(kst + kread + hh * 32 * kKStride + 32 * kk), qf[kk], s[hh]);
+      for (int hh = 0; hh < 2; ++hh)
+        fr[(kk + kQkAhead) % (kQkAhead + 1)][hh] =
+            ld_s16(kst + kread + hh * 32 * kKStride + 32 * (kk + kQkAhead));
+    }
+#pragma unroll
+    for (int hh = 0; hh < 2; ++hh) s[hh] = mfma_32x32x16(fr[kk % (kQkAhead + 1)][hh], qf[kk], s[hh]);
   }
+  // Keep the reads kQkAhead steps ahead: the scheduler would otherwise sink
+  // them next to their MFMAs and expose the LDS latency.
+  __builtin_amdgcn_sched_group_barrier(0x100, 2 * kQkAhead, 0);
+#pragma unroll
+  for (int i = 0; i < 32 - 2 * kQkAhead; ++i) {
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+    __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+  }
+  __builtin_amdgcn_sched_group_barrier(0x008, 2 * kQkAhead, 0);
 }
 
-// Online softmax of one tile's scores (raw, unscaled) for this lane's row;
-// leaves P^T packed as the B operands of the four 16-key PV steps.  Returns
-// true (wave-uniform) when the accumulator must be multiplied by alpha.
 // Sets the scores of keys past this lane's last visible key to -inf.
 __device__ __forceinline__ void mask_tile(f32x16 (&s)[2], int k0, int g, int limit) {
 #pragma unroll
@@ -181,54 +220,74 @@ __device__ __forceinline__ void mask_tile(f32x16 (&s)[2], int k0, int g, int lim
       if (k0 + 32 * hh + 8 * (r >> 2) + 4 * g + (r & 3) > limit) s[hh][r] = -INFINITY;
 }
 
-// Online softmax of one tile's scores (raw, unscaled) for this lane's row;
-// leaves P^T packed as the B operands of the four 16-key PV steps.  Returns
-// true (wave-uniform) when the accumulator must be multiplied by alpha.
-__device__ __forceinline__ bool softmax_tile(f32x16 (&s)[2], float& m, float& l, float sl2,
-                                             u32x4 (&pt)[4], float& alpha) {
+// Online softmax of one tile's scores (raw, unscaled) for this lane's row, in
+// two halves so that the rare accumulator rescale can sit between them and the
+// exps stay in the same scheduling region as the PV MFMAs that consume them.
+//
+// softmax_max: the row max over the tile; the reference max m is raised only
+// when some row of the wave outgrew it by more than 2^kRescaleLog2 (returns
+// true, wave-uniform, with alpha = the factor for the accumulator and l).
+__device__ __forceinline__ bool softmax_max(const f32x16 (&s)[2], float& m, float& l, float sl2,
+                                            float& alpha) {
   float mx = s[0][0];
 #pragma unroll
   for (int r = 1; r < 16; ++r) mx = fmaxf(mx, s[0][r]);
 #pragma unroll
   for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[1][r]);
   mx = wave_max_xor(mx, 32);
-  // Raise the reference max only when some row of the wave outgrew it by 2^8.
   const bool grow = (mx - m) * sl2 > kRescaleLog2;
   const bool any = __ballot(grow) != 0;
   const float mnew = any ? fmaxf(m, mx) : m;
   alpha = any ? fast_exp2((m - mnew) * sl2) : 1.f;
-  const float moff = mnew == -INFINITY ? 0.f : mnew * sl2;
-  float psum = 0.f;
-#pragma unroll
-  for (int hh = 0; hh < 2; ++hh)
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const float p = fast_exp2(fmaf(s[hh][r], sl2, -moff));
-      s[hh][r] = p;
-      psum += p;
-    }
-  l = l * alpha + psum;
+  l *= alpha;
   m = mnew;
-#pragma unroll
-  for (int q4 = 0; q4 < 4; ++q4) {
-    const int hh = q4 >> 1, o = 8 * (q4 & 1);
-#pragma unroll
-    for (int k = 0; k < 4; ++k) pt[q4][k] = pack_bf16(s[hh][o + 2 * k], s[hh][o + 2 * k + 1]);
-  }
   return any;
 }
 
-// O^T += V^T P^T.  A operand of step q4 for output dims 32 mt + n: V^T row
-// 32 mt + n, positions 16 q4 + 8 g .. +8, i.e. keys 16 q4 + 8 (j / 4) + 4 g + j % 4
-// (the order in which P^T leaves the S^T accumulator).
-__device__ __forceinline__ void pv_tile(const uint8_t* vst, const int (&vb)[4][2],
-                                        const u32x4 (&pt)[4], f32x16 (&acc)[8]) {
+// Exp half of the softmax fused with O^T += V^T P^T.
+//
+// p = 2^(s sl2 - m sl2) for the tile's 32 scores of this lane, l += sum p, and
+// P^T packed as the B operands of four 16-key steps: step q4 takes scores
+// 8 q4 .. 8 q4 + 7 (keys 16 q4 + 8 (j / 4) + 4 g + j % 4), and its A operand for
+// output dims 32 mt + n is V^T row 32 mt + n, positions 16 q4 + 8 g .. +8.
+// The exps of step q4 + 1 are issued one per MFMA of step q4, and the V^T
+// reads kPvAhead MFMAs ahead; scheduling barriers keep that order.
+constexpr int kPvAhead = 6;
+__device__ __forceinline__ void exp_pv_tile(const uint8_t* vst, const int (&vb)[4][2],
+                                            const f32x16 (&s)[2], float m, float& l,
+                                            float sl2, f32x16 (&acc)[8]) {
+  const float moff = m == -INFINITY ? 0.f : m * sl2;
+  float p[32];
+  u32x4 pt[4];
+  auto ex = [&](int i) { p[i] = fast_exp2(fmaf(s[i >> 4][i & 15], sl2, -moff)); };
+  auto pack = [&](int q4) {
 #pragma unroll
-  for (int q4 = 0; q4 < 4; ++q4)
+    for (int k = 0; k < 4; ++k) pt[q4][k] = pack_bf16(p[8 * q4 + 2 * k], p[8 * q4 + 2 * k + 1]);
+  };
+  auto vread = [&](int i) {
+    return ld_s16(vst + vb[i / 8][i & 1] + 32 * kVtStride * (i % 8));
+  };
+  u32x4 fr[kPvAhead + 1];
 #pragma unroll
-    for (int mt = 0; mt < 8; ++mt)
-      acc[mt] = mfma_32x32x16(ld_s16(vst + vb[q4][mt & 1] + 32 * kVtStride * mt), pt[q4],
-                              acc[mt]);
+  for (int i = 0; i < kPvAhead; ++i) fr[i] = vread(i);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) ex(i);
+  pack(0);
+#pragma unroll
+  for (int i = 0; i < 32; ++i) {
+    __builtin_amdgcn_sched_barrier(0);
+    acc[i % 8] = mfma_32x32x16(fr[i % (kPvAhead + 1)], pt[i / 8], acc[i % 8]);
+    if (i + kPvAhead < 32) fr[(i + kPvAhead) % (kPvAhead + 1)] = vread(i + kPvAhead);
+    if (i < 24) {
+      ex(8 + i);
+      if (i % 8 == 7) pack(i / 8 + 1);
+    }
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  float ps[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int i = 0; i < 32; ++i) ps[i & 3] += p[i];
+  l += (ps[0] + ps[1]) + (ps[2] + ps[3]);
 }
 
 // Multiplies an accumulator tile held in AGPRs by a per-lane factor one
@@ -306,8 +365,9 @@ extend_kernel(ExtendArgs a) {
   const int run0 = 16 * (grp >> 1) + 4 * (grp & 1);
   constexpr int kRowBytes = FP8 ? kD : 2 * kD;
   const int64_t slot_bytes = (int64_t)a.hkv * kRowBytes;
-  const uint8_t* kb = a.k_pool + (int64_t)hk * kRowBytes + (FP8 ? 8 : 16) * c;
-  const uint8_t* vb = a.v_pool + (int64_t)hk * kRowBytes + (FP8 ? 8 : 16) * c;
+  const uint8_t* kb = a.k_pool + (int64_t)hk * kRowBytes;
+  const uint8_t* vb = a.v_pool + (int64_t)hk * kRowBytes;
+  const uint32_t lane_off = (FP8 ? 8 : 16) * c;
 
   // LDS read offsets of this lane.
   const int kread = n * kKStride + 16 * g;
@@ -341,14 +401,16 @@ extend_kernel(ExtendArgs a) {
 
   // ---- prologue: K(0), V(0), K(1) in LDS; V(1) in registers; S(0) computed.
   // With a single tile the unused K(1) / V(1) stages are simply never read.
-  stage_slots(a, rtt, 0, kend, tid, sm.slots);
+  SlotPrefetch spf;
+  slot_load(rtt, 0, kend, tid, spf);
+  slot_store(spf, 0, tid, a.pool_slots, sm.slots);
   __syncthreads();
   TileRegs<FP8> regs;
-  gather_tile<FP8>(sm.slots, kb, vb, slot_bytes, 0, run0, regs);
+  gather_tile<FP8>(sm.slots, kb, vb, lane_off, slot_bytes, 0, run0, regs);
   store_k<FP8>(kst0, run0, c, regs);
   store_vt<FP8>(vst0, grp, c, regs);
   if (n_tiles > 1) {
-    gather_tile<FP8>(sm.slots, kb, vb, slot_bytes, kBN, run0, regs);
+    gather_tile<FP8>(sm.slots, kb, vb, lane_off, slot_bytes, kBN, run0, regs);
     store_k<FP8>(kst1, run0, c, regs);
   }
   __syncthreads();
@@ -367,24 +429,29 @@ extend_kernel(ExtendArgs a) {
     uint8_t* const v_this = odd ? vst1 : vst0;   // V(j)
     uint8_t* const v_next = odd ? vst0 : vst1;   // V(j + 1), written now
 
-    if ((j % kTilesPerSlotChunk) == kTilesPerSlotChunk / 2 &&
-        (j / kTilesPerSlotChunk + 1) * kSlotChunk < kend)
-      stage_slots(a, rtt, j / kTilesPerSlotChunk + 1, kend, tid, sm.slots);
+    // Slot ids of the next 1024 keys: loaded at tile 4 of a chunk, written at
+    // tile 8, first read by the gather at tile 14.
+    if ((j / kTilesPerSlotChunk + 1) * kSlotChunk < kend) {
+      if (j % kTilesPerSlotChunk == 4) slot_load(rtt, j / kTilesPerSlotChunk + 1, kend, tid, spf);
+      if (j % kTilesPerSlotChunk == 8)
+        slot_store(spf, j / kTilesPerSlotChunk + 1, tid, a.pool_slots, sm.slots);
+    }
     store_vt<FP8>(v_next, grp, c, regs);
-    gather_tile<FP8>(sm.slots, kb, vb, slot_bytes, min(j + 2, n_tiles - 1) * kBN, run0, regs);
+    gather_tile<FP8>(sm.slots, kb, vb, lane_off, slot_bytes,
+                          min(j + 2, n_tiles - 1) * kBN, run0, regs);
 
     const int k0 = j * kBN;
     if (k0 + kBN > w_full) mask_tile(sa, k0, g, limit);
     f32x16 sn[2];
+    __builtin_amdgcn_sched_barrier(0);
     qk_tile(k_next, kread, qf, sn);
-    u32x4 pt[4];
+    __builtin_amdgcn_sched_barrier(0);
     float alpha;
-    const bool rescale = softmax_tile(sa, m, l, sl2, pt, alpha);
-    if (rescale) {
+    if (softmax_max(sa, m, l, sl2, alpha)) {
 #pragma unroll
       for (int i = 0; i < 8; ++i) scale_acc(acc[i], alpha);
     }
-    pv_tile(v_this, vbo, pt, acc);
+    exp_pv_tile(v_this, vbo, sa, m, l, sl2, acc);
     sa[0] = sn[0];
     sa[1] = sn[1];
     store_k<FP8>(k_this, run0, c, regs);
