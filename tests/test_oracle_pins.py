@@ -276,3 +276,56 @@ def test_forward_batch_defaults_follow_reference_rules():
     assert fb.max_extend_len == 3 and fb.max_seq_len == 12
     assert fb.extend_lens_tensor.tolist() == [1, 3]
     assert fb.req_pool_indices_list == [3, 1]
+
+
+def _ocp_e4m3_value(code: int) -> float:
+    """OCP 8-bit float E4M3 (FN) decoding from the format definition: sign bit,
+    4 exponent bits (bias 7), 3 mantissa bits, subnormals at exponent 0, no
+    infinities, S.1111.111 is NaN."""
+    sign = -1.0 if code & 0x80 else 1.0
+    exp = (code >> 3) & 0xF
+    man = code & 0x7
+    if exp == 0xF and man == 0x7:
+        return float("nan")
+    if exp == 0:
+        return sign * man / 8.0 * 2.0 ** -6
+    return sign * (1.0 + man / 8.0) * 2.0 ** (exp - 7)
+
+
+def test_e4m3_oracle_matches_ocp_definition():
+    """The fp8 oracle's dequantisation of every code equals the OCP formula, and
+    its quantisation is round-to-nearest-even onto that table with saturation at
+    +-448 (checked on random values, exact table values and every midpoint)."""
+    from oracle.kv_quant import dequantize_e4m3, quantize_e4m3
+    codes = torch.arange(256, dtype=torch.uint8).view(torch.float8_e4m3fn)
+    got = dequantize_e4m3(codes, 1.0).numpy()
+    want = np.array([_ocp_e4m3_value(c) for c in range(256)])
+    nan = np.isnan(want)
+    assert np.array_equal(np.isnan(got), nan)
+    assert np.array_equal(got[~nan], want[~nan])
+
+    table = np.unique(want[~nan])                    # sorted finite values
+    assert table.max() == 448.0 and table.min() == -448.0
+    mids = (table[1:] + table[:-1]) / 2
+    rng = np.random.default_rng(5)
+    xs = np.concatenate([rng.normal(0, 100, 4000), rng.uniform(-600, 600, 2000), table, mids,
+                         [1e-9, -1e-9, 2.0 ** -10, 500.0, -1e6]]).astype(np.float32)
+
+    def rne(x):
+        x = min(max(float(x), -448.0), 448.0)
+        i = np.searchsorted(table, x)
+        if i < len(table) and table[i] == x:
+            return x
+        lo, hi = table[i - 1], table[i]
+        if x - lo != hi - x:
+            return lo if x - lo < hi - x else hi
+        # tie: the even code (mantissa lsb 0)
+        code_lo = int(np.nonzero(want == lo)[0][0])
+        return lo if (code_lo & 1) == 0 else hi
+
+    q = dequantize_e4m3(quantize_e4m3(torch.from_numpy(xs), 1.0), 1.0).numpy()
+    ref = np.array([rne(x) for x in xs])
+    assert np.array_equal(q, ref)
+    # a scale divides before rounding
+    q2 = dequantize_e4m3(quantize_e4m3(torch.from_numpy(xs[:100]), 0.5), 0.5).numpy()
+    assert np.array_equal(q2, np.array([rne(x / 0.5) for x in xs[:100]]) * 0.5)
