@@ -44,8 +44,8 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--only", default="decode,extend,mixed,fp8",
-                    help="comma list of decode,extend,mixed,fp8,copy")
+    ap.add_argument("--only", default="decode,extend,mixed,fp8,prep",
+                    help="comma list of decode,extend,mixed,fp8,prep,copy")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--workgroups", type=int, default=0,
                     help="decode persistent grid size (0 = one per CU)")
@@ -182,6 +182,42 @@ def bench_fp8(torch, workloads, SlotAttentionCall, args):
                          "kernel": "decode_kernel<fp8>"}}
 
 
+def bench_prep(torch, args):
+    """Fused q/k RMSNorm + partial RoPE + KV write over one 20k-token prefill
+    step (24 q / 4 kv heads, head_dim 256, bf16): HBM-bound elementwise work."""
+    from oracle.qk_prep import inv_freq_ref
+    from tokenfactory_amd import qk_norm_rope_kv_write
+    T, hq, hkv, d, pool = 20480, 24, 4, 256, 1 << 18
+    g = torch.Generator(device="cuda").manual_seed(23)
+    qg = torch.randn(T, hq, 2 * d, device="cuda", generator=g).to(torch.bfloat16)
+    k = torch.randn(T, hkv, d, device="cuda", generator=g).to(torch.bfloat16)
+    v = torch.randn(T, hkv, d, device="cuda", generator=g).to(torch.bfloat16)
+    qw = torch.ones(d, device="cuda")
+    kw = torch.ones(d, device="cuda")
+    pos = torch.arange(T, device="cuda")
+    loc = torch.randperm(pool - 1, device="cuda", generator=g)[:T] + 1
+    kp = torch.zeros(pool, hkv, d, dtype=torch.bfloat16, device="cuda")
+    vp = torch.zeros_like(kp)
+    out = torch.empty(T, hq, d, dtype=torch.bfloat16, device="cuda")
+    invf = inv_freq_ref(64, 1e7).cuda()
+    q = qg[:, :, :d]
+    fn = lambda: qk_norm_rope_kv_write(q, k, v, qw, kw, 1e-6, pos, invf, 64, [11, 11, 10],
+                                       True, kp, vp, loc, out=out)
+    k_ms = time_kernel(torch, [None], args.steps, lambda c: fn())
+    # read q, k, v and positions / slots; write q_out, K, V rows
+    nbytes = T * ((hq + 2 * hkv) * d * 2 * 2 + 16)
+    log(f"qk_prep (20k tokens): {k_ms*1e3:.1f} us, {nbytes/(k_ms*1e-3)/1e9:.0f} GB/s "
+        f"({nbytes/(k_ms*1e-3)/HBM_PEAK*100:.1f}% of HBM peak)")
+    return {"workload": "fused q/k RMSNorm + partial RoPE + KV write: 20480 tokens, 24q/4kv, "
+                        "head_dim 256, bf16, scattered slots",
+            "value": nbytes / (k_ms * 1e-3) / 1e9, "unit": "GB/s", "kernel_ms": k_ms,
+            "bytes_per_launch": nbytes,
+            "roofline": {"bound": "hbm", "achieved": nbytes / (k_ms * 1e-3) / 1e9,
+                         "peak": HBM_PEAK / 1e9, "unit": "GB/s",
+                         "frac": nbytes / (k_ms * 1e-3) / HBM_PEAK,
+                         "kernel": "qk_prep_kernel"}}
+
+
 def bench_copy(torch, args):
     """A plain device copy of known size, the reference point for HBM counters."""
     n = 1 << 30
@@ -261,6 +297,9 @@ def main():
         torch.cuda.empty_cache()
     if "fp8" in only:
         secondary["decode_fp8_128k"] = bench_fp8(torch, workloads, SlotAttentionCall, args)
+        torch.cuda.empty_cache()
+    if "prep" in only:
+        secondary["qk_prep_20k"] = bench_prep(torch, args)
         torch.cuda.empty_cache()
     if dec is None:
         print(json.dumps({"metric": METRIC, "value": None, "secondary": secondary},

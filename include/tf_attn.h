@@ -59,7 +59,7 @@ enum {
   TF_ERR_HIP = -3          /* a HIP runtime call failed */
 };
 
-/* Integer ABI revision; bumped whenever a signature below changes. */
+/* Integer ABI revision; bumped whenever a signature below changes or one is added. */
 int32_t tf_attn_abi_version(void);
 
 /* Message for the last non-zero return on the calling thread ("" if none). */
@@ -192,6 +192,42 @@ int32_t tf_kv_write(const void* k, const void* v, int64_t src_row_stride,
                     void* k_pool, void* v_pool, int64_t pool_slots, int32_t kv_dtype,
                     const float* k_scale, const float* v_scale,
                     int32_t num_kv_heads, int32_t head_dim, tf_stream_t stream);
+
+/* ------------------------------------------------------------------ q/k prep
+ * Fused q/k RMSNorm + partial (M-)RoPE + KV scatter-write, the steps right
+ * before attention: q = q_norm(q), k = k_norm(k) (full_attention.py:141-142,
+ * rms_norm.py:19-24), q, k = rotary_emb(q, k, positions) (:143,
+ * rotary_embedding.py:46-95), layer_k_buffer[out_cache_loc] = k and the same
+ * for v (:146-149), with the reference's bf16 rounding steps.
+ *
+ * q: bf16 rows of n_tokens x num_q_heads x head_dim at (q_token_stride,
+ * q_head_stride) elements (a view of the gated q projection works as is);
+ * k / v: bf16 [n_tokens, num_kv_heads, head_dim] with token strides.
+ * q_norm_weight / k_norm_weight: fp32 [head_dim], 16-byte aligned.
+ * positions: int64 [position_rows, *] (1 = text positions, 3 = M-RoPE),
+ * rows position_row_stride elements apart. inv_freq: fp32 [rotary_dim / 2].
+ * mrope_section*: the three M-RoPE sections (summing to rotary_dim / 2),
+ * mrope_interleaved: 1 for the interleaved layout.
+ * q_out: bf16 [n_tokens, num_q_heads, head_dim] (token stride q_out_token_stride).
+ * K / V rows go to the pool like tf_kv_write (bf16, or fp8-e4m3 with
+ * k_scale / v_scale); slots outside [0, pool_slots) are skipped.
+ * head_dim 256 only; rotary_dim a multiple of 16.
+ */
+int32_t tf_qk_norm_rope_kv_write(const void* q, int64_t q_token_stride, int64_t q_head_stride,
+                                 const void* k, int64_t k_token_stride,
+                                 const void* v, int64_t v_token_stride,
+                                 int64_t n_tokens, int32_t num_q_heads, int32_t num_kv_heads,
+                                 int32_t head_dim, const float* q_norm_weight,
+                                 const float* k_norm_weight, float eps,
+                                 const int64_t* positions, int32_t position_rows,
+                                 int64_t position_row_stride, const float* inv_freq,
+                                 int32_t rotary_dim, int32_t mrope_section0,
+                                 int32_t mrope_section1, int32_t mrope_section2,
+                                 int32_t mrope_interleaved, void* q_out,
+                                 int64_t q_out_token_stride, const int64_t* out_cache_loc,
+                                 void* k_pool, void* v_pool, int64_t pool_slots,
+                                 int32_t kv_dtype, const float* k_scale, const float* v_scale,
+                                 tf_stream_t stream);
 
 /* ------------------------------------------------------------------ gather
  * Padded slot gather of the batched branches (full_attention.py:216-220):

@@ -6,11 +6,11 @@ Public surface (the reference's names and contracts, see each module):
 * ``FullAttnKVPool``    - slot-indexed K/V pool, bf16 or fp8-e4m3 + scales
 * ``FullAttention``     - module with the reference's ``forward`` /
   ``_slot_based_attention`` signatures
-* ``slot_based_attention`` / ``write_kv`` / ``gather_kv`` - the kernels'
-  Python entry points
+* ``slot_based_attention`` / ``write_kv`` / ``gather_kv`` /
+  ``qk_norm_rope_kv_write`` - the kernels' Python entry points
 """
 from .forward_batch import ForwardBatch
-from .attention import gather_kv, slot_based_attention, write_kv
+from .attention import gather_kv, qk_norm_rope_kv_write, slot_based_attention, write_kv
 from .kv_pool import FullAttnKVPool
 from .full_attention import FullAttention
 
@@ -19,6 +19,7 @@ __all__ = [
     "FullAttnKVPool",
     "FullAttention",
     "gather_kv",
+    "qk_norm_rope_kv_write",
     "slot_based_attention",
     "write_kv",
 ]

@@ -12,7 +12,7 @@ from pathlib import Path
 from typing import Optional
 
 LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libtf_attn.so"
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 TF_DTYPE_BF16 = 0
 TF_DTYPE_FP8_E4M3 = 1
@@ -63,6 +63,18 @@ SIGNATURES = {
         _p, _i64,                      # out_cache_loc, n_tokens
         _p, _p, _i64, _i32, _p, _p,    # k_pool, v_pool, pool_slots, kv_dtype, k_scale, v_scale
         _i32, _i32, _p,                # num_kv_heads, head_dim, stream
+    ]),
+    "tf_qk_norm_rope_kv_write": (_i32, [
+        _p, _i64, _i64,                # q, q_token_stride, q_head_stride
+        _p, _i64, _p, _i64,            # k, k_token_stride, v, v_token_stride
+        _i64, _i32, _i32, _i32,        # n_tokens, num_q_heads, num_kv_heads, head_dim
+        _p, _p, _f32,                  # q_norm_weight, k_norm_weight, eps
+        _p, _i32, _i64,                # positions, position_rows, position_row_stride
+        _p, _i32, _i32, _i32, _i32,    # inv_freq, rotary_dim, mrope sections
+        _i32,                          # mrope_interleaved
+        _p, _i64,                      # q_out, q_out_token_stride
+        _p, _p, _p, _i64, _i32,        # out_cache_loc, k_pool, v_pool, pool_slots, kv_dtype
+        _p, _p, _p,                    # k_scale, v_scale, stream
     ]),
     "tf_gather_kv": (_i32, [
         _p, _i32, _i64, _i64,          # pool, kv_dtype, pool_slots, row_elems

@@ -306,3 +306,73 @@ def write_kv(layer_k_buffer: torch.Tensor, layer_v_buffer: torch.Tensor,
                  layer_v_buffer.data_ptr(), layer_k_buffer.shape[0], kv_dtype,
                  _ptr(k_scale), _ptr(v_scale), n_kv, head_dim,
                  torch.cuda.current_stream(k.device).cuda_stream)
+
+
+def qk_norm_rope_kv_write(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
+                          q_norm_weight: torch.Tensor, k_norm_weight: torch.Tensor,
+                          eps: float, positions: torch.Tensor, inv_freq: torch.Tensor,
+                          rotary_dim: int, mrope_section, mrope_interleaved: bool,
+                          layer_k_buffer: torch.Tensor, layer_v_buffer: torch.Tensor,
+                          out_cache_loc: torch.Tensor,
+                          k_scale: Optional[torch.Tensor] = None,
+                          v_scale: Optional[torch.Tensor] = None,
+                          out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """``q_norm``/``k_norm`` + ``rotary_emb`` + the KV write of
+    ``full_attention.py:141-149`` in one ``tf_qk_norm_rope_kv_write`` launch.
+
+    ``q`` is ``[T, Hq, D]`` (any token and head stride, e.g. the q half of the
+    gated projection), ``k`` / ``v`` ``[T, Hkv, D]`` bf16; ``positions`` is
+    ``[T]`` or ``[3, T]`` (M-RoPE). Returns the normalised, rotated q as a new
+    contiguous ``[T, Hq, D]`` bf16 tensor (or writes ``out``); K and V land in
+    the pool at ``out_cache_loc``.
+    """
+    if not q.is_cuda:
+        raise RuntimeError("qk_norm_rope_kv_write runs only on ROCm devices")
+    if q.dtype != torch.bfloat16 or k.dtype != torch.bfloat16 or v.dtype != torch.bfloat16:
+        raise NotImplementedError("q/k/v must be bf16")
+    if q.dim() != 3 or k.dim() != 3 or k.shape != v.shape or q.shape[0] != k.shape[0]:
+        raise ValueError(f"bad q/k/v shapes {tuple(q.shape)} {tuple(k.shape)} {tuple(v.shape)}")
+    T, hq, d = q.shape
+    hkv = k.shape[1]
+    if k.shape[2] != d or layer_k_buffer.shape[1:] != (hkv, d):
+        raise ValueError(f"k {tuple(k.shape)} does not match pool rows {tuple(layer_k_buffer.shape[1:])}")
+    if q.stride(2) != 1:
+        raise ValueError("q rows must be contiguous along head_dim")
+    if k.stride(2) != 1 or k.stride(1) != d or v.stride(2) != 1 or v.stride(1) != d:
+        k, v = k.contiguous(), v.contiguous()
+    kv_dtype = _KV_DTYPES.get(layer_k_buffer.dtype)
+    if kv_dtype is None:
+        raise NotImplementedError(f"pool dtype {layer_k_buffer.dtype}")
+    if not (layer_k_buffer.is_contiguous() and layer_v_buffer.is_contiguous()):
+        raise ValueError("KV pools must be contiguous")
+    if kv_dtype == _native.TF_DTYPE_FP8_E4M3:
+        if k_scale is None or v_scale is None:
+            raise ValueError("an fp8 KV pool needs k_scale and v_scale")
+        k_scale = k_scale.to(device=q.device, dtype=torch.float32).reshape(1).contiguous()
+        v_scale = v_scale.to(device=q.device, dtype=torch.float32).reshape(1).contiguous()
+    loc = out_cache_loc.to(device=q.device, dtype=torch.int64).contiguous()
+    if loc.numel() != T:
+        raise ValueError(f"out_cache_loc has {loc.numel()} slots for {T} tokens")
+    pos = positions.to(device=q.device, dtype=torch.int64)
+    if pos.dim() == 1:
+        pos = pos.reshape(1, -1)
+    if pos.dim() != 2 or pos.shape[0] not in (1, 3) or pos.shape[1] != T:
+        raise ValueError(f"positions {tuple(positions.shape)} for {T} tokens")
+    pos = pos.contiguous()
+    qw = q_norm_weight.to(device=q.device, dtype=torch.float32).contiguous()
+    kw = k_norm_weight.to(device=q.device, dtype=torch.float32).contiguous()
+    freqs = inv_freq.to(device=q.device, dtype=torch.float32).contiguous()
+    if freqs.numel() != rotary_dim // 2:
+        raise ValueError(f"inv_freq has {freqs.numel()} entries for rotary_dim {rotary_dim}")
+    sec = list(mrope_section) if mrope_section is not None else [0, 0, 0]
+    if out is None:
+        out = torch.empty((T, hq, d), dtype=torch.bfloat16, device=q.device)
+    _native.call("tf_qk_norm_rope_kv_write", q.data_ptr(), q.stride(0), q.stride(1),
+                 k.data_ptr(), k.stride(0), v.data_ptr(), v.stride(0), T, hq, hkv, d,
+                 qw.data_ptr(), kw.data_ptr(), float(eps), pos.data_ptr(), pos.shape[0],
+                 pos.stride(0), freqs.data_ptr(), rotary_dim, sec[0], sec[1], sec[2],
+                 int(bool(mrope_interleaved)), out.data_ptr(), out.stride(0), loc.data_ptr(),
+                 layer_k_buffer.data_ptr(), layer_v_buffer.data_ptr(),
+                 layer_k_buffer.shape[0], kv_dtype, _ptr(k_scale), _ptr(v_scale),
+                 torch.cuda.current_stream(q.device).cuda_stream)
+    return out

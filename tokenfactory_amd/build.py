@@ -17,7 +17,7 @@ REPO_DIR = PKG_DIR.parent
 CSRC = PKG_DIR / "csrc"
 LIB_DIR = PKG_DIR / "_lib"
 LIB_PATH = LIB_DIR / "libtf_attn.so"
-SOURCES = ["abi.hip", "decode.hip", "extend.hip", "kv_ops.hip"]
+SOURCES = ["abi.hip", "decode.hip", "extend.hip", "kv_ops.hip", "qk_prep.hip"]
 ARCH = "gfx950"
 
 

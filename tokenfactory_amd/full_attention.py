@@ -4,16 +4,19 @@ Keeps the reference's call signatures
 ``forward(hidden_states, positions, cache_pool, forward_batch)``
 (``qwen3_8/full_attention.py:112-161``) and
 ``_slot_based_attention(q, layer_k_buffer, layer_v_buffer, batch)`` (``:163-283``),
-and its per-rank head bookkeeping (``:36-52``). The two hot steps run on the
-gfx950 kernels: the KV scatter-write (``:146-149``, ``tf_kv_write``) and the
-attention itself (``tf_attn_decode`` / ``tf_attn_extend``).
+and its per-rank head bookkeeping (``:36-52``). The hot steps run on the
+gfx950 kernels: q/k norm + RoPE + the KV scatter-write (``:141-149``,
+``tf_qk_norm_rope_kv_write``) and the attention itself (``tf_attn_decode`` /
+``tf_attn_extend``).
 
-The surrounding steps stay PyTorch ops, as the reference has them: q/k/v/o
-projections (plain bf16 ``nn.Linear`` here; the reference's block-FP8 linears
-are a separate component), q/k RMSNorm with the ``w * x`` convention
-(``qwen3_8/rms_norm.py:19-24``), partial rotate-half RoPE on the first
-``head_dim * partial_rotary_factor`` dims (``qwen3_8/rotary_embedding.py:46-95``)
-and the ``silu(gate)`` output gate (``full_attention.py:157-158``).
+q/k RMSNorm with the ``w * x`` convention (``qwen3_8/rms_norm.py:19-24``),
+partial rotate-half RoPE on the first ``head_dim * partial_rotary_factor`` dims
+(``qwen3_8/rotary_embedding.py:46-95``) and the KV write run as one fused
+kernel (``tf_qk_norm_rope_kv_write``); ``RMSNorm`` / ``PartialRoPE`` below hold
+their parameters and state the same math in PyTorch. The q/k/v/o projections
+(plain bf16 ``nn.Linear`` here; the reference's block-FP8 linears are a
+separate component) and the ``silu(gate)`` output gate
+(``full_attention.py:157-158``) stay PyTorch ops, as the reference has them.
 """
 from __future__ import annotations
 
@@ -23,7 +26,7 @@ import torch
 import torch.nn as nn
 import torch.nn.functional as F
 
-from .attention import slot_based_attention, write_kv
+from .attention import qk_norm_rope_kv_write, slot_based_attention
 
 
 class RMSNorm(nn.Module):
@@ -135,14 +138,15 @@ class FullAttention(nn.Module):
         k = self.k_proj(hidden_states).view(n_tok, self.num_kv_heads, self.head_dim)
         v = self.v_proj(hidden_states).view(n_tok, self.num_kv_heads, self.head_dim)
 
-        q = self.q_norm(q)
-        k = self.k_norm(k)
-        q, k = self.rotary_emb(q, k, positions)
-
         k_buf, v_buf = cache_pool.get_full_kv_buffers(self.layer_idx)
         scales = (cache_pool.get_full_kv_scales(self.layer_idx)
                   if hasattr(cache_pool, "get_full_kv_scales") else (None, None))
-        write_kv(k_buf, v_buf, forward_batch.out_cache_loc, k, v, *scales)
+        # q_norm / k_norm, partial RoPE and the KV write (:141-149) in one launch.
+        rope = self.rotary_emb
+        q = qk_norm_rope_kv_write(
+            q, k, v, self.q_norm.weight, self.k_norm.weight, self.q_norm.eps, positions,
+            rope.inv_freq, rope.rotary_dim, rope.mrope_section, rope.mrope_interleaved,
+            k_buf, v_buf, forward_batch.out_cache_loc, *scales)
 
         self._kv_scales = scales
         try:
