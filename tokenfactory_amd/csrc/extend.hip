@@ -128,6 +128,24 @@ __device__ __forceinline__ void gather_tile(const int32_t* slots, const uint8_t*
 }
 
 template <bool FP8>
+__device__ __forceinline__ void gather_k(const int32_t* slots, const uint8_t* kb, uint32_t lane_off,
+                                         int64_t slot_bytes, int key0, int run0,
+                                         TileRegs<FP8>& r) {
+  const u32x4 s0 = *reinterpret_cast<const u32x4*>(slots + ((key0 + run0) & kSlotMask));
+  const u32x4 s1 = *reinterpret_cast<const u32x4*>(slots + ((key0 + run0 + 8) & kSlotMask));
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const int64_t off = (int64_t)(j < 4 ? s0[j] : s1[j - 4]) * slot_bytes + lane_off;
+    if (FP8) {
+      const u32x2 x = ld_g8(kb + off);
+      r.k[j] = u32x4{x[0], x[1], 0u, 0u};
+    } else {
+      r.k[j] = ld_g16(kb + off);
+    }
+  }
+}
+
+template <bool FP8>
 __device__ __forceinline__ void store_k(uint8_t* kst, int run0, int c, const TileRegs<FP8>& r) {
   uint8_t* p = kst + run0 * kKStride + 16 * c;
 #pragma unroll
@@ -218,6 +236,85 @@ __device__ __forceinline__ void mask_tile(f32x16 (&s)[2], int k0, int g, int lim
 #pragma unroll
     for (int r = 0; r < 16; ++r)
       if (k0 + 32 * hh + 8 * (r >> 2) + 4 * g + (r & 3) > limit) s[hh][r] = -INFINITY;
+}
+
+// Phase A of a pipelined step: S^T of tile j + 1 (as qk_tile) with the tile
+// staging spread one item per MFMA, so that LDS writes, global-load issue and
+// the V transpose overlap matrix-core work instead of stalling in a burst:
+//   MFMA 0:      slot ids of K tile kt and V tile vt from the LDS slot buffer
+//   MFMAs 0-7:   K rows in registers -> K stage k_dst (one key per MFMA)
+//   MFMAs 8-15:  V rows in registers -> transposed V^T stage v_dst (8 dims each)
+//   MFMAs 16-23: global loads of tile kt's K rows into the registers just freed
+//   MFMAs 24-31: global loads of tile vt's V rows
+template <bool FP8>
+__device__ __forceinline__ void qk_tile_staged(
+    const uint8_t* kst, int kread, const u32x4 (&qf)[16], f32x16 (&s)[2], TileRegs<FP8>& r,
+    uint8_t* k_dst, uint8_t* v_dst, int run0, int grp, int c, const int32_t* slots,
+    const uint8_t* kb, const uint8_t* vb, uint32_t lane_off, int64_t slot_bytes, int kt, int vt) {
+  u32x4 fr[kQkAhead + 1][2];
+#pragma unroll
+  for (int p = 0; p < kQkAhead; ++p)
+#pragma unroll
+    for (int hh = 0; hh < 2; ++hh) fr[p][hh] = ld_s16(kst + kread + hh * 32 * kKStride + 32 * p);
+  s[0] = f32x16{};
+  s[1] = f32x16{};
+  u32x4 sk[2], sv[2];
+  u32x4 vin[8];
+  uint8_t* const kp = k_dst + run0 * kKStride + 16 * c;
+  const int y = (grp ^ c) & 7;
+  uint8_t* const vp = v_dst + 8 * c * kVtStride;
+#pragma unroll
+  for (int i = 0; i < 32; ++i) {
+    const int kk = i >> 1, hh = i & 1;
+    __builtin_amdgcn_sched_barrier(0);
+    if (hh == 0 && kk + kQkAhead < 16) {
+#pragma unroll
+      for (int h2 = 0; h2 < 2; ++h2)
+        fr[(kk + kQkAhead) % (kQkAhead + 1)][h2] =
+            ld_s16(kst + kread + h2 * 32 * kKStride + 32 * (kk + kQkAhead));
+    }
+    s[hh] = mfma_32x32x16(fr[kk % (kQkAhead + 1)][hh], qf[kk], s[hh]);
+    if (i == 0) {
+      const int kk0 = kt * kBN + run0, vk0 = vt * kBN + run0;
+      sk[0] = *reinterpret_cast<const u32x4*>(slots + (kk0 & kSlotMask));
+      sk[1] = *reinterpret_cast<const u32x4*>(slots + ((kk0 + 8) & kSlotMask));
+      sv[0] = *reinterpret_cast<const u32x4*>(slots + (vk0 & kSlotMask));
+      sv[1] = *reinterpret_cast<const u32x4*>(slots + ((vk0 + 8) & kSlotMask));
+    }
+    if (i < 8) {
+      st_s16(kp + run_key(i) * kKStride,
+             FP8 ? e4m3x8_to_bf16x8(r.k[i][0], r.k[i][1]) : r.k[i]);
+    } else if (i < 16) {
+      const int d = i - 8;
+      if (d == 0) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) vin[j] = FP8 ? e4m3x8_to_bf16x8(r.v[j][0], r.v[j][1]) : r.v[j];
+      }
+      u32x4 o;
+#pragma unroll
+      for (int w = 0; w < 4; ++w) o[w] = pair_sel(vin[2 * w + 1][d >> 1], vin[2 * w][d >> 1], d & 1);
+      st_s16(vp + d * kVtStride + 16 * (y ^ d), o);
+    } else if (i < 24) {
+      const int j = i - 16;
+      const int64_t off = (int64_t)(j < 4 ? sk[0][j] : sk[1][j - 4]) * slot_bytes + lane_off;
+      if (FP8) {
+        const u32x2 x = ld_g8(kb + off);
+        r.k[j] = u32x4{x[0], x[1], 0u, 0u};
+      } else {
+        r.k[j] = ld_g16(kb + off);
+      }
+    } else {
+      const int j = i - 24;
+      const int64_t off = (int64_t)(j < 4 ? sv[0][j] : sv[1][j - 4]) * slot_bytes + lane_off;
+      if (FP8) {
+        const u32x2 x = ld_g8(vb + off);
+        r.v[j] = u32x4{x[0], x[1], 0u, 0u};
+      } else {
+        r.v[j] = ld_g16(vb + off);
+      }
+    }
+  }
+  __builtin_amdgcn_sched_barrier(0);
 }
 
 // Online softmax of one tile's scores (raw, unscaled) for this lane's row, in
@@ -399,53 +496,48 @@ extend_kernel(ExtendArgs a) {
   uint8_t* const vst0 = sm.vt;
   uint8_t* const vst1 = sm.vt + kVtStage;
 
-  // ---- prologue: K(0), V(0), K(1) in LDS; V(1) in registers; S(0) computed.
-  // With a single tile the unused K(1) / V(1) stages are simply never read.
+  // ---- prologue: K(0), K(1), V(0) in LDS; K(2) and V(1) in registers; S(0)
+  // computed. Tiles past the last one are stand-ins for the last tile (its
+  // slots are staged, so every load stays inside the pool) and are never read.
   SlotPrefetch spf;
   slot_load(rtt, 0, kend, tid, spf);
   slot_store(spf, 0, tid, a.pool_slots, sm.slots);
   __syncthreads();
+  const int last = n_tiles - 1;
   TileRegs<FP8> regs;
   gather_tile<FP8>(sm.slots, kb, vb, lane_off, slot_bytes, 0, run0, regs);
   store_k<FP8>(kst0, run0, c, regs);
   store_vt<FP8>(vst0, grp, c, regs);
-  if (n_tiles > 1) {
-    gather_tile<FP8>(sm.slots, kb, vb, lane_off, slot_bytes, kBN, run0, regs);
-    store_k<FP8>(kst1, run0, c, regs);
-  }
+  gather_tile<FP8>(sm.slots, kb, vb, lane_off, slot_bytes, min(1, last) * kBN, run0, regs);
+  store_k<FP8>(kst1, run0, c, regs);
+  gather_k<FP8>(sm.slots, kb, lane_off, slot_bytes, min(2, last) * kBN, run0, regs);
   __syncthreads();
 
   f32x16 sa[2];
   qk_tile(kst0, kread, qf, sa);
 
-  // One pipelined step per tile: tile j's softmax + PV, tile j + 1's QK^T,
-  // tile j + 2's gather.  Past the last tile the same steps run on the last
-  // tile's slots (already staged, so every load stays inside the pool) and
-  // their results are never read.
+  // Step j: phase A computes S^T of tile j + 1 while K(j + 2) and V(j + 1)
+  // move from registers to LDS and the loads of K(j + 3) and V(j + 2) are
+  // issued; phase B is the softmax and PV of tile j. One barrier per step.
   for (int j = 0; j < n_tiles; ++j) {
     const int odd = j & 1;
     uint8_t* const k_this = odd ? kst1 : kst0;   // K(j) stage, gets K(j + 2)
     uint8_t* const k_next = odd ? kst0 : kst1;   // K(j + 1)
     uint8_t* const v_this = odd ? vst1 : vst0;   // V(j)
-    uint8_t* const v_next = odd ? vst0 : vst1;   // V(j + 1), written now
+    uint8_t* const v_next = odd ? vst0 : vst1;   // gets V(j + 1)
 
     // Slot ids of the next 1024 keys: loaded at tile 4 of a chunk, written at
-    // tile 8, first read by the gather at tile 14.
+    // tile 8, first read by the loads issued at tile 13.
     if ((j / kTilesPerSlotChunk + 1) * kSlotChunk < kend) {
       if (j % kTilesPerSlotChunk == 4) slot_load(rtt, j / kTilesPerSlotChunk + 1, kend, tid, spf);
       if (j % kTilesPerSlotChunk == 8)
         slot_store(spf, j / kTilesPerSlotChunk + 1, tid, a.pool_slots, sm.slots);
     }
-    store_vt<FP8>(v_next, grp, c, regs);
-    gather_tile<FP8>(sm.slots, kb, vb, lane_off, slot_bytes,
-                          min(j + 2, n_tiles - 1) * kBN, run0, regs);
-
     const int k0 = j * kBN;
     if (k0 + kBN > w_full) mask_tile(sa, k0, g, limit);
     f32x16 sn[2];
-    __builtin_amdgcn_sched_barrier(0);
-    qk_tile(k_next, kread, qf, sn);
-    __builtin_amdgcn_sched_barrier(0);
+    qk_tile_staged<FP8>(k_next, kread, qf, sn, regs, k_this, v_next, run0, grp, c, sm.slots,
+                        kb, vb, lane_off, slot_bytes, min(j + 3, last), min(j + 2, last));
     float alpha;
     if (softmax_max(sa, m, l, sl2, alpha)) {
 #pragma unroll
@@ -454,7 +546,6 @@ extend_kernel(ExtendArgs a) {
     exp_pv_tile(v_this, vbo, sa, m, l, sl2, acc);
     sa[0] = sn[0];
     sa[1] = sn[1];
-    store_k<FP8>(k_this, run0, c, regs);
     __syncthreads();
   }
 
