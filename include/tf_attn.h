@@ -142,7 +142,7 @@ int32_t tf_attn_decode_merge(const void* q, int64_t q_row_stride,
  * full_attention.py:179-213.
  *
  * work: device int32 [n_work][8] from tf_attn_plan_extend(); one entry per
- * (request, kv head, tile of 128 (token, q-head) rows).
+ * (request, kv head, tile of 256 (token, q-head) rows).
  */
 int32_t tf_attn_extend(const void* q, int64_t q_row_stride,
                        const void* k_pool, const void* v_pool, int64_t pool_slots,

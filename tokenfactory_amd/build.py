@@ -10,6 +10,7 @@ import os
 import shutil
 import subprocess
 import sys
+import tempfile
 from pathlib import Path
 
 PKG_DIR = Path(__file__).resolve().parent
@@ -17,7 +18,7 @@ REPO_DIR = PKG_DIR.parent
 CSRC = PKG_DIR / "csrc"
 LIB_DIR = PKG_DIR / "_lib"
 LIB_PATH = LIB_DIR / "libtf_attn.so"
-SOURCES = ["abi.hip", "decode.hip", "extend.hip", "kv_ops.hip", "qk_prep.hip"]
+SOURCES = ["abi.hip", "decode.hip", "extend.hip", "extend_bf16.hip", "kv_ops.hip", "qk_prep.hip"]
 ARCH = "gfx950"
 
 
@@ -43,23 +44,47 @@ def compile_flags() -> list:
     ]
 
 
+# Per-file flags on top of compile_flags().  extend_bf16.hip: its builtin
+# MFMAs (S^T = K Q^T) must produce VGPR results, because the O^T accumulators
+# of its inline-assembly MFMAs occupy every AGPR.
+EXTRA_FLAGS = {"extend_bf16.hip": ["-mllvm", "--amdgpu-mfma-vgpr-form=1"]}
+
+
+def _filter_stderr(text: str) -> str:
+    # hipcc's host pass warns about the device-only target feature; keep the rest.
+    return "\n".join(ln for ln in text.splitlines() if "packed-fp32-ops" not in ln).strip()
+
+
 def build_library(verbose: bool = False) -> Path:
-    """Compile every source into one shared library; returns its path."""
+    """Compile every source (in parallel) and link one shared library; returns its path."""
     LIB_DIR.mkdir(exist_ok=True)
     tmp = LIB_PATH.with_suffix(".so.tmp")
-    cmd = [hipcc_path(), *compile_flags(), "-shared", "-o", str(tmp),
-           *[str(CSRC / s) for s in SOURCES]]
-    if verbose:
-        print(" ".join(cmd), flush=True)
-    res = subprocess.run(cmd, capture_output=True, text=True)
-    if res.returncode != 0:
-        raise RuntimeError(f"hipcc failed ({res.returncode}):\n{res.stdout}\n{res.stderr}")
-    if verbose and res.stderr.strip():
-        # hipcc's host pass warns about the device-only target feature; show
-        # anything else.
-        lines = [ln for ln in res.stderr.splitlines() if "packed-fp32-ops" not in ln]
-        if any(ln.strip() for ln in lines):
-            print("\n".join(lines), file=sys.stderr)
+    with tempfile.TemporaryDirectory(prefix="tf_attn_build_") as objdir:
+        procs = []
+        for src in SOURCES:
+            obj = Path(objdir) / (Path(src).stem + ".o")
+            cmd = [hipcc_path(), *compile_flags(), *EXTRA_FLAGS.get(src, []), "-c",
+                   str(CSRC / src), "-o", str(obj)]
+            if verbose:
+                print(" ".join(cmd), flush=True)
+            procs.append((src, obj, subprocess.Popen(cmd, stdout=subprocess.PIPE,
+                                                     stderr=subprocess.PIPE, text=True)))
+        objs, failures = [], []
+        for src, obj, proc in procs:
+            out, err = proc.communicate()
+            if proc.returncode != 0:
+                failures.append(f"{src}: hipcc failed ({proc.returncode}):\n{out}\n{err}")
+            elif verbose and _filter_stderr(err):
+                print(_filter_stderr(err), file=sys.stderr)
+            objs.append(str(obj))
+        if failures:
+            raise RuntimeError("\n".join(failures))
+        cmd = [hipcc_path(), f"--offload-arch={ARCH}", "-shared", "-o", str(tmp), *objs]
+        if verbose:
+            print(" ".join(cmd), flush=True)
+        res = subprocess.run(cmd, capture_output=True, text=True)
+        if res.returncode != 0:
+            raise RuntimeError(f"link failed ({res.returncode}):\n{res.stdout}\n{res.stderr}")
     os.replace(tmp, LIB_PATH)
     return LIB_PATH
 

@@ -62,7 +62,7 @@ int32_t tf_attn_plan_decode_items(const int64_t* extend_lens, int32_t batch_size
   return n;
 }
 
-// Extend tiles hold 128 flattened (token, q-head-of-group) rows; see extend.hip.
+// Extend items hold kExtendItemRows flattened (token, q-head-of-group) rows.
 int32_t tf_attn_plan_extend(const int64_t* extend_lens, int32_t batch_size,
                             int32_t num_q_heads, int32_t num_kv_heads,
                             int32_t decode_to_decode_kernel, int32_t* work,
@@ -73,7 +73,7 @@ int32_t tf_attn_plan_extend(const int64_t* extend_lens, int32_t batch_size,
   if (num_kv_heads <= 0 || num_q_heads <= 0 || num_q_heads % num_kv_heads)
     return tfa::fail(TF_ERR_INVALID, "plan_extend: heads %d/%d", num_q_heads, num_kv_heads);
   const int64_t group = num_q_heads / num_kv_heads;
-  const int64_t tile_rows = 128;
+  const int64_t tile_rows = tfa::kExtendItemRows;
 
   std::vector<int64_t> q_start(batch_size);
   std::vector<int32_t> order;

@@ -1,4 +1,5 @@
-// Causal prefill / extend attention over cached prefix + new tokens (bf16 MFMA).
+// Causal prefill / extend attention over an fp8-e4m3 KV pool (bf16 MFMA), and
+// the tf_attn_extend entry point (bf16 pools run extend_bf16.hip's kernel).
 //
 // Replaces the reference's extend / mixed branch (qwen3_8/full_attention.py:244-283)
 // and the ext_len > 1 case of its bsz == 1 branch (:179-213).  The reference
@@ -8,15 +9,17 @@
 //
 // Work item (from tf_attn_plan_extend): (request b, kv head hk, row0).  The
 // rows of a (b, hk) pair are the ext_b * G flattened (token t, q head h) pairs
-// of the kv head's q-head group, row = t * G + h; an item covers 128 of them
-// (32 per wave), so all G heads of a GQA group share every K/V tile.
+// of the kv head's q-head group, row = t * G + h; an item covers 256 of them
+// and runs as two workgroups of 128 rows (32 per wave), so all G heads of a
+// GQA group share every K/V tile.
 // Row (t, h) attends to context positions 0 .. P + t, P = L - ext.
 //
 // Each wave computes, per 64-key tile j, with v_mfma_f32_32x32x16_bf16:
 //   S^T[key, row] = K Q^T        (Q^T register-resident, K from LDS)
 //   online softmax of S^T        (a row's 64 scores live in lanes n and n + 32)
 //   O^T[dim, row] += V^T P^T     (V^T from LDS, P^T packed straight from S^T)
-// so each lane owns one row: its max, sum and 128 of its output dims.
+// so each lane owns one row: its max, sum and 128 of its output dims.  The
+// e4m3 rows are widened to bf16 (exactly) on their way into LDS.
 //
 // Software pipeline (one barrier per tile, no wave-dependent branches around
 // the accumulator so it stays in AGPRs):
@@ -47,6 +50,7 @@ constexpr int kD = 256;
 constexpr int kWaves = 4;
 constexpr int kThreads = kWaves * kWave;
 constexpr int kRowsPerWave = 32;
+static_assert(2 * kWaves * kRowsPerWave == kExtendItemRows, "two workgroups per item");
 constexpr int kBN = 64;                         // keys per tile
 constexpr int kKStride = 2 * kD + 16;           // bytes per K row in LDS (padded)
 constexpr int kKStage = kBN * kKStride;         // 33792
@@ -57,25 +61,6 @@ constexpr int kSlotMask = 2 * kSlotChunk - 1;
 constexpr int kTilesPerSlotChunk = kSlotChunk / kBN;
 constexpr float kRescaleLog2 = 8.f;             // lazy-rescale threshold (log2 units)
 
-struct ExtendArgs {
-  const __bf16* q;
-  int64_t q_stride;
-  const uint8_t* k_pool;
-  const uint8_t* v_pool;
-  int64_t pool_slots;
-  const float* k_scale;
-  const float* v_scale;
-  const int64_t* rtt;
-  int64_t rtt_rows, rtt_stride, rtt_cols;
-  const int64_t* rpi;
-  const int64_t* seq_lens;
-  int32_t seq_override;
-  const int32_t* work;
-  int32_t hkv, group;
-  float scale_log2;
-  __bf16* out;
-  int64_t out_stride;
-};
 
 struct __attribute__((aligned(16))) ExtendSmem {
   uint8_t k[2 * kKStage];          // 66 KB
@@ -415,10 +400,11 @@ extend_kernel(ExtendArgs a) {
   const int g = lane >> 5;
   const int n = lane & 31;
 
-  const int32_t* wk = a.work + 8 * (int64_t)blockIdx.x;
+  // Two workgroups per 256-row work item, 128 rows each.
+  const int32_t* wk = a.work + 8 * (int64_t)(blockIdx.x >> 1);
   const int b = wk[0];
   const int hk = wk[1];
-  const int row0 = wk[2];
+  const int row0 = wk[2] + kWaves * kRowsPerWave * (int)(blockIdx.x & 1);
   const int q_start = wk[3];
   const int ext = wk[4];
   const int G = a.group;
@@ -428,7 +414,7 @@ extend_kernel(ExtendArgs a) {
   const int L = (int)len;
   const int P = L - ext;
   const int rows_total = ext * G;
-  if (L <= 0) return;
+  if (L <= 0 || row0 >= rows_total) return;
 
   const int64_t rrow = clamp_i64(a.rpi[b], 0, a.rtt_rows - 1);
   const int64_t* rtt = a.rtt + rrow * a.rtt_stride;
@@ -627,8 +613,8 @@ extern "C" int32_t tf_attn_extend(const void* q, int64_t q_row_stride, const voi
 
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   if (kv_dtype == TF_DTYPE_FP8_E4M3)
-    hipLaunchKernelGGL(extend_kernel<true>, dim3((unsigned)n_work), dim3(kThreads), 0, s, a);
+    hipLaunchKernelGGL(extend_kernel<true>, dim3(2u * (unsigned)n_work), dim3(kThreads), 0, s, a);
   else
-    hipLaunchKernelGGL(extend_kernel<false>, dim3((unsigned)n_work), dim3(kThreads), 0, s, a);
+    launch_extend_bf16(a, n_work, s);
   return launch_status("tf_attn_extend launch");
 }

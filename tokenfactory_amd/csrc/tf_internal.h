@@ -30,4 +30,29 @@ int make_decode_plan(int32_t n_items, int32_t num_q_heads, int32_t num_kv_heads,
                      int32_t head_dim, int32_t max_seq_len, int32_t num_workgroups,
                      DecodePlan* plan);
 
+// Extend kernel arguments (validated by tf_attn_extend).  Work items cover
+// kExtendItemRows flattened (token, q-head-of-group) rows each.
+constexpr int kExtendItemRows = 256;
+struct ExtendArgs {
+  const __bf16* q;
+  int64_t q_stride;
+  const uint8_t* k_pool;
+  const uint8_t* v_pool;
+  int64_t pool_slots;
+  const float* k_scale;
+  const float* v_scale;
+  const int64_t* rtt;
+  int64_t rtt_rows, rtt_stride, rtt_cols;
+  const int64_t* rpi;
+  const int64_t* seq_lens;
+  int32_t seq_override;
+  const int32_t* work;
+  int32_t hkv, group;
+  float scale_log2;
+  __bf16* out;
+  int64_t out_stride;
+};
+// bf16 pool: one 256-thread workgroup per work item (extend_bf16.hip).
+void launch_extend_bf16(const ExtendArgs& a, int32_t n_work, hipStream_t stream);
+
 }  // namespace tfa

@@ -12,7 +12,7 @@ import numpy as np
 
 from . import _native
 
-EXTEND_TILE_ROWS = 128   # (token, q-head) rows per extend work item
+EXTEND_TILE_ROWS = 256   # (token, q-head) rows per extend work item
 WORK_FIELDS = 8          # int32 fields per extend work item
 
 
