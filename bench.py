@@ -119,8 +119,10 @@ def bench_extend(torch, workloads, SlotAttentionCall, args):
     log("building extend_prefix (16 requests, 4 radix groups)")
     wl = workloads.extend_prefix(device="cuda")
     call = SlotAttentionCall(wl.q, wl.k_pool, wl.v_pool, wl.batch, scaling=wl.scale)
-    steps = max(3, args.steps // 5)
-    ms = time_steps(torch, [call], steps, max(1, args.warmup // 5), lambda c: [c.run])
+    # About 2 ms per step: half the step count, and the full warm-up so that
+    # the clocks have settled (MFMA-heavy launches ramp over the first ~20 ms).
+    steps = max(3, args.steps // 2)
+    ms = time_steps(torch, [call], steps, max(1, args.warmup), lambda c: [c.run])
     k_ms = time_kernel(torch, [call], steps, lambda c: c.run_extend())
     flops = wl.extend_flops()
     tf = flops / (k_ms * 1e-3)
@@ -133,15 +135,17 @@ def bench_extend(torch, workloads, SlotAttentionCall, args):
             "steps": steps, "flops_per_step": flops, "kernel_ms": k_ms,
             "roofline": {"bound": "mfma", "achieved": tf / 1e12, "peak": MFMA_BF16_PEAK / 1e12,
                          "unit": "TFLOP/s", "frac": tf / MFMA_BF16_PEAK,
-                         "kernel": "extend_kernel<bf16>"}}
+                         "kernel": "extend_bf16_kernel"}}
 
 
 def bench_mixed(torch, workloads, SlotAttentionCall, args):
     log("building mixed (4 x 2k extend + 128 decode, 2M-slot pool)")
     wl = workloads.mixed(device="cuda")
     call = SlotAttentionCall(wl.q, wl.k_pool, wl.v_pool, wl.batch, scaling=wl.scale)
-    steps = max(3, args.steps // 5)
-    ms = time_steps(torch, [call], steps, max(1, args.warmup // 5), lambda c: [c.run])
+    # About 2 ms per step: half the step count, and the full warm-up so that
+    # the clocks have settled (MFMA-heavy launches ramp over the first ~20 ms).
+    steps = max(3, args.steps // 2)
+    ms = time_steps(torch, [call], steps, max(1, args.warmup), lambda c: [c.run])
     ph = {"extend": time_kernel(torch, [call], steps, lambda c: c.run_extend()),
           "decode": time_kernel(torch, [call], steps, lambda c: c.run_decode_partial())}
     flops, nbytes = wl.extend_flops(), wl.decode_bytes()

@@ -585,6 +585,8 @@ extern "C" int32_t tf_attn_extend(const void* q, int64_t q_row_stride, const voi
   if (!aligned16(q) || !aligned16(out) || !aligned16(k_pool) || !aligned16(v_pool) ||
       (q_row_stride * 2) % 16 || (out_row_stride * 2) % 16 || !aligned16(work))
     return fail(TF_ERR_INVALID, "extend: q/out/pools/work must be 16-byte aligned");
+  if ((int64_t)num_kv_heads * head_dim * 2 > INT32_MAX)
+    return fail(TF_ERR_INVALID, "extend: num_kv_heads=%d too large", num_kv_heads);
   if (q_row_stride < (int64_t)num_q_heads * head_dim ||
       out_row_stride < (int64_t)num_q_heads * head_dim)
     return fail(TF_ERR_INVALID, "extend: row stride smaller than num_q_heads*head_dim");

@@ -25,9 +25,11 @@
 //
 // Staging: K and V rows go from global memory straight into LDS
 // (global_load_lds_dwordx4, 1 KB = two keys per instruction, 4 + 4 per wave
-// per tile), three stages each, issued two tiles ahead and spread one
-// instruction per QK^T MFMA; one barrier per tile.  Slot ids reach LDS the same
-// way, 1024 keys at a time (the low dword of each req_to_token entry).
+// per tile) two tiles ahead, into 3 K stages and 4 V stages (V is read one
+// tile later than K), one pair per QK^T MFMA; one barrier per tile.  Slot ids
+// reach LDS the same way, 1024 keys at a time (the low dword of each
+// req_to_token entry).  Each tile's softmax runs beside the neighbouring
+// tiles' MFMAs (see "one step" below).
 // The running max is raised lazily: the accumulators are rescaled only when a
 // row's max grows by more than 2^8 (exact in exact arithmetic; p <= 2^8).
 #include <math.h>
@@ -59,8 +61,9 @@ constexpr int kKStage = (kBN / 2) * kKPair;          // 16896
 // vswz(n) = 10 (n & 1) + 4 ((n >> 1) & 1), which makes every transposing read
 // (4 keys x 64 B per 32 lanes) conflict-free.
 constexpr int kVStage = kBN * kRowBytes;             // 16384
-constexpr int kStages = 3;                           // K stages
-constexpr int kVStages = 4;                          // V stages (read one tile later)
+constexpr int kAhead = 2;                            // tiles staged ahead of QK^T
+constexpr int kStages = kAhead + 1;                  // K stages
+constexpr int kVStages = kAhead + 2;                 // V stages (read one tile later)
 constexpr int kSlotChunk = 1024;
 constexpr int kSlotMask = 2 * kSlotChunk - 1;
 constexpr int kTilesPerSlotChunk = kSlotChunk / kBN;
@@ -69,8 +72,8 @@ constexpr int kQkAhead = 4;                          // K fragments in flight
 constexpr int kPvAhead = 4;                          // V fragments in flight
 
 struct __attribute__((aligned(16))) Smem {
-  uint8_t k[kStages * kKStage];    // 49.5 KB
-  uint8_t v[kVStages * kVStage];   // 64 KB
+  uint8_t k[kStages * kKStage];
+  uint8_t v[kVStages * kVStage];
   int32_t slots[2 * kSlotChunk];   // 8 KB: key k's slot id at slots[k % 2048]
 };
 
@@ -93,6 +96,16 @@ __device__ __forceinline__ void dma16(const void* gptr, uint32_t lds) {
                :: "v"(gptr), "s"(lds) : "m0");
 }
 
+// End of step j: tile j + 1 (issued at step j + 1 - kAhead) must have landed;
+// the 8 loads per tile of the newer kAhead - 1 tiles may still be in flight.
+__device__ __forceinline__ void vm_wait_staged() {
+  static_assert(kAhead == 2 || kAhead == 3, "vmcnt immediates");
+  if (kAhead == 2)
+    asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
+  else
+    asm volatile("s_waitcnt vmcnt(16)" ::: "memory");
+}
+
 // Slot ids of keys [chunk * 1024, +1024) clamped to [0, kend): wave w moves
 // 256 of them (4 dword instructions) into slot-buffer half chunk & 1.
 __device__ __forceinline__ void slot_issue(const int64_t* rtt, int chunk, int kend, int w,
@@ -112,19 +125,30 @@ __device__ __forceinline__ int32_t stage_slot(const int32_t* slots, int tile, in
   return slots[(tile * kBN + 8 * w + 2 * p + g) & kSlotMask];
 }
 
-__device__ __forceinline__ void k_issue(const uint8_t* kb, int64_t slot_bytes, int32_t slot,
-                                        int32_t smax, int w, int lane, int p, uint8_t* kst) {
+// Per-lane global bases: lane l loads 16-byte chunk (l % 32) ^ (key & 1) of a
+// K row and chunk (l % 32) ^ vswz(key) of a V row; key & 1 = l / 32 and
+// vswz(key) = 10 (l / 32) + 4 (p & 1) for instruction p.
+struct StageBases {
+  const uint8_t* k;
+  const uint8_t* v[2];   // by p & 1
+};
+
+__device__ __forceinline__ StageBases stage_bases(const uint8_t* kb, const uint8_t* vb, int lane) {
   const int pos = lane & 31, g = lane >> 5;
-  slot = min(max(slot, 0), smax);
-  dma16(kb + (int64_t)slot * slot_bytes + 16 * (pos ^ g), lds_addr(kst + (4 * w + p) * kKPair));
+  StageBases sb;
+  sb.k = kb + 16 * (pos ^ g);
+  sb.v[0] = vb + 16 * (pos ^ (10 * g));
+  sb.v[1] = vb + 16 * (pos ^ (10 * g + 4));
+  return sb;
 }
 
-__device__ __forceinline__ void v_issue(const uint8_t* vb, int64_t slot_bytes, int32_t slot,
-                                        int32_t smax, int w, int lane, int p, uint8_t* vst) {
-  const int pos = lane & 31, g = lane >> 5;
-  const int c = pos ^ (10 * g + 4 * (p & 1));   // vswz(8w + 2p + g)
-  slot = min(max(slot, 0), smax);
-  dma16(vb + (int64_t)slot * slot_bytes + 16 * c, lds_addr(vst + (8 * w + 2 * p) * kRowBytes));
+// Row `slot` (clamped into the pool) of K and V: one 32 x 32 -> 64-bit
+// multiply-add per address (slot ids and the slot stride fit 32 bits).
+__device__ __forceinline__ void kv_issue(const StageBases& sb, uint32_t slot_bytes, int32_t slot,
+                                         int32_t smax, int w, int p, uint8_t* kst, uint8_t* vst) {
+  const uint64_t off = (uint64_t)(uint32_t)min(max(slot, 0), smax) * slot_bytes;
+  dma16(sb.k + off, lds_addr(kst + (4 * w + p) * kKPair));
+  dma16(sb.v[p & 1] + off, lds_addr(vst + (8 * w + 2 * p) * kRowBytes));
 }
 
 // ---------------------------------------------------------------- MFMAs
@@ -209,7 +233,7 @@ __device__ __forceinline__ float half_swap_max(float v) {
 // Step j runs three tiles at once, each phase one MFMA stream with the other
 // work placed one item per MFMA (sched_barrier regions):
 //   phase A: S^T(j) = K(j) Q^T (32 MFMAs) | staging of tile j + 2 (slot ids at
-//            MFMA 0, K rows 4-7, V rows 8-11) | second-half exps of tile j - 1
+//            MFMA 0, K and V rows 4-7) | second-half exps of tile j - 1
 //            (MFMAs 12-27);
 //   phase B: O^T += V(j - 1)^T P^T(j - 1) (32 MFMAs) | row max of tile j
 //            (MFMAs 0-7, lane-half swap 8, reference update 9) | first-half
@@ -220,10 +244,10 @@ __device__ __forceinline__ float half_swap_max(float v) {
 template <bool kQk, bool kExp>
 __device__ __forceinline__ void phase_a(const uint8_t* kst, int kaddr, const u32x4 (&qf)[2][16],
                                         f32x16 (&s)[2], const int32_t* slots, int tile2, int w,
-                                        int lane, int32_t smax, const uint8_t* kb,
-                                        const uint8_t* vb, int64_t slot_bytes, uint8_t* k_dst,
-                                        uint8_t* v_dst, const float (&sh)[2][8], Rows& rows,
-                                        float sl2, u32x4 (&pt)[2][2]) {
+                                        int lane, int32_t smax, const StageBases& sb,
+                                        uint32_t slot_bytes, uint8_t* k_dst, uint8_t* v_dst,
+                                        const float (&sh)[2][8], Rows& rows, float sl2,
+                                        u32x4 (&pt)[2][2]) {
   auto kread = [&](int kk) { return ld_s16(kst + kaddr + 32 * kk); };
   u32x4 fr[kQkAhead + 1];
   if (kQk) {
@@ -235,7 +259,11 @@ __device__ __forceinline__ void phase_a(const uint8_t* kst, int kaddr, const u32
 #pragma unroll
   for (int i = 0; i < 32; ++i) {
     const int kk = i >> 1, rb = i & 1;
+    // One region per MFMA: the MFMA issues first, this region's other work
+    // follows it and overlaps its 32 cycles.
     __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+    __builtin_amdgcn_sched_group_barrier(0x7f7, 64, 0);
     if (kQk) {
       if (rb == 0 && kk + kQkAhead < 16) fr[(kk + kQkAhead) % (kQkAhead + 1)] = kread(kk + kQkAhead);
       s[rb] = mfma_32x32x16(fr[kk % (kQkAhead + 1)], qf[rb][kk], kk == 0 ? f32x16{} : s[rb]);
@@ -243,9 +271,7 @@ __device__ __forceinline__ void phase_a(const uint8_t* kst, int kaddr, const u32
 #pragma unroll
         for (int q = 0; q < 4; ++q) ss[q] = stage_slot(slots, tile2, w, lane >> 5, q);
       } else if (i >= 4 && i < 8) {
-        k_issue(kb, slot_bytes, ss[i - 4], smax, w, lane, i - 4, k_dst);
-      } else if (i >= 8 && i < 12) {
-        v_issue(vb, slot_bytes, ss[i - 8], smax, w, lane, i - 8, v_dst);
+        kv_issue(sb, slot_bytes, ss[i - 4], smax, w, i - 4, k_dst, v_dst);
       }
     }
     if (!kExp) continue;
@@ -254,9 +280,9 @@ __device__ __forceinline__ void phase_a(const uint8_t* kst, int kaddr, const u32
       // soon as it is complete.
       const int e = i - 12, eb = e & 1, r = e >> 1;
       p[eb][r] = fast_exp2(fmaf(sh[eb][r], sl2, -rows.moff[eb]));
-      rows.l[eb] += p[eb][r];
       if (r & 1) {
         pt[eb][1][r >> 1] = pack_bf16(p[eb][r - 1], p[eb][r]);
+        rows.l[eb] += p[eb][r - 1] + p[eb][r];
         // Pin the result here: otherwise it is sunk past the rescale branch
         // into phase B's block, where it would run ahead of the PV MFMAs.
         asm volatile("" : "+v"(pt[eb][1][r >> 1]));
@@ -285,7 +311,9 @@ __device__ __forceinline__ void phase_b(const uint8_t* vst, const int (&vaddr)[4
 #pragma unroll
   for (int i = 0; i < 32; ++i) {
     const int f = i >> 1, rb = i & 1;
-    __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_sched_barrier(0);   // MFMA first, as in phase_a
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+    __builtin_amdgcn_sched_group_barrier(0x7f7, 64, 0);
     if (kPv) {
       if (rb == 0 && f + kPvAhead < 16)
         fr[(f + kPvAhead) % (kPvAhead + 1)] = v_frag(vst, vaddr, f + kPvAhead);
@@ -305,23 +333,26 @@ __device__ __forceinline__ void phase_b(const uint8_t* vst, const int (&vaddr)[4
 #pragma unroll
         for (int mb = 0; mb < 2; ++mb) mx[mb] = half_swap_max(mx[mb]);
       } else if (i == 9) {
-        // Lazy reference max: raised only when some row of the wave outgrew it
-        // by more than 2^kRescaleLog2 (exact in exact arithmetic; p <= 2^8).
+        // Lazy reference max, per row: raised only when the row outgrew it by
+        // more than 2^kRescaleLog2 (exact in exact arithmetic; p <= 2^8).  The
+        // wave-wide vote only decides whether the rescale runs at all.
 #pragma unroll
         for (int mb = 0; mb < 2; ++mb) {
           const bool grow = (mx[mb] - rows.m[mb]) * sl2 > kRescaleLog2;
-          grew[mb] = __ballot(grow) != 0;
-          const float mnew = grew[mb] ? fmaxf(rows.m[mb], mx[mb]) : rows.m[mb];
-          alpha[mb] = grew[mb] ? fast_exp2((rows.m[mb] - mnew) * sl2) : 1.f;
+          const float mnew = grow ? mx[mb] : rows.m[mb];
+          alpha[mb] = grow ? fast_exp2((rows.m[mb] - mnew) * sl2) : 1.f;
           rows.l[mb] *= alpha[mb];
           rows.m[mb] = mnew;
           rows.moff[mb] = mnew * sl2;
+          grew[mb] = __ballot(grow) != 0;
         }
       } else if (i >= 10 && i < 26) {
         const int e = i - 10, eb = e & 1, r = e >> 1;
         p[eb][r] = fast_exp2(fmaf(s[eb][r], sl2, -rows.moff[eb]));
-        rows.l[eb] += p[eb][r];
-        if (r & 1) p_pair[eb][r >> 1] = pack_bf16(p[eb][r - 1], p[eb][r]);
+        if (r & 1) {
+          p_pair[eb][r >> 1] = pack_bf16(p[eb][r - 1], p[eb][r]);
+          rows.l[eb] += p[eb][r - 1] + p[eb][r];
+        }
       } else if (i == 26) {
 #pragma unroll
         for (int b2 = 0; b2 < 2; ++b2) {
@@ -392,12 +423,12 @@ __global__ void __launch_bounds__(kThreads) extend_bf16_kernel(ExtendArgs a) {
   const int w_full = w_first < rows_total ? P + w_first / G + 1 : 0;
 
   const float sl2 = a.scale_log2;
-  const int64_t slot_bytes = (int64_t)a.hkv * kRowBytes;
-  const uint8_t* kb = a.k_pool + (int64_t)hk * kRowBytes;
-  const uint8_t* vb = a.v_pool + (int64_t)hk * kRowBytes;
+  const uint32_t slot_bytes = (uint32_t)a.hkv * kRowBytes;
+  const StageBases sb = stage_bases(a.k_pool + (int64_t)hk * kRowBytes,
+                                    a.v_pool + (int64_t)hk * kRowBytes, lane);
   const int32_t smax = (int32_t)min(a.pool_slots - 1, (int64_t)INT32_MAX);
 
-  // LDS read offsets of this lane (see k_issue / v_frag).
+  // LDS read offsets of this lane (see kv_issue / v_frag).
   const int kaddr = (n >> 1) * kKPair + (n & 1) * kRowBytes + 16 * (g ^ (n & 1));
   int vaddr[4];
   {
@@ -448,16 +479,15 @@ __global__ void __launch_bounds__(kThreads) extend_bf16_kernel(ExtendArgs a) {
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
 #pragma unroll
-  for (int tl = 0; tl < 2; ++tl) {
+  for (int tl = 0; tl < kAhead; ++tl) {
     const int tile = min(tl, last);
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
-      const int32_t slot = stage_slot(sm.slots, tile, w, g, q);
-      k_issue(kb, slot_bytes, slot, smax, w, lane, q, sm.k + tl * kKStage);
-      v_issue(vb, slot_bytes, slot, smax, w, lane, q, sm.v + tl * kVStage);
+      kv_issue(sb, slot_bytes, stage_slot(sm.slots, tile, w, g, q), smax, w, q,
+               sm.k + tl * kKStage, sm.v + tl * kVStage);
     }
   }
-  asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
+  vm_wait_staged();
   __syncthreads();
 
   // K tile t lives in K stage t % 3, V tile t in V stage t % 4. Step j stages
@@ -487,13 +517,14 @@ __global__ void __launch_bounds__(kThreads) extend_bf16_kernel(ExtendArgs a) {
   auto step_end = [&]() {
     // Tile j + 1 was issued one step earlier: only this step's 8 tile loads
     // may still be in flight.
-    asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
+    vm_wait_staged();
     __syncthreads();
   };
 
   // Step 0: S^T(0) and the max / first-half exps of tile 0 (no PV yet).
-  phase_a<true, false>(sm.k, kaddr, qf, s, sm.slots, min(2, last), w, lane, smax, kb, vb, slot_bytes,
-                sm.k + 2 * kKStage, sm.v + 2 * kVStage, sh, rows, sl2, pt);
+  phase_a<true, false>(sm.k, kaddr, qf, s, sm.slots, min(kAhead, last), w, lane, smax, sb,
+                       slot_bytes, sm.k + kAhead * kKStage, sm.v + kAhead * kVStage, sh, rows,
+                       sl2, pt);
   if (kBN > w_full) {
 #pragma unroll
     for (int rb = 0; rb < 2; ++rb) mask_tile(s[rb], 0, g, limit[rb]);
@@ -507,11 +538,11 @@ __global__ void __launch_bounds__(kThreads) extend_bf16_kernel(ExtendArgs a) {
     // at step 32 c - 3), first read when tile 32 (c + 1) is staged.
     if (j % kTilesPerSlotChunk == 4 && (j / kTilesPerSlotChunk + 1) * kSlotChunk < kend)
       slot_issue(rtt, j / kTilesPerSlotChunk + 1, kend, w, lane, sm.slots);
-    const int kst = j % kStages, kst2 = (j + 2) % kStages;
-    const int vst = (j - 1) % kVStages, vst2 = (j + 2) % kVStages;
+    const int kst = j % kStages, kst2 = (j + kAhead) % kStages;
+    const int vst = (j - 1) % kVStages, vst2 = (j + kAhead) % kVStages;
 
-    phase_a<true, true>(sm.k + kst * kKStage, kaddr, qf, s, sm.slots, min(j + 2, last), w, lane, smax,
-                  kb, vb, slot_bytes, sm.k + kst2 * kKStage, sm.v + vst2 * kVStage, sh, rows, sl2,
+    phase_a<true, true>(sm.k + kst * kKStage, kaddr, qf, s, sm.slots, min(j + kAhead, last), w, lane,
+                        smax, sb, slot_bytes, sm.k + kst2 * kKStage, sm.v + vst2 * kVStage, sh, rows, sl2,
                   pt);
     const int k0 = j * kBN;
     if (k0 + kBN > w_full) {
@@ -524,7 +555,7 @@ __global__ void __launch_bounds__(kThreads) extend_bf16_kernel(ExtendArgs a) {
   }
 
   // Tail: second-half exps and PV of the last tile.
-  phase_a<false, true>(sm.k, kaddr, qf, s, sm.slots, 0, w, lane, smax, kb, vb, slot_bytes, sm.k, sm.v,
+  phase_a<false, true>(sm.k, kaddr, qf, s, sm.slots, 0, w, lane, smax, sb, slot_bytes, sm.k, sm.v,
                  sh, rows, sl2, pt);
   rescale();
   phase_b<true, false>(sm.v + (last % kVStages) * kVStage, vaddr, acc, s, rows, sl2, pt, sh,
