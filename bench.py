@@ -44,7 +44,7 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--only", default="decode,extend,mixed,fp8,prep",
+    ap.add_argument("--only", default="decode,extend,mixed,fp8,prep,gate",
                     help="comma list of decode,extend,mixed,fp8,prep,copy")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--workgroups", type=int, default=0,
@@ -222,6 +222,34 @@ def bench_prep(torch, args):
                          "kernel": "qk_prep_kernel"}}
 
 
+def bench_gate(torch, workloads, SlotAttentionCall, args):
+    """The module's output gate ``attn * F.silu(gate)`` (full_attention.py:157-159)
+    over the extend_prefix step: fused into the extend kernel's output write
+    against the reference's two PyTorch ops after an ungated kernel."""
+    import torch.nn.functional as F
+    wl = workloads.extend_prefix(device="cuda")
+    T, H, D = wl.q.shape
+    g = torch.Generator(device="cuda").manual_seed(29)
+    qg = torch.randn((T, H, 2 * D), device="cuda", generator=g).to(torch.bfloat16)
+    gate = qg[..., D:]
+    plain = SlotAttentionCall(wl.q, wl.k_pool, wl.v_pool, wl.batch, scaling=wl.scale)
+    gated = SlotAttentionCall(wl.q, wl.k_pool, wl.v_pool, wl.batch, scaling=wl.scale, gate=gate)
+    steps = max(3, args.steps // 2)
+    for c in (plain, gated):
+        time_steps(torch, [c], 2, max(1, args.warmup), lambda x: [x.run_extend])
+    k_plain = time_kernel(torch, [plain], steps, lambda c: c.run_extend())
+    k_gated = time_kernel(torch, [gated], steps, lambda c: c.run_extend())
+    attn = plain.out
+    ops = lambda: attn.reshape(T, H * D) * F.silu(gate.reshape(T, H * D))
+    ops_ms = time_steps(torch, [None], steps, max(1, args.warmup), lambda c: [ops])
+    log(f"output gate over extend_prefix: fused +{(k_gated-k_plain)*1e3:.1f} us in the extend "
+        f"kernel ({k_plain*1e3:.1f} -> {k_gated*1e3:.1f} us); reference ops {ops_ms*1e3:.1f} us")
+    return {"workload": "attn * silu(gate) on the extend_prefix step (20k tokens x 24 heads x "
+                        "256, bf16; gate = strided view of the q projection)",
+            "extend_kernel_ms": k_plain, "extend_kernel_gated_ms": k_gated,
+            "fused_cost_ms": k_gated - k_plain, "reference_ops_ms": ops_ms}
+
+
 def bench_copy(torch, args):
     """A plain device copy of known size, the reference point for HBM counters."""
     n = 1 << 30
@@ -304,6 +332,8 @@ def main():
         torch.cuda.empty_cache()
     if "prep" in only:
         secondary["qk_prep_20k"] = bench_prep(torch, args)
+    if "gate" in only:
+        secondary["output_gate"] = bench_gate(torch, workloads, SlotAttentionCall, args)
         torch.cuda.empty_cache()
     if dec is None:
         print(json.dumps({"metric": METRIC, "value": None, "secondary": secondary},

@@ -85,6 +85,14 @@ const char* tf_attn_last_error(void);
  * max_seq_len: an upper bound of every L_b processed (host int, as
  * ForwardBatch.max_seq_len); kept for the caller's bookkeeping.
  *
+ * gate (optional, NULL = none): bf16 output gate, element (row, head, dim) at
+ * gate + row * gate_row_stride + head * gate_head_stride + dim (16-byte aligned,
+ * strides multiples of 8 elements).  With a gate the kernels write
+ * bf16(bf16(attn) * bf16(silu(gate))), the module's
+ * `attn_output * F.silu(gate)` (full_attention.py:157-159) fused into the
+ * output write; the gate of the reference is the second half of each head's
+ * q projection, so a strided view of it is passed as is.
+ *
  * tf_attn_decode runs both phases.  tf_attn_decode_partial runs the
  * HBM-streaming split kernel only (requests that fit one split get their final
  * output, the others leave partials in the workspace); tf_attn_decode_merge then
@@ -107,7 +115,9 @@ int32_t tf_attn_decode(const void* q, int64_t q_row_stride,
                        int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
                        float scale, void* out, int64_t out_row_stride,
                        void* workspace, int64_t workspace_bytes,
-                       int32_t max_seq_len, int32_t num_workgroups, tf_stream_t stream);
+                       int32_t max_seq_len, int32_t num_workgroups,
+                       const void* gate, int64_t gate_row_stride, int64_t gate_head_stride,
+                       tf_stream_t stream);
 
 int32_t tf_attn_decode_partial(const void* q, int64_t q_row_stride,
                                const void* k_pool, const void* v_pool, int64_t pool_slots,
@@ -120,7 +130,9 @@ int32_t tf_attn_decode_partial(const void* q, int64_t q_row_stride,
                                int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
                                float scale, void* out, int64_t out_row_stride,
                                void* workspace, int64_t workspace_bytes,
-                               int32_t max_seq_len, int32_t num_workgroups, tf_stream_t stream);
+                               int32_t max_seq_len, int32_t num_workgroups,
+                               const void* gate, int64_t gate_row_stride, int64_t gate_head_stride,
+                               tf_stream_t stream);
 
 int32_t tf_attn_decode_merge(const void* q, int64_t q_row_stride,
                              const void* k_pool, const void* v_pool, int64_t pool_slots,
@@ -133,7 +145,9 @@ int32_t tf_attn_decode_merge(const void* q, int64_t q_row_stride,
                              int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
                              float scale, void* out, int64_t out_row_stride,
                              void* workspace, int64_t workspace_bytes,
-                             int32_t max_seq_len, int32_t num_workgroups, tf_stream_t stream);
+                             int32_t max_seq_len, int32_t num_workgroups,
+                             const void* gate, int64_t gate_row_stride, int64_t gate_head_stride,
+                             tf_stream_t stream);
 
 /* ------------------------------------------------------------------ extend
  * Causal prefill / extend attention over cached prefix + new tokens, bf16
@@ -143,6 +157,7 @@ int32_t tf_attn_decode_merge(const void* q, int64_t q_row_stride,
  *
  * work: device int32 [n_work][8] from tf_attn_plan_extend(); one entry per
  * (request, kv head, tile of 256 (token, q-head) rows).
+ * gate: optional output gate, as for tf_attn_decode.
  */
 int32_t tf_attn_extend(const void* q, int64_t q_row_stride,
                        const void* k_pool, const void* v_pool, int64_t pool_slots,
@@ -154,6 +169,7 @@ int32_t tf_attn_extend(const void* q, int64_t q_row_stride,
                        const int32_t* work, int32_t n_work,
                        int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
                        float scale, void* out, int64_t out_row_stride,
+                       const void* gate, int64_t gate_row_stride, int64_t gate_head_stride,
                        tf_stream_t stream);
 
 /* ------------------------------------------------------------------ planning

@@ -15,6 +15,7 @@ import torch
 
 from tests import module_golden as mg
 from tests.helpers import assert_attn_close
+from tokenfactory_amd import full_attention as fa
 from tokenfactory_amd.full_attention import FullAttention
 
 pytestmark = pytest.mark.gpu
@@ -31,21 +32,23 @@ class _Pool:
 
 
 @pytest.mark.parametrize("name", mg.CASES)
-def test_full_attention_forward_matches_reference_module(gpu, name):
+def test_full_attention_forward_matches_reference_module(gpu, name, monkeypatch):
     d, meta = mg.load()
     print(f"[module] case={name}", flush=True)
     mod = FullAttention(mg.config(meta), layer_idx=3, dtype=torch.bfloat16).to(gpu)
     mg.load_weights(mod, d)
     pool = _Pool(d, gpu)
     captured = {}
-    inner = mod._slot_based_attention
+    inner = fa.slot_based_attention
 
-    def spy(q, kb, vb, batch):
-        out = inner(q, kb, vb, batch)
-        captured["q"], captured["attn"] = q.clone(), out.clone()
-        return out
+    def spy(q, kb, vb, batch, *, gate=None, **kw):
+        # forward fuses the output gate into the attention call; the ungated
+        # attention (the reference's intermediate) comes from a second call.
+        captured["q"] = q.clone()
+        captured["attn"] = inner(q, kb, vb, batch, **kw).clone()
+        return inner(q, kb, vb, batch, gate=gate, **kw)
 
-    mod._slot_based_attention = spy
+    monkeypatch.setattr(fa, "slot_based_attention", spy)
     hidden = mg.bf16(d[f"{name}_hidden"]).to(device=gpu, dtype=torch.bfloat16)
     pos = torch.from_numpy(d[f"{name}_positions"]).to(gpu)
     with torch.no_grad():

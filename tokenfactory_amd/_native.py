@@ -12,7 +12,7 @@ from pathlib import Path
 from typing import Optional
 
 LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libtf_attn.so"
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 TF_DTYPE_BF16 = 0
 TF_DTYPE_FP8_E4M3 = 1
@@ -42,6 +42,7 @@ SIGNATURES = {
         _i32, _i32, _i32, _f32,        # num_q_heads, num_kv_heads, head_dim, scale
         _p, _i64,                      # out, out_row_stride
         _p, _i64, _i32, _i32,          # workspace, workspace_bytes, max_seq_len, num_workgroups
+        _p, _i64, _i64,                # gate, gate_row_stride, gate_head_stride
         _p,                            # stream
     ]),
     "tf_attn_decode_partial": None,   # same signature as tf_attn_decode
@@ -54,6 +55,7 @@ SIGNATURES = {
         _p, _i32,                      # work, n_work
         _i32, _i32, _i32, _f32,
         _p, _i64,
+        _p, _i64, _i64,                # gate, gate_row_stride, gate_head_stride
         _p,
     ]),
     "tf_attn_plan_extend": (_i32, [_p, _i32, _i32, _i32, _i32, _p, _i32]),

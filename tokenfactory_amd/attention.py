@@ -117,7 +117,7 @@ class SlotAttentionCall:
 
     def __init__(self, q, layer_k_buffer, layer_v_buffer, batch, *, scaling=None,
                  k_scale=None, v_scale=None, decode_workgroups: int = 0, out=None,
-                 stream=None):
+                 stream=None, gate=None):
         _check_inputs(q, layer_k_buffer, layer_v_buffer, batch)
         n_tok, n_q, head_dim = q.shape
         n_slots, n_kv, _ = layer_k_buffer.shape
@@ -140,6 +140,18 @@ class SlotAttentionCall:
         elif out.shape != q.shape or out.dtype != q.dtype or out.stride(2) != 1 \
                 or out.stride(1) != head_dim:
             raise ValueError("out must match q's shape/dtype with dense heads and dims")
+
+        if gate is not None:
+            if gate.shape != q.shape or gate.dtype != torch.bfloat16 or gate.device != q.device \
+                    or gate.stride(2) != 1 or gate.stride(0) % 8 or gate.stride(1) % 8 \
+                    or gate.data_ptr() % 16:
+                raise ValueError("gate must be a bf16 [T, Hq, D] view on q's device with "
+                                 "contiguous dims, strides in multiples of 8 and a 16-byte "
+                                 "aligned start")
+            self._gate_args = (gate.data_ptr(), gate.stride(0), gate.stride(1))
+        else:
+            self._gate_args = (None, 0, 0)
+        self.gate = gate
 
         bsz = batch.batch_size
         ext_lens = [int(e) for e in batch.extend_lens]
@@ -202,14 +214,15 @@ class SlotAttentionCall:
                      self.n_q, self.n_kv, self.head_dim, self.scaling,
                      self.out.data_ptr(), self.out.stride(0),
                      _ptr(ws), 0 if ws is None else ws.numel(), self.max_len,
-                     self.decode_workgroups, self.stream.cuda_stream)
+                     self.decode_workgroups, *self._gate_args, self.stream.cuda_stream)
 
     def run_extend(self) -> None:
         if self.n_work:
             _native.call("tf_attn_extend", self.q.data_ptr(), self.q.stride(0),
                          *self._pool_args, self._meta.data_ptr(), self.n_work,
                          self.n_q, self.n_kv, self.head_dim, self.scaling,
-                         self.out.data_ptr(), self.out.stride(0), self.stream.cuda_stream)
+                         self.out.data_ptr(), self.out.stride(0), *self._gate_args,
+                         self.stream.cuda_stream)
 
     def run_decode_partial(self) -> None:
         self._decode("tf_attn_decode_partial")
@@ -234,6 +247,7 @@ def slot_based_attention(
     v_scale: Optional[torch.Tensor] = None,
     decode_workgroups: int = 0,
     out: Optional[torch.Tensor] = None,
+    gate: Optional[torch.Tensor] = None,
 ) -> torch.Tensor:
     """Attention of ``q [T, Hq, D]`` over one layer's slot pool; returns ``[T, Hq, D]``.
 
@@ -241,10 +255,13 @@ def slot_based_attention(
     ``k_scale`` / ``v_scale`` (fp32 device scalars) are required for a
     ``float8_e4m3fn`` pool. ``decode_workgroups`` overrides the size of the
     decode kernel's persistent grid (0 = one workgroup per compute unit).
+    ``gate`` (bf16 ``[T, Hq, D]``, any view with contiguous dims): the result is
+    ``attn * F.silu(gate)`` (``full_attention.py:157-159``), computed in the
+    kernels' output write with the same bf16 roundings.
     """
     call = SlotAttentionCall(q, layer_k_buffer, layer_v_buffer, batch, scaling=scaling,
                              k_scale=k_scale, v_scale=v_scale,
-                             decode_workgroups=decode_workgroups, out=out)
+                             decode_workgroups=decode_workgroups, out=out, gate=gate)
     return call.run()
 
 

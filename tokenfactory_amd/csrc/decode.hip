@@ -73,6 +73,8 @@ struct DecodeArgs {
   float scale_log2;
   __bf16* out;
   int64_t out_stride;
+  const __bf16* gate;   // optional output gate (NULL: none)
+  int64_t gate_stride, gate_hstride;
   float* ws_ml;
   float* ws_o;
   int32_t n_blocks;   // P: workgroups of the streaming kernel
@@ -167,6 +169,17 @@ __device__ __forceinline__ void write_output(const DecodeArgs& a, int qrow, int 
                                              const WaveState& st, float vscale) {
   const float inv = vscale / st.l;
   __bf16* o = a.out + (int64_t)qrow * a.out_stride + (int64_t)hq * kD;
+  const __bf16* gt =
+      a.gate ? a.gate + (int64_t)qrow * a.gate_stride + (int64_t)hq * a.gate_hstride : nullptr;
+  // 8 outputs (dims off .. off + 7) per store; gated when the caller passed one.
+  auto store8 = [&](int off, u32x4 v) {
+    if (gt) {
+      const u32x4 gv = ld_g16(gt + off);
+#pragma unroll
+      for (int k = 0; k < 4; ++k) v[k] = gate_pair(v[k], gv[k]);
+    }
+    *reinterpret_cast<u32x4*>(o + off) = v;
+  };
   if (FP8) {
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
@@ -176,7 +189,7 @@ __device__ __forceinline__ void write_output(const DecodeArgs& a, int qrow, int 
 #pragma unroll
         for (int k = 0; k < 4; ++k)
           v[k] = pack_bf16(st.acc[8 * h + 2 * k][r] * inv, st.acc[8 * h + 2 * k + 1][r] * inv);
-        *reinterpret_cast<u32x4*>(o + 64 * g + 16 * r + 8 * h) = v;
+        store8(64 * g + 16 * r + 8 * h, v);
       }
     }
   } else {
@@ -188,7 +201,7 @@ __device__ __forceinline__ void write_output(const DecodeArgs& a, int qrow, int 
 #pragma unroll
         for (int k = 0; k < 4; ++k)
           v[k] = pack_bf16(st.acc[8 * s + 2 * k][r] * inv, st.acc[8 * s + 2 * k + 1][r] * inv);
-        *reinterpret_cast<u32x4*>(o + 128 * s + 32 * g + 8 * r) = v;
+        store8(128 * s + 32 * g + 8 * r, v);
       }
     }
   }
@@ -649,7 +662,9 @@ int decode_launch(const void* q, int64_t q_row_stride, const void* k_pool, const
                   const int32_t* q_rows, int32_t n_items, int32_t num_q_heads,
                   int32_t num_kv_heads, int32_t head_dim, float scale, void* out,
                   int64_t out_row_stride, void* workspace, int64_t workspace_bytes,
-                  int32_t max_seq_len, int32_t num_workgroups, tf_stream_t stream, int phases) {
+                  int32_t max_seq_len, int32_t num_workgroups, const void* gate,
+                  int64_t gate_row_stride, int64_t gate_head_stride, tf_stream_t stream,
+                  int phases) {
   clear_error();
   DecodePlan p;
   int rc = make_decode_plan(n_items, num_q_heads, num_kv_heads, head_dim, max_seq_len,
@@ -673,6 +688,9 @@ int decode_launch(const void* q, int64_t q_row_stride, const void* k_pool, const
   if (q_row_stride < (int64_t)num_q_heads * head_dim ||
       out_row_stride < (int64_t)num_q_heads * head_dim)
     return fail(TF_ERR_INVALID, "decode: row stride smaller than num_q_heads*head_dim");
+  if (gate && (!aligned16(gate) || gate_row_stride % 8 || gate_head_stride % 8 ||
+               gate_head_stride < head_dim))
+    return fail(TF_ERR_INVALID, "decode: gate must be 16-byte aligned with strides of 8 elements");
   if (p.total_bytes > 0 &&
       (!workspace || workspace_bytes < p.total_bytes || !aligned16(workspace)))
     return fail(TF_ERR_INVALID, "decode: workspace needs %lld bytes, got %lld",
@@ -703,6 +721,9 @@ int decode_launch(const void* q, int64_t q_row_stride, const void* k_pool, const
   a.scale_log2 = scale * kLog2e;
   a.out = static_cast<__bf16*>(out);
   a.out_stride = out_row_stride;
+  a.gate = static_cast<const __bf16*>(gate);
+  a.gate_stride = gate_row_stride;
+  a.gate_hstride = gate_head_stride;
   char* ws = static_cast<char*>(workspace);
   a.ws_ml = reinterpret_cast<float*>(ws);
   a.ws_o = reinterpret_cast<float*>(ws + p.ml_bytes);
@@ -741,12 +762,14 @@ int decode_launch(const void* q, int64_t q_row_stride, const void* k_pool, const
       int32_t n_items, int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,        \
       float scale, void *out, int64_t out_row_stride, void *workspace,                     \
       int64_t workspace_bytes, int32_t max_seq_len, int32_t num_workgroups,                \
+      const void *gate, int64_t gate_row_stride, int64_t gate_head_stride,                 \
       tf_stream_t stream
 #define TF_DECODE_ARGS                                                                      \
   q, q_row_stride, k_pool, v_pool, pool_slots, kv_dtype, k_scale, v_scale, req_to_token,   \
       rtt_rows, rtt_row_stride, rtt_cols, req_pool_indices, seq_lens, seq_len_override,    \
       items, q_rows, n_items, num_q_heads, num_kv_heads, head_dim, scale, out,             \
-      out_row_stride, workspace, workspace_bytes, max_seq_len, num_workgroups, stream
+      out_row_stride, workspace, workspace_bytes, max_seq_len, num_workgroups, gate,       \
+      gate_row_stride, gate_head_stride, stream
 
 extern "C" {
 

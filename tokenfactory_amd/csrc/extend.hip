@@ -539,13 +539,21 @@ extend_kernel(ExtendArgs a) {
   l += __shfl_xor(l, 32, kWave);
   const float inv = vscale / l;
   __bf16* o = a.out + (int64_t)(q_start + t) * a.out_stride + (int64_t)(hk * G + h) * kD;
+  const __bf16* gt = a.gate ? a.gate + (int64_t)(q_start + t) * a.gate_stride +
+                                  (int64_t)(hk * G + h) * a.gate_hstride
+                            : nullptr;
 #pragma unroll
   for (int mt = 0; mt < 8; ++mt) {
 #pragma unroll
     for (int rq = 0; rq < 4; ++rq) {
-      const u32x2 v = {pack_bf16(acc[mt][4 * rq + 0] * inv, acc[mt][4 * rq + 1] * inv),
-                       pack_bf16(acc[mt][4 * rq + 2] * inv, acc[mt][4 * rq + 3] * inv)};
-      *reinterpret_cast<u32x2*>(o + 32 * mt + 8 * rq + 4 * g) = v;
+      const int off = 32 * mt + 8 * rq + 4 * g;
+      u32x2 v = {pack_bf16(acc[mt][4 * rq + 0] * inv, acc[mt][4 * rq + 1] * inv),
+                 pack_bf16(acc[mt][4 * rq + 2] * inv, acc[mt][4 * rq + 3] * inv)};
+      if (gt) {
+        const u32x2 gv = ld_g8(gt + off);
+        v = u32x2{gate_pair(v[0], gv[0]), gate_pair(v[1], gv[1])};
+      }
+      *reinterpret_cast<u32x2*>(o + off) = v;
     }
   }
 }
@@ -562,7 +570,9 @@ extern "C" int32_t tf_attn_extend(const void* q, int64_t q_row_stride, const voi
                                   int32_t seq_len_override, const int32_t* work,
                                   int32_t n_work, int32_t num_q_heads, int32_t num_kv_heads,
                                   int32_t head_dim, float scale, void* out,
-                                  int64_t out_row_stride, tf_stream_t stream) {
+                                  int64_t out_row_stride, const void* gate,
+                                  int64_t gate_row_stride, int64_t gate_head_stride,
+                                  tf_stream_t stream) {
   using namespace tfa;
   clear_error();
   if (n_work < 0) return fail(TF_ERR_INVALID, "extend: n_work=%d", n_work);
@@ -585,6 +595,9 @@ extern "C" int32_t tf_attn_extend(const void* q, int64_t q_row_stride, const voi
   if (!aligned16(q) || !aligned16(out) || !aligned16(k_pool) || !aligned16(v_pool) ||
       (q_row_stride * 2) % 16 || (out_row_stride * 2) % 16 || !aligned16(work))
     return fail(TF_ERR_INVALID, "extend: q/out/pools/work must be 16-byte aligned");
+  if (gate && (!aligned16(gate) || gate_row_stride % 8 || gate_head_stride % 8 ||
+               gate_head_stride < head_dim))
+    return fail(TF_ERR_INVALID, "extend: gate must be 16-byte aligned with strides of 8 elements");
   if ((int64_t)num_kv_heads * head_dim * 2 > INT32_MAX)
     return fail(TF_ERR_INVALID, "extend: num_kv_heads=%d too large", num_kv_heads);
   if (q_row_stride < (int64_t)num_q_heads * head_dim ||
@@ -612,6 +625,9 @@ extern "C" int32_t tf_attn_extend(const void* q, int64_t q_row_stride, const voi
   a.scale_log2 = scale * kLog2e;
   a.out = static_cast<__bf16*>(out);
   a.out_stride = out_row_stride;
+  a.gate = static_cast<const __bf16*>(gate);
+  a.gate_stride = gate_row_stride;
+  a.gate_hstride = gate_head_stride;
 
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   if (kv_dtype == TF_DTYPE_FP8_E4M3)

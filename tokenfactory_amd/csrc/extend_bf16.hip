@@ -573,13 +573,21 @@ __global__ void __launch_bounds__(kThreads) extend_bf16_kernel(ExtendArgs a) {
     const int t = rho / G, h = rho - t * G;
     const float inv = 1.f / lt;
     __bf16* o = a.out + (int64_t)(q_start + t) * a.out_stride + (int64_t)(hk * G + h) * kD;
+    const __bf16* gt = a.gate ? a.gate + (int64_t)(q_start + t) * a.gate_stride +
+                                    (int64_t)(hk * G + h) * a.gate_hstride
+                              : nullptr;
 #pragma unroll
     for (int mt = 0; mt < 8; ++mt) {
 #pragma unroll
       for (int rq = 0; rq < 4; ++rq) {
-        const u32x2 v = {pack_bf16(acc[rb][mt][4 * rq + 0] * inv, acc[rb][mt][4 * rq + 1] * inv),
-                         pack_bf16(acc[rb][mt][4 * rq + 2] * inv, acc[rb][mt][4 * rq + 3] * inv)};
-        *reinterpret_cast<u32x2*>(o + 32 * mt + 8 * rq + 4 * g) = v;
+        const int off = 32 * mt + 8 * rq + 4 * g;
+        u32x2 v = {pack_bf16(acc[rb][mt][4 * rq + 0] * inv, acc[rb][mt][4 * rq + 1] * inv),
+                   pack_bf16(acc[rb][mt][4 * rq + 2] * inv, acc[rb][mt][4 * rq + 3] * inv)};
+        if (gt) {
+          const u32x2 gv = ld_g8(gt + off);
+          v = u32x2{gate_pair(v[0], gv[0]), gate_pair(v[1], gv[1])};
+        }
+        *reinterpret_cast<u32x2*>(o + off) = v;
       }
     }
   }

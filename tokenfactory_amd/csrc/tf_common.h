@@ -96,6 +96,25 @@ __device__ __forceinline__ u32x4 e4m3x8_to_bf16x8(uint32_t d0, uint32_t d1) {
   return r;
 }
 
+// ---------------------------------------------------------------- output gate
+// The attention output gate of full_attention.py:157-159 on a pair of
+// outputs: bf16(o * bf16(silu(g))), the reference's two bf16 tensor ops, each
+// rounding to bf16.  silu(x) = x / (1 + exp(-x)) is evaluated in fp32 with the
+// hardware exp2 and reciprocal (about 1 ulp each), so after the bf16 rounding
+// it agrees with an exactly rounded evaluation except, rarely, by one bf16 ulp;
+// +-inf, NaN and huge magnitudes give the same results (inf, NaN, NaN, x, -0).
+// o: the two attention outputs already rounded to bf16; gp: two bf16 gates.
+__device__ __forceinline__ float bf16_lo(uint32_t p) { return __uint_as_float(p << 16); }
+__device__ __forceinline__ float bf16_hi(uint32_t p) { return __uint_as_float(p & 0xffff0000u); }
+__device__ __forceinline__ float silu_to_bf16(float g) {
+  const float e = __builtin_amdgcn_exp2f(-g * kLog2e);
+  return bf16_lo(pack_bf16(g * __builtin_amdgcn_rcpf(1.f + e), 0.f));
+}
+__device__ __forceinline__ uint32_t gate_pair(uint32_t o, uint32_t gp) {
+  return pack_bf16(bf16_lo(o) * silu_to_bf16(bf16_lo(gp)),
+                   bf16_hi(o) * silu_to_bf16(bf16_hi(gp)));
+}
+
 // Wave index within the workgroup as a scalar (wave-uniform) value, so loops
 // and branches keyed on it compile to scalar control flow.
 __device__ __forceinline__ int wave_id() {

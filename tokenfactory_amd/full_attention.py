@@ -13,10 +13,12 @@ q/k RMSNorm with the ``w * x`` convention (``qwen3_8/rms_norm.py:19-24``),
 partial rotate-half RoPE on the first ``head_dim * partial_rotary_factor`` dims
 (``qwen3_8/rotary_embedding.py:46-95``) and the KV write run as one fused
 kernel (``tf_qk_norm_rope_kv_write``); ``RMSNorm`` / ``PartialRoPE`` below hold
-their parameters and state the same math in PyTorch. The q/k/v/o projections
-(plain bf16 ``nn.Linear`` here; the reference's block-FP8 linears are a
-separate component) and the ``silu(gate)`` output gate
-(``full_attention.py:157-158``) stay PyTorch ops, as the reference has them.
+their parameters and state the same math in PyTorch. The ``attn * silu(gate)``
+output gate (``full_attention.py:157-159``) is fused into the attention
+kernels' output write (the gate is passed as a strided view of the q
+projection). The q/k/v/o projections stay PyTorch ops (plain bf16
+``nn.Linear`` here; the reference's block-FP8 linears are a separate
+component).
 """
 from __future__ import annotations
 
@@ -24,7 +26,6 @@ from typing import List, Optional
 
 import torch
 import torch.nn as nn
-import torch.nn.functional as F
 
 from .attention import qk_norm_rope_kv_write, slot_based_attention
 
@@ -123,15 +124,13 @@ class FullAttention(nn.Module):
                                       getattr(config, "rope_theta", 1e7),
                                       getattr(config, "mrope_section", None),
                                       getattr(config, "mrope_interleaved", True))
-        self._kv_scales = (None, None)
 
     def forward(self, hidden_states: torch.Tensor, positions: torch.Tensor, cache_pool,
                 forward_batch) -> torch.Tensor:
         n_tok = hidden_states.shape[0]
         if self.attn_output_gate:
             qg = self.q_proj(hidden_states).view(n_tok, self.num_heads, 2 * self.head_dim)
-            q, gate = qg.chunk(2, dim=-1)
-            gate = gate.reshape(n_tok, self.num_heads * self.head_dim)
+            q, gate = qg.chunk(2, dim=-1)   # gate stays a [T, Hq, D] view of qg
         else:
             q = self.q_proj(hidden_states).view(n_tok, self.num_heads, self.head_dim)
             gate = None
@@ -148,18 +147,16 @@ class FullAttention(nn.Module):
             rope.inv_freq, rope.rotary_dim, rope.mrope_section, rope.mrope_interleaved,
             k_buf, v_buf, forward_batch.out_cache_loc, *scales)
 
-        self._kv_scales = scales
-        try:
-            attn = self._slot_based_attention(q, k_buf, v_buf, forward_batch)
-        finally:
-            self._kv_scales = (None, None)
-        attn = attn.reshape(n_tok, self.num_heads * self.head_dim)
-        if gate is not None:
-            attn = attn * F.silu(gate)
-        return self.o_proj(attn)
+        # Attention with the output gate `attn * silu(gate)` (:150-159) fused
+        # into the kernels' output write.
+        attn = slot_based_attention(q, k_buf, v_buf, forward_batch, scaling=self.scaling,
+                                    k_scale=scales[0], v_scale=scales[1], gate=gate)
+        return self.o_proj(attn.reshape(n_tok, self.num_heads * self.head_dim))
 
     def _slot_based_attention(self, q: torch.Tensor, layer_k_buffer: torch.Tensor,
-                              layer_v_buffer: torch.Tensor, batch) -> torch.Tensor:
-        k_scale, v_scale = self._kv_scales
+                              layer_v_buffer: torch.Tensor, batch, k_scale=None,
+                              v_scale=None) -> torch.Tensor:
+        """The reference's ungated attention call (``:163-283``); ``forward``
+        uses the same kernels with the output gate fused."""
         return slot_based_attention(q, layer_k_buffer, layer_v_buffer, batch,
                                     scaling=self.scaling, k_scale=k_scale, v_scale=v_scale)
