@@ -44,7 +44,7 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--only", default="decode,extend,mixed,fp8,prep,gate",
+    ap.add_argument("--only", default="decode,extend,mixed,fp8,prep,gate,plan",
                     help="comma list of decode,extend,mixed,fp8,prep,copy")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--workgroups", type=int, default=0,
@@ -250,6 +250,65 @@ def bench_gate(torch, workloads, SlotAttentionCall, args):
             "fused_cost_ms": k_gated - k_plain, "reference_ops_ms": ops_ms}
 
 
+def bench_plan(torch, workloads, SlotAttentionCall, args):
+    """Whole mixed step as a caller sees it, wall clock per step: host-planned
+    (plan + pinned upload + launches), device-planned (planner kernel +
+    launches) and the device-planned step replayed from a HIP graph."""
+    import time
+    n = max(5, args.steps // 2)
+    res = {}
+    for tag, wl in (("mixed", workloads.mixed(device="cuda")),
+                    ("small_mixed", workloads.mixed(device="cuda", n_extend=2, extend_new=64,
+                                                    prefix_hi=512, n_decode=16, dec_lo=256,
+                                                    dec_hi=2048, pool_slots=1 << 16))):
+        res[tag] = _plan_step(torch, wl, SlotAttentionCall, args, n, time)
+        r = res[tag]
+        log(f"{tag} step (wall / host enqueue per step): host-planned "
+            f"{r['host_planned_ms']*1e3:.0f} / {r['host_planned_cpu_ms']*1e3:.0f} us, "
+            f"device-planned {r['device_planned_ms']*1e3:.0f} / "
+            f"{r['device_planned_cpu_ms']*1e3:.0f} us, graph replay "
+            f"{r['graph_replay_ms']*1e3:.0f} / {r['graph_replay_cpu_ms']*1e3:.0f} us")
+    res["workload"] = ("one attention step incl. planning and launch: mixed (4 x 2k extend + "
+                       "128 decode) and small_mixed (2 x 64 extend + 16 decode, contexts "
+                       "U[256, 2k])")
+    return res
+
+
+def _plan_step(torch, wl, SlotAttentionCall, args, n, time):
+    kw = dict(scaling=wl.scale)
+
+    def wall(fn):
+        """(wall ms per step, host ms per step spent enqueuing)."""
+        for _ in range(max(2, args.warmup // 2)):
+            fn()
+        torch.cuda.synchronize()
+        host = 0.0
+        t0 = time.perf_counter()
+        for _ in range(n):
+            h = time.perf_counter()
+            fn()
+            host += time.perf_counter() - h
+        torch.cuda.synchronize()
+        return (time.perf_counter() - t0) / n * 1e3, host / n * 1e3
+
+    host_ms = wall(lambda: SlotAttentionCall(wl.q, wl.k_pool, wl.v_pool, wl.batch, **kw).run())
+    dev_ms = wall(lambda: SlotAttentionCall(wl.q, wl.k_pool, wl.v_pool, wl.batch,
+                                            device_plan=True, **kw).run())
+    call = SlotAttentionCall(wl.q, wl.k_pool, wl.v_pool, wl.batch, device_plan=True, **kw)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        call.run()
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        call.run()
+    graph_ms = wall(graph.replay)
+    return {"host_planned_ms": host_ms[0], "device_planned_ms": dev_ms[0],
+            "graph_replay_ms": graph_ms[0], "host_planned_cpu_ms": host_ms[1],
+            "device_planned_cpu_ms": dev_ms[1], "graph_replay_cpu_ms": graph_ms[1]}
+
+
 def bench_copy(torch, args):
     """A plain device copy of known size, the reference point for HBM counters."""
     n = 1 << 30
@@ -332,6 +391,8 @@ def main():
         torch.cuda.empty_cache()
     if "prep" in only:
         secondary["qk_prep_20k"] = bench_prep(torch, args)
+    if "plan" in only:
+        secondary["step_planning"] = bench_plan(torch, workloads, SlotAttentionCall, args)
     if "gate" in only:
         secondary["output_gate"] = bench_gate(torch, workloads, SlotAttentionCall, args)
         torch.cuda.empty_cache()

@@ -72,7 +72,8 @@ const char* tf_attn_last_error(void);
  *
  * Processes n_items requests.  Item i is batch entry items[i] (or i when
  * items is NULL) and reads / writes query row q_rows[i] (or items[i] / i when
- * q_rows is NULL) of q and out.
+ * q_rows is NULL) of q and out; items[i] < 0 is a padding entry (no work, no
+ * output), as tf_attn_plan_device writes them.
  *
  * The streaming kernel runs a persistent grid of num_workgroups workgroups
  * (0 = one per compute unit) that split the (request, kv head, 16-token tile)
@@ -195,6 +196,34 @@ int32_t tf_attn_plan_extend(const int64_t* extend_lens, int32_t batch_size,
 
 int32_t tf_attn_plan_decode_items(const int64_t* extend_lens, int32_t batch_size,
                                   int32_t* items, int32_t* q_rows, int32_t capacity);
+
+/* ------------------------------------------------------------------ device-side planning
+ * tf_attn_plan_device: the same two lists built on the GPU (one workgroup) from
+ * DEVICE extend_lens (int64 [batch_size], batch_size <= 4096), enqueued on
+ * stream, so a step needs no host loop, no host->device copy and no sync and
+ * can be captured in a HIP graph (it replaces the per-step host bookkeeping
+ * of full_attention.py:250-265 and engine/model_runner.py:108-188).
+ * work: device int32 [work_capacity][8], filled with the entries of
+ * tf_attn_plan_extend in the same order, then padding entries (ext 0) up to
+ * work_capacity; launching tf_attn_extend with n_work = work_capacity is then
+ * exact (padding workgroups exit at once).  dec_items / dec_rows: device int32
+ * [dec_capacity], the decode items of tf_attn_plan_decode_items then -1 / 0
+ * padding (tf_attn_decode* skip items < 0; pass n_items = dec_capacity).
+ * status: device int32 [3] = {real work entries, real decode items, flags}
+ * (flags bit 0: a capacity was too small; bit 1: an extend length outside
+ * [1, 2^31)).
+ * tf_attn_plan_device_capacity: num_kv_heads * (ceil(T * G / 256) + B), the
+ * work entries the plan of any B requests with T tokens in total can need
+ * (G = num_q_heads / num_kv_heads); dec_capacity = B suffices.
+ */
+int64_t tf_attn_plan_device_capacity(int64_t total_tokens, int32_t batch_size,
+                                     int32_t num_q_heads, int32_t num_kv_heads);
+
+int32_t tf_attn_plan_device(const int64_t* extend_lens, int32_t batch_size,
+                            int32_t num_q_heads, int32_t num_kv_heads,
+                            int32_t decode_to_decode_kernel, int32_t* work,
+                            int32_t work_capacity, int32_t* dec_items, int32_t* dec_rows,
+                            int32_t dec_capacity, int32_t* status, tf_stream_t stream);
 
 /* ------------------------------------------------------------------ KV write
  * k_pool[out_cache_loc[t]] = k[t]; v_pool[out_cache_loc[t]] = v[t]

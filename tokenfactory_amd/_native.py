@@ -12,7 +12,7 @@ from pathlib import Path
 from typing import Optional
 
 LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libtf_attn.so"
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 TF_DTYPE_BF16 = 0
 TF_DTYPE_FP8_E4M3 = 1
@@ -59,6 +59,13 @@ SIGNATURES = {
         _p,
     ]),
     "tf_attn_plan_extend": (_i32, [_p, _i32, _i32, _i32, _i32, _p, _i32]),
+    "tf_attn_plan_device_capacity": (_i64, [_i64, _i32, _i32, _i32]),
+    "tf_attn_plan_device": (_i32, [
+        _p, _i32, _i32, _i32, _i32,    # extend_lens (device int64), batch, heads, decode_to_decode
+        _p, _i32,                      # work, work_capacity
+        _p, _p, _i32,                  # dec_items, dec_rows, dec_capacity
+        _p, _p,                        # status, stream
+    ]),
     "tf_attn_plan_decode_items": (_i32, [_p, _i32, _p, _p, _i32]),
     "tf_kv_write": (_i32, [
         _p, _p, _i64, _i32,            # k, v, src_row_stride, src_dtype
@@ -145,6 +152,14 @@ def call(name: str, *args) -> int:
             raise NotImplementedError(f"{name}: {msg}")
         raise NativeCallError(name, rc, msg)
     return rc
+
+
+def plan_device_capacity(total_tokens, batch_size, num_q_heads, num_kv_heads) -> int:
+    """Work-list entries tf_attn_plan_device fills for T tokens and B requests."""
+    n = load().tf_attn_plan_device_capacity(total_tokens, batch_size, num_q_heads, num_kv_heads)
+    if n < 0:
+        raise ValueError(load().tf_attn_last_error().decode(errors="replace"))
+    return int(n)
 
 
 def decode_workspace_bytes(n_items, num_q_heads, num_kv_heads, head_dim, max_seq_len,

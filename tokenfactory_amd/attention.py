@@ -117,7 +117,7 @@ class SlotAttentionCall:
 
     def __init__(self, q, layer_k_buffer, layer_v_buffer, batch, *, scaling=None,
                  k_scale=None, v_scale=None, decode_workgroups: int = 0, out=None,
-                 stream=None, gate=None):
+                 stream=None, gate=None, device_plan: bool = False):
         _check_inputs(q, layer_k_buffer, layer_v_buffer, batch)
         n_tok, n_q, head_dim = q.shape
         n_slots, n_kv, _ = layer_k_buffer.shape
@@ -162,7 +162,8 @@ class SlotAttentionCall:
         self.k_buf, self.v_buf = layer_k_buffer, layer_v_buffer
         self.k_scale, self.v_scale = k_scale, v_scale
         self.batch = batch
-        self.stream = stream if stream is not None else torch.cuda.current_stream(q.device)
+        self._fixed_stream = stream
+        self.device_plan = bool(device_plan)
         self.n_q, self.n_kv, self.head_dim = n_q, n_kv, head_dim
         self.scaling = float(scaling)
         self.decode_workgroups = int(decode_workgroups)
@@ -178,9 +179,27 @@ class SlotAttentionCall:
         self.n_dec = 0
         self._meta = None
         self._items = self._rows = None
+        self._status = None
         if n_tok == 0:
             return
-        if batch.max_extend_len == 1 or (bsz == 1 and ext_lens[0] == 1):
+        if self.device_plan:
+            # Lists built on the device at every run() from extend_lens_tensor,
+            # padded to capacities fixed by T and B (graph-capturable step).
+            ext_t = batch.extend_lens_tensor
+            if ext_t is None or ext_t.device != q.device or ext_t.dtype != torch.long \
+                    or ext_t.numel() != bsz or not ext_t.is_contiguous():
+                raise ValueError("device_plan needs batch.extend_lens_tensor: contiguous int64 "
+                                 "[batch_size] on q's device")
+            self.n_work = _native.plan_device_capacity(n_tok, bsz, n_q, n_kv)
+            self.n_dec = bsz
+            self._ext_t = ext_t
+            self._meta = torch.empty(self.n_work * 8 + 2 * bsz + 4, dtype=torch.int32,
+                                     device=q.device)
+            base = self._meta.data_ptr() + 4 * self.n_work * 8
+            self._items = _DevPtr(base)
+            self._rows = _DevPtr(base + 4 * bsz)
+            self._status = _DevPtr(base + 8 * bsz)
+        elif batch.max_extend_len == 1 or (bsz == 1 and ext_lens[0] == 1):
             # Pure decode: batch entry b is query row b; nothing to upload.
             self.n_dec = bsz
         else:
@@ -204,7 +223,32 @@ class SlotAttentionCall:
             if nbytes:
                 self.ws = _workspace(q.device, self.stream, nbytes)
 
+    @property
+    def stream(self) -> torch.cuda.Stream:
+        """The stream given at construction, else the current one at launch time
+        (so a call built outside a graph capture launches into the capture)."""
+        if self._fixed_stream is not None:
+            return self._fixed_stream
+        return torch.cuda.current_stream(self.q.device)
+
     # -- launches
+    def run_plan(self) -> None:
+        """Device-side planning (device_plan=True): the work and decode lists."""
+        if self.device_plan and self.n_work:
+            base = self._meta.data_ptr()
+            _native.call("tf_attn_plan_device", self._ext_t.data_ptr(), self.batch.batch_size,
+                         self.n_q, self.n_kv, 1, base, self.n_work, self._items.data_ptr(),
+                         self._rows.data_ptr(), self.n_dec, self._status.data_ptr(),
+                         self.stream.cuda_stream)
+
+    def plan_status(self):
+        """(real work entries, real decode items, flags) of the last device plan:
+        flags bit 0 = capacity exceeded, bit 1 = an extend length outside [1, 2^31)."""
+        if self._status is None:
+            return None
+        n = self.n_work * 8 + 2 * self.n_dec
+        return tuple(int(x) for x in self._meta[n:n + 3].cpu())
+
     def _decode(self, entry: str) -> None:
         if not self.n_dec:
             return
@@ -231,6 +275,7 @@ class SlotAttentionCall:
         self._decode("tf_attn_decode_merge")
 
     def run(self) -> torch.Tensor:
+        self.run_plan()
         self.run_extend()
         self._decode("tf_attn_decode")
         return self.out

@@ -18,7 +18,8 @@ REPO_DIR = PKG_DIR.parent
 CSRC = PKG_DIR / "csrc"
 LIB_DIR = PKG_DIR / "_lib"
 LIB_PATH = LIB_DIR / "libtf_attn.so"
-SOURCES = ["abi.hip", "decode.hip", "extend.hip", "extend_bf16.hip", "kv_ops.hip", "qk_prep.hip"]
+SOURCES = ["abi.hip", "decode.hip", "extend.hip", "extend_bf16.hip", "kv_ops.hip", "plan.hip",
+           "qk_prep.hip"]
 ARCH = "gfx950"
 
 

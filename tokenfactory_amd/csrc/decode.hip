@@ -334,8 +334,14 @@ __device__ __forceinline__ void pv(const VBuf<FP8>& vb, u32x2 pt, WaveState& st)
 
 
 // Context length of item i (the request's seq_len, or the bsz == 1 override),
-// clamped to the req_to_token row.
+// clamped to the req_to_token row.  A negative batch index marks a padding
+// entry of a device-built item list: no work and no output.
+__device__ __forceinline__ bool item_is_padding(const DecodeArgs& a, int i) {
+  return a.items && a.items[i] < 0;
+}
+
 __device__ __forceinline__ int item_len(const DecodeArgs& a, int i) {
+  if (item_is_padding(a, i)) return 0;
   const int b = a.items ? a.items[i] : i;
   int64_t len = a.seq_override > 0 ? (int64_t)a.seq_override : a.seq_lens[b];
   if (len > a.rtt_cols) len = a.rtt_cols;
@@ -574,7 +580,9 @@ decode_merge_kernel(DecodeArgs a) {
   WaveState st;
   reset_state(st);
   if (Ti == 0) {
-    if (w == 0 && head_ok) {
+    // An empty context (seq_len 0) is a NaN row, as the reference's softmax
+    // over no keys; padding entries write nothing.
+    if (w == 0 && head_ok && !item_is_padding(a, item)) {
       st.m = 0.f;
       st.l = __builtin_nanf("");
       write_output<FP8>(a, qrow, hq, g, st, 1.f);

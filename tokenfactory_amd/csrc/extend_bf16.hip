@@ -391,6 +391,7 @@ __global__ void __launch_bounds__(kThreads) extend_bf16_kernel(ExtendArgs a) {
   const int ext = wk[4];
   const int G = a.group;
 
+  if (ext <= 0) return;   // padding entry of a device-built work list
   int64_t len = a.seq_override > 0 ? (int64_t)a.seq_override : a.seq_lens[b];
   if (len > a.rtt_cols) len = a.rtt_cols;
   const int L = (int)len;
