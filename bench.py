@@ -32,6 +32,7 @@ sys.path.insert(0, str(REPO))
 
 HBM_PEAK = 8.0e12          # MI355X HBM3E bytes/s
 MFMA_BF16_PEAK = 2.5e15    # MI355X dense bf16 FLOP/s
+FP8_PEAK_TFLOPS = 5000.0   # MI355X dense fp8 TFLOP/s
 METRIC = ("decode attn HBM GB/s (% peak) + prefill attn TFLOP/s (% MFMA peak), 1 MI355X")
 
 
@@ -44,7 +45,7 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--only", default="decode,extend,mixed,fp8,prep,gate,plan",
+    ap.add_argument("--only", default="decode,extend,mixed,fp8,prep,gate,plan,oproj",
                     help="comma list of decode,extend,mixed,fp8,prep,copy")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--workgroups", type=int, default=0,
@@ -250,6 +251,44 @@ def bench_gate(torch, workloads, SlotAttentionCall, args):
             "fused_cost_ms": k_gated - k_plain, "reference_ops_ms": ops_ms}
 
 
+def bench_oproj(torch, args):
+    """The block-FP8 o_proj after the gated attention (fp8_linear.py:196-214 ->
+    triton_block_fp8_linear): 24 x 256 -> 5120, 128 x 128 weight-scale blocks,
+    at the token counts of the decode_b64, mixed and extend_prefix steps."""
+    from tokenfactory_amd import fp8_linear as fl
+    from oracle.fp8_linear import quantize_weight_blocks
+    n_out, k_in = 5120, 24 * 256
+    g = torch.Generator().manual_seed(31)
+    wq, ws = quantize_weight_blocks(torch.randn((n_out, k_in), generator=g) * 0.02)
+    wq, ws = wq.cuda(), ws.cuda()
+    steps = max(5, args.steps)
+    res = {}
+    for m in (64, 8320, 21938):
+        x = (torch.randn((m, k_in), device="cuda") * 2).to(torch.bfloat16)
+        xq, sx = fl.quantize_activations(x)
+        out = torch.empty((m, n_out), dtype=torch.bfloat16, device="cuda")
+        gemm = lambda _: fl.block_fp8_gemm(xq, sx, wq, ws, None, out=out)
+        quant = lambda _: fl.quantize_activations(x)
+        for fn in (gemm, quant):
+            time_kernel(torch, [None], max(2, args.warmup), fn)
+        t_gemm = time_kernel(torch, [None], steps, gemm)
+        t_quant = time_kernel(torch, [None], steps, quant)
+        flops = 2.0 * m * n_out * k_in
+        tf = flops / (t_gemm * 1e-3) / 1e12
+        wbytes = n_out * k_in + ws.numel() * 4 + m * k_in + m * n_out * 2
+        res[f"m{m}"] = {"gemm_ms": t_gemm, "quant_ms": t_quant, "gemm_tflops": tf,
+                        "gemm_frac_of_fp8_peak": tf / FP8_PEAK_TFLOPS,
+                        "gemm_gbps": wbytes / (t_gemm * 1e-3) / 1e9}
+        log(f"o_proj fp8 m={m}: gemm {t_gemm*1e3:.1f} us = {tf:.0f} TFLOP/s "
+            f"({tf / FP8_PEAK_TFLOPS * 100:.1f}% of fp8 peak, {wbytes / t_gemm / 1e6:.0f} GB/s), "
+            f"activation quant {t_quant*1e3:.1f} us")
+        del x, xq, out
+    res["workload"] = ("block-FP8 o_proj: bf16 [m, 6144] -> dynamic e4m3 -> x e4m3 [5120, 6144] "
+                       "with 128x128 fp32 block scales -> bf16 [m, 5120]; m = tokens of the "
+                       "decode_b64, mixed and extend_prefix steps")
+    return res
+
+
 def bench_plan(torch, workloads, SlotAttentionCall, args):
     """Whole mixed step as a caller sees it, wall clock per step: host-planned
     (plan + pinned upload + launches), device-planned (planner kernel +
@@ -395,6 +434,9 @@ def main():
         secondary["step_planning"] = bench_plan(torch, workloads, SlotAttentionCall, args)
     if "gate" in only:
         secondary["output_gate"] = bench_gate(torch, workloads, SlotAttentionCall, args)
+        torch.cuda.empty_cache()
+    if "oproj" in only:
+        secondary["oproj_fp8"] = bench_oproj(torch, args)
         torch.cuda.empty_cache()
     if dec is None:
         print(json.dumps({"metric": METRIC, "value": None, "secondary": secondary},

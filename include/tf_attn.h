@@ -274,6 +274,48 @@ int32_t tf_qk_norm_rope_kv_write(const void* q, int64_t q_token_stride, int64_t 
                                  int32_t kv_dtype, const float* k_scale, const float* v_scale,
                                  tf_stream_t stream);
 
+/* ------------------------------------------------------------------ FP8 linear
+ * The block-FP8 o_proj that follows the gated attention output
+ * (full_attention.py:161 -> RowParallelFP8Linear, fp8_linear.py:196-214 ->
+ * triton_block_fp8_linear, fp8_triton.py:107-183), as two calls.
+ *
+ * tf_fp8_act_quant replaces the dynamic activation quantisation of
+ * fp8_triton.py:127-130:
+ *   x_scale = bf16(max(max|x|, 1e-12) / 448)   (a NaN in x makes it NaN)
+ *   xq      = e4m3(clamp(x / x_scale, -448, 448)), round to nearest even.
+ * x: bf16 [rows, cols], cols a multiple of 8, row stride x_row_stride
+ * elements (a multiple of 8), 16-byte aligned.  xq: e4m3 [rows, cols], row
+ * stride xq_row_stride bytes (a multiple of 8), 8-byte aligned.  x_scale: a
+ * device fp32 scalar that receives the scale.  workspace: device scratch of at
+ * least TF_FP8_QUANT_WORKSPACE_BYTES bytes, 4-byte aligned (no initial
+ * contents needed).
+ *
+ * tf_fp8_block_gemm replaces _block_fp8_gemm_kernel (fp8_triton.py:17-98):
+ *   out[i, j] = bf16( sum over 128-wide K slices s of
+ *                     (sum_{k in s} xq[i, k] w[j, k]) * (x_scale * w_scale[j / block_h, 128 s / block_w])
+ *                     + bias[j] ),   fp32 accumulation.
+ * xq: e4m3 [m, k]; w: e4m3 [n, k] (nn.Linear layout); both 16-byte aligned
+ * with row strides (bytes) that are multiples of 16; k a multiple of 128.
+ * w_scale: fp32 [ceil(n / block_h), ceil(k / block_w)] at the given element
+ * strides (block_w a multiple of 128), or NULL for a weight without block
+ * scales (weight_scale_inv None: every scale 1).  bias: bf16 [n] or NULL.
+ * out: bf16 [m, n], row stride out_row_stride elements (a multiple of 4),
+ * 8-byte aligned.
+ */
+#define TF_FP8_QUANT_WORKSPACE_BYTES 4096
+
+int32_t tf_fp8_act_quant(const void* x, int32_t x_dtype, int64_t rows, int64_t cols,
+                         int64_t x_row_stride, void* xq, int64_t xq_row_stride,
+                         float* x_scale, void* workspace, int64_t workspace_bytes,
+                         tf_stream_t stream);
+
+int32_t tf_fp8_block_gemm(const void* xq, int64_t xq_row_stride, const float* x_scale,
+                          const void* w, int64_t w_row_stride, const float* w_scale,
+                          int64_t w_scale_row_stride, int64_t w_scale_col_stride,
+                          int32_t block_h, int32_t block_w, const void* bias, int64_t m,
+                          int64_t n, int64_t k, void* out, int64_t out_row_stride,
+                          tf_stream_t stream);
+
 /* ------------------------------------------------------------------ gather
  * Padded slot gather of the batched branches (full_attention.py:216-220):
  * out[b, t] = pool[max(req_to_token[req_pool_indices[b], t], 0)] for

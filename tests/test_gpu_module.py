@@ -64,3 +64,44 @@ def test_full_attention_forward_matches_reference_module(gpu, name, monkeypatch)
     keep[loc] = False
     ref_k = mg.bf16(d["k_pool0"]).to(device=gpu, dtype=torch.bfloat16)
     assert torch.equal(pool.k[keep], ref_k[keep])
+
+
+def test_full_attention_fp8_projections(gpu, monkeypatch):
+    """FP8 quantization_config: q/k/v/o are block-FP8 linears. Each projection
+    is checked against the oracle's block-FP8 linear on the same input (q/k/v on
+    the hidden states, o_proj on the gated attention output the module feeds it)."""
+    from oracle import fp8_linear as ofl
+    from tokenfactory_amd.fp8_linear import Fp8Linear
+
+    d, meta = mg.load()
+    cfg = mg.config(meta)
+    cfg.quantization_config = {"quant_method": "fp8", "fmt": "e4m3",
+                               "activation_scheme": "dynamic", "weight_block_size": [128, 128]}
+    mod = FullAttention(cfg, layer_idx=3, dtype=torch.bfloat16).to(gpu)
+    for name in ("q_proj", "k_proj", "v_proj", "o_proj"):
+        lin = getattr(mod, name)
+        assert isinstance(lin, Fp8Linear) and lin.weight.dtype == torch.float8_e4m3fn
+        lin.quantize_from(mg.bf16(d[f"w_{name}"]).to(gpu))
+    pool = _Pool(d, gpu)
+    seen = {}
+    inner = fa.slot_based_attention
+
+    def spy(q, kb, vb, batch, *, gate=None, **kw):
+        seen["gated"] = inner(q, kb, vb, batch, gate=gate, **kw)
+        return seen["gated"]
+
+    monkeypatch.setattr(fa, "slot_based_attention", spy)
+    hidden = mg.bf16(d["mixed_hidden"]).to(device=gpu, dtype=torch.bfloat16)
+    pos = torch.from_numpy(d["mixed_positions"]).to(gpu)
+    print("[module fp8] mixed case", flush=True)
+    with torch.no_grad():
+        out = mod(hidden, pos, pool, mg.batch(d, meta, "mixed", gpu))
+        proj = {n: getattr(mod, n)(hidden) for n in ("q_proj", "k_proj", "v_proj")}
+    torch.cuda.synchronize()
+    n_tok = hidden.shape[0]
+    x_o = seen["gated"].reshape(n_tok, -1)
+    for name, x, got in [(n, hidden, proj[n]) for n in proj] + [("o_proj", x_o, out)]:
+        lin = getattr(mod, name)
+        ref, _, _ = ofl.block_fp8_linear(x.cpu(), lin.weight.cpu(), lin.weight_scale_inv.cpu())
+        rms = float(ref.pow(2).mean().sqrt())
+        assert torch.allclose(got.cpu().float(), ref, atol=2e-2 * rms, rtol=1e-2), name

@@ -8,16 +8,21 @@ Public surface (the reference's names and contracts, see each module):
   ``_slot_based_attention`` signatures
 * ``slot_based_attention`` / ``write_kv`` / ``gather_kv`` /
   ``qk_norm_rope_kv_write`` - the kernels' Python entry points
+* ``Fp8Linear`` / ``block_fp8_linear`` - block-FP8 linear (``qwen3_8/fp8_linear.py``,
+  ``qwen3_8/fp8_triton.py``) on the gfx950 FP8 GEMM
 """
 from .forward_batch import ForwardBatch
 from .attention import gather_kv, qk_norm_rope_kv_write, slot_based_attention, write_kv
 from .kv_pool import FullAttnKVPool
+from .fp8_linear import Fp8Linear, block_fp8_linear
 from .full_attention import FullAttention
 
 __all__ = [
+    "Fp8Linear",
     "ForwardBatch",
     "FullAttnKVPool",
     "FullAttention",
+    "block_fp8_linear",
     "gather_kv",
     "qk_norm_rope_kv_write",
     "slot_based_attention",

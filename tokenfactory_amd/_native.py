@@ -12,7 +12,7 @@ from pathlib import Path
 from typing import Optional
 
 LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libtf_attn.so"
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 TF_DTYPE_BF16 = 0
 TF_DTYPE_FP8_E4M3 = 1
@@ -22,6 +22,8 @@ TF_OK = 0
 TF_ERR_INVALID = -1
 TF_ERR_UNSUPPORTED = -2
 TF_ERR_HIP = -3
+
+TF_FP8_QUANT_WORKSPACE_BYTES = 4096
 
 # Exported symbols and their ctypes signatures (restype, argtypes).
 _p = ctypes.c_void_p
@@ -84,6 +86,18 @@ SIGNATURES = {
         _p, _i64,                      # q_out, q_out_token_stride
         _p, _p, _p, _i64, _i32,        # out_cache_loc, k_pool, v_pool, pool_slots, kv_dtype
         _p, _p, _p,                    # k_scale, v_scale, stream
+    ]),
+    "tf_fp8_act_quant": (_i32, [
+        _p, _i32, _i64, _i64, _i64,    # x, x_dtype, rows, cols, x_row_stride
+        _p, _i64, _p,                  # xq, xq_row_stride, x_scale
+        _p, _i64, _p,                  # workspace, workspace_bytes, stream
+    ]),
+    "tf_fp8_block_gemm": (_i32, [
+        _p, _i64, _p,                  # xq, xq_row_stride, x_scale
+        _p, _i64,                      # w, w_row_stride
+        _p, _i64, _i64, _i32, _i32,    # w_scale, its row / col strides, block_h, block_w
+        _p, _i64, _i64, _i64,          # bias, m, n, k
+        _p, _i64, _p,                  # out, out_row_stride, stream
     ]),
     "tf_gather_kv": (_i32, [
         _p, _i32, _i64, _i64,          # pool, kv_dtype, pool_slots, row_elems

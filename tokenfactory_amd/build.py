@@ -18,8 +18,8 @@ REPO_DIR = PKG_DIR.parent
 CSRC = PKG_DIR / "csrc"
 LIB_DIR = PKG_DIR / "_lib"
 LIB_PATH = LIB_DIR / "libtf_attn.so"
-SOURCES = ["abi.hip", "decode.hip", "extend.hip", "extend_bf16.hip", "kv_ops.hip", "plan.hip",
-           "qk_prep.hip"]
+SOURCES = ["abi.hip", "decode.hip", "extend.hip", "extend_bf16.hip", "fp8_linear.hip",
+           "kv_ops.hip", "plan.hip", "qk_prep.hip"]
 ARCH = "gfx950"
 
 
@@ -48,7 +48,10 @@ def compile_flags() -> list:
 # Per-file flags on top of compile_flags().  extend_bf16.hip: its builtin
 # MFMAs (S^T = K Q^T) must produce VGPR results, because the O^T accumulators
 # of its inline-assembly MFMAs occupy every AGPR.
-EXTRA_FLAGS = {"extend_bf16.hip": ["-mllvm", "--amdgpu-mfma-vgpr-form=1"]}
+# fp8_linear.hip: the GEMM folds each MFMA product into fp32 accumulators
+# with a VALU FMA, which reads VGPRs only.
+EXTRA_FLAGS = {"extend_bf16.hip": ["-mllvm", "--amdgpu-mfma-vgpr-form=1"],
+               "fp8_linear.hip": ["-mllvm", "--amdgpu-mfma-vgpr-form=1"]}
 
 
 def _filter_stderr(text: str) -> str:

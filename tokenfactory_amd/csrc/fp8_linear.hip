@@ -1,0 +1,456 @@
+// Block-scaled FP8 linear layer: the o_proj after the attention output gate.
+//
+// Replaces the reference's triton_block_fp8_linear (qwen3_8/fp8_triton.py:107-183)
+// and its GEMM kernel _block_fp8_gemm_kernel (fp8_triton.py:17-98), which
+// Qwen3_8FP8Linear._linear_op (qwen3_8/fp8_linear.py:196-214) uses for a
+// float8_e4m3fn weight:
+//   x_scale = bf16(max(amax|x|, 1e-12) / 448)            dynamic, per tensor
+//   xq      = e4m3(clamp(x / x_scale, -448, 448))          round to nearest even
+//   out     = bf16(sum_kb (xq[:, kb] w[:, kb]^T) * (x_scale * ws[n / bh, kb / bw]) + bias)
+// with fp32 accumulation, kb running over 128-wide slices of K (the weight
+// scale blocks are 128 x 128 in the Qwen3 FP8 checkpoints; any block_h and any
+// block_w that is a multiple of 128 is accepted here).
+//
+// Activation quantisation is two HBM-bound passes: act_amax_kernel writes
+// per-workgroup maxima of |x| (as bf16 bit patterns, so NaN wins like torch's
+// max), act_quant_kernel reduces them, forms x_scale and writes e4m3 rows.
+//
+// GEMM (fp8_gemm_kernel<MT>): out^T tiles D[n][m] = sum_k w[n][k] xq[m][k] with
+// v_mfma_f32_16x16x128_f8f6f4 (one instruction covers a whole 128-wide scale
+// block).  A workgroup owns 128 output columns x 32 MT rows; its four waves
+// split that 2 x 2, a wave holding 64 columns x 16 MT rows (4 x MT 16x16
+// tiles).  Each MFMA starts from zero and its product is folded into the fp32
+// accumulator with that block's scale, acc += p * s, one FMA per accumulator
+// element per 128 of K.  Per 128-wide K slice the workgroup stages the weight
+// tile (128 rows), the activation tile (32 MT rows) and the 128 column scales
+// straight from global memory into LDS (global_load_lds_dwordx4 /
+// global_load_lds_dword), two slices ahead of the MFMAs, three stages deep.
+// Rows are 128 bytes; a row's 16-byte chunk c is stored at chunk
+// c ^ swz(row) so the operand reads (16 rows x 16 bytes per 16 lanes) hit 16
+// distinct bank groups.  The transposed product makes each lane own four
+// consecutive output columns of a row: the epilogue stores 8 bytes per lane.
+#include <algorithm>
+
+#include "tf_common.h"
+#include "tf_internal.h"
+
+namespace tfa {
+namespace {
+
+typedef int32_t i32x8 __attribute__((ext_vector_type(8)));
+typedef __attribute__((address_space(3))) void lds_void;
+
+constexpr int kThreads = 256;
+constexpr int kQuantMaxBlocks = TF_FP8_QUANT_WORKSPACE_BYTES / 4;
+constexpr float kFp8Max = 448.f;
+
+// ---------------------------------------------------------------- quantisation
+struct QuantArgs {
+  const uint16_t* x;      // bf16 [rows, cols], row stride xs elements
+  int64_t xs;
+  uint32_t rows, c8;      // rows, cols / 8
+  uint8_t* xq;            // e4m3 [rows, cols], row stride qs bytes
+  int64_t qs;
+  uint32_t* partial;      // per-workgroup max of |x| bits
+  uint32_t nblocks;
+  float* scale_out;
+};
+
+__device__ __forceinline__ uint32_t block_max(uint32_t v, uint32_t* red) {
+#pragma unroll
+  for (int d = 32; d >= 1; d >>= 1) v = max(v, (uint32_t)__shfl_xor((int)v, d, kWave));
+  if ((threadIdx.x & (kWave - 1)) == 0) red[threadIdx.x / kWave] = v;
+  __syncthreads();
+  v = red[0];
+#pragma unroll
+  for (int i = 1; i < kThreads / kWave; ++i) v = max(v, red[i]);
+  return v;
+}
+
+// |x| as bf16 bit patterns: for non-negative values the integer order is the
+// float order and every NaN pattern sorts above +inf.
+__device__ __forceinline__ uint32_t abs_max8(u32x4 v) {
+  uint32_t m = 0;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) m = max(m, max(v[j] & 0x7fffu, (v[j] >> 16) & 0x7fffu));
+  return m;
+}
+
+__global__ void __launch_bounds__(kThreads) act_amax_kernel(QuantArgs a) {
+  __shared__ uint32_t red[kThreads / kWave];
+  const uint32_t n = a.rows * a.c8;
+  uint32_t m = 0;
+  for (uint32_t q = blockIdx.x * kThreads + threadIdx.x; q < n; q += gridDim.x * kThreads) {
+    const uint32_t r = q / a.c8, c = q - r * a.c8;
+    m = max(m, abs_max8(ld_nt16(a.x + r * a.xs + 8 * c)));
+  }
+  m = block_max(m, red);
+  if (threadIdx.x == 0) a.partial[blockIdx.x] = m;
+}
+
+__device__ __forceinline__ float sat448(float x) {
+  return x != x ? x : fminf(fmaxf(x, -kFp8Max), kFp8Max);
+}
+
+__global__ void __launch_bounds__(kThreads) act_quant_kernel(QuantArgs a) {
+  __shared__ uint32_t red[kThreads / kWave];
+  uint32_t m = 0;
+  for (uint32_t i = threadIdx.x; i < a.nblocks; i += kThreads) m = max(m, a.partial[i]);
+  m = block_max(m, red);
+  // amax.clamp(min=1e-12) and amax / 448 on bf16 tensors (fp8_triton.py:128-129):
+  // both results are rounded to bf16.  NaN stays NaN.
+  float amax = __uint_as_float(m << 16);
+  if (m <= 0x7f80u) amax = fmaxf(amax, (float)(__bf16)1e-12f);
+  const float scale = (float)(__bf16)(amax / kFp8Max);
+  if (blockIdx.x == 0 && threadIdx.x == 0) *a.scale_out = scale;
+
+  const uint32_t n = a.rows * a.c8;
+  for (uint32_t q = blockIdx.x * kThreads + threadIdx.x; q < n; q += gridDim.x * kThreads) {
+    const uint32_t r = q / a.c8, c = q - r * a.c8;
+    const u32x4 v = ld_nt16(a.x + r * a.xs + 8 * c);
+    u32x2 f;
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const uint32_t lo = __builtin_amdgcn_cvt_pk_fp8_f32(sat448(bf16_lo(v[2 * j]) / scale),
+                                                          sat448(bf16_hi(v[2 * j]) / scale),
+                                                          0u, false);
+      f[j] = __builtin_amdgcn_cvt_pk_fp8_f32(sat448(bf16_lo(v[2 * j + 1]) / scale),
+                                             sat448(bf16_hi(v[2 * j + 1]) / scale), lo, true);
+    }
+    *reinterpret_cast<u32x2*>(a.xq + r * a.qs + 8 * c) = f;
+  }
+}
+
+// ---------------------------------------------------------------- GEMM
+constexpr int kStages = 3;            // K slices resident in LDS (2 staged ahead)
+constexpr int kBN = 128;              // output columns per workgroup
+constexpr int kKSlice = 128;          // K per slice = one weight-scale block
+constexpr int kWBytes = kBN * kKSlice;
+constexpr int kSBytes = 1024;         // 128 column scales, twice
+
+template <int MT>
+struct Tile {
+  static constexpr int kBM = 32 * MT;             // activation rows per workgroup
+  static constexpr int kXBytes = kBM * kKSlice;
+  static constexpr int kStage = kXBytes + kWBytes + kSBytes;
+  static constexpr int kLoads = MT + 4 + 1;       // staging instructions per thread per slice
+};
+
+struct GemmArgs {
+  const uint8_t* xq;      // e4m3 [M, K], row stride xs bytes
+  int64_t xs;
+  const float* x_scale;   // device scalar
+  const uint8_t* w;       // e4m3 [N, K], row stride wrs bytes
+  int64_t wrs;
+  const float* wsc;       // fp32 block scales (NULL: all 1)
+  int64_t sn, sk;         // their strides (elements)
+  int32_t bh, bw_slices;  // block_h, block_w / 128
+  const uint16_t* bias;   // bf16 [N] or NULL
+  uint16_t* out;          // bf16 [M, N], row stride os elements
+  int64_t os;
+  int32_t M, N, KB, tiles_m;
+};
+
+__device__ __forceinline__ int swz(int r) { return (r & 7) ^ ((r >> 3) & 1); }
+
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return (uint32_t)(uintptr_t)(const lds_void*)p;
+}
+// global_load_lds_dword{,x4} with a scalar base and a 32-bit per-lane offset:
+// lane l's 4 / 16 bytes from sbase + voff land at LDS address M0 + 4 l / 16 l.
+// Invisible to the compiler's wait counting: readers wait with an explicit
+// s_waitcnt vmcnt and a barrier.
+__device__ __forceinline__ void dma4(const void* sbase, uint32_t voff, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dword %0, %1"
+               :: "v"(voff), "s"(sbase), "s"(lds) : "m0");
+}
+__device__ __forceinline__ void dma16(const void* sbase, uint32_t voff, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1"
+               :: "v"(voff), "s"(sbase), "s"(lds) : "m0");
+}
+
+template <int N>
+__device__ __forceinline__ void vm_wait() {
+  asm volatile("s_waitcnt vmcnt(%0)" :: "n"(N) : "memory");
+}
+
+// Operand fragment of 16 rows x 128 bytes: lane l holds row l % 16, bytes
+// 32 (l / 16) .. + 31 (chunks 2 (l / 16) and 2 (l / 16) + 1, stored swizzled).
+// The f8f6f4 MFMA sums over (lane group, byte) pairs in the same way for both
+// operands, so any k order shared by the two operands gives the same product.
+__device__ __forceinline__ i32x8 frag(const uint8_t* row, int o0, int o1) {
+  const u32x4 a = ld_s16(row + o0), b = ld_s16(row + o1);
+  i32x8 f;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    f[j] = (int32_t)a[j];
+    f[4 + j] = (int32_t)b[j];
+  }
+  return f;
+}
+
+__device__ __forceinline__ f32x4 mfma_fp8(const i32x8& w, const i32x8& x) {
+  // e4m3 x e4m3 (format 0 for both operands), no block exponents: an
+  // unscaled v_mfma_f32_16x16x128_f8f6f4 from zero.
+  return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(w, x, f32x4{0.f, 0.f, 0.f, 0.f}, 0,
+                                                          0, 0, 0, 0, 0);
+}
+
+// kUni: block_h is a multiple of 64, so the 64 columns of a wave share one
+// weight-scale row and the slice's scale is one value per wave.
+template <int MT, bool kUni>
+__global__ void __launch_bounds__(kThreads) fp8_gemm_kernel(GemmArgs a) {
+  using T = Tile<MT>;
+  __shared__ __attribute__((aligned(16))) uint8_t smem[kStages * T::kStage];
+  const int t = threadIdx.x, w = wave_id(), l = t & 63;
+  const int wm = w >> 1, wn = w & 1;
+  const int m0 = (blockIdx.x % a.tiles_m) * T::kBM;
+  const int n0 = (blockIdx.x / a.tiles_m) * kBN;
+
+  const float xsc = *a.x_scale;
+  asm volatile("" :: "v"(xsc));   // land the scale before any staging load is in flight
+
+  // Staging: thread t moves 16-byte chunk t % 8 of row 32 i + t / 8 of a tile
+  // (instruction i), fetched from chunk (t % 8) ^ swz(row) of the source row;
+  // rows past the matrix repeat its last row.  Byte offsets fit 32 bits.
+  const int srow = t >> 3;
+  const uint32_t cb = 16 * ((t & 7) ^ swz(srow));
+  uint32_t xo[MT], wo[4];
+#pragma unroll
+  for (int i = 0; i < MT; ++i)
+    xo[i] = (uint32_t)min(m0 + 32 * i + srow, a.M - 1) * (uint32_t)a.xs + cb;
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    wo[i] = (uint32_t)min(n0 + 32 * i + srow, a.N - 1) * (uint32_t)a.wrs + cb;
+  // Without block scales every lane stages x_scale itself and the staged value
+  // is used as is; otherwise the staged weight scale times x_scale.
+  const bool ones = a.wsc == nullptr;
+  const float sfac = ones ? 1.f : xsc;
+  const int scol = min(n0 + 64 * (w & 1) + l, a.N - 1);
+  const uint32_t so = ones ? 0u : (uint32_t)((scol / a.bh) * a.sn) * 4u;
+  const uint32_t lds0 = lds_addr(smem);
+
+  auto issue = [&](int kb, int st) {
+    const uint32_t sb = lds0 + st * T::kStage + w * 1024;
+    const uint8_t* xb = a.xq + (int64_t)kb * kKSlice;
+    const uint8_t* wb = a.w + (int64_t)kb * kKSlice;
+#pragma unroll
+    for (int i = 0; i < MT; ++i) dma16(xb, xo[i], sb + i * 4096);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) dma16(wb, wo[i], sb + T::kXBytes + i * 4096);
+    const float* sbase = ones ? a.x_scale : a.wsc + (int64_t)(kb / a.bw_slices) * a.sk;
+    dma4(sbase, so, lds0 + st * T::kStage + T::kXBytes + kWBytes + w * 256);
+  };
+
+  // Fragment reads: row l % 16 of a 16-row tile, chunks 2g and 2g + 1.
+  const int rr = l & 15, g = l >> 4;
+  const int o0 = 16 * ((2 * g) ^ swz(rr)), o1 = 16 * ((2 * g + 1) ^ swz(rr));
+  const int xrow = wm * 16 * MT + rr;   // + 16 tm
+  const int wrow = wn * 64 + rr;        // + 16 tn
+  const int scol4 = wn * 64 + 4 * g;    // + 16 tn: first of this lane's 4 columns
+
+  f32x4 acc[MT][4];
+#pragma unroll
+  for (int i = 0; i < MT; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  // Slices past the last are never read; their stage is refilled with the last
+  // slice so that every step issues (and waits for) the same loads.
+  const int KB = a.KB;
+  issue(0, 0);
+  issue(min(1, KB - 1), 1);
+  vm_wait<T::kLoads>();
+  __syncthreads();
+
+  int st = 0;
+  for (int j = 0; j < KB; ++j) {
+    issue(min(j + 2, KB - 1), st == 0 ? 2 : st - 1);
+    const uint8_t* sp = smem + st * T::kStage;
+    const uint8_t* ssp = sp + T::kXBytes + kWBytes;
+    f32x4 s4[4];
+    if constexpr (kUni) {
+      const float s1 = sfac * *reinterpret_cast<const float*>(ssp + 4 * (wn * 64));
+#pragma unroll
+      for (int tn = 0; tn < 4; ++tn) s4[tn] = f32x4{s1, s1, s1, s1};
+    } else {
+#pragma unroll
+      for (int tn = 0; tn < 4; ++tn)
+        s4[tn] = sfac * *reinterpret_cast<const f32x4*>(ssp + 4 * (scol4 + 16 * tn));
+    }
+    i32x8 wf[4];
+#pragma unroll
+    for (int tn = 0; tn < 4; ++tn) wf[tn] = frag(sp + T::kXBytes + (wrow + 16 * tn) * kKSlice, o0, o1);
+    // Row tm's products are folded in while row tm + 1's MFMAs run.
+    f32x4 p[MT][4];
+#pragma unroll
+    for (int tm = 0; tm < MT; ++tm) {
+      const i32x8 xf = frag(sp + (xrow + 16 * tm) * kKSlice, o0, o1);
+#pragma unroll
+      for (int tn = 0; tn < 4; ++tn) {
+        p[tm][tn] = mfma_fp8(wf[tn], xf);
+        if (tm > 0) acc[tm - 1][tn] += p[tm - 1][tn] * s4[tn];
+      }
+    }
+#pragma unroll
+    for (int tn = 0; tn < 4; ++tn) acc[MT - 1][tn] += p[MT - 1][tn] * s4[tn];
+    vm_wait<T::kLoads>();
+    __syncthreads();
+    st = st == kStages - 1 ? 0 : st + 1;
+  }
+  vm_wait<0>();   // the refills of the last steps land before the workgroup ends
+
+  // Epilogue: lane holds D[n0 + wn 64 + 16 tn + 4 g + r][m0 + wm 16 MT + 16 tm + rr].
+#pragma unroll
+  for (int tn = 0; tn < 4; ++tn) {
+    const int n = n0 + scol4 + 16 * tn;
+    float b[4] = {0.f, 0.f, 0.f, 0.f};
+    if (a.bias) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        if (n + r < a.N) b[r] = __uint_as_float((uint32_t)a.bias[n + r] << 16);
+    }
+#pragma unroll
+    for (int tm = 0; tm < MT; ++tm) {
+      const int m = m0 + xrow + 16 * tm;
+      if (m >= a.M) continue;
+      const f32x4 v = acc[tm][tn];
+      uint16_t* o = a.out + (int64_t)m * a.os + n;
+      if (n + 3 < a.N) {
+        u32x2 pk;
+        pk[0] = pack_bf16(v[0] + b[0], v[1] + b[1]);
+        pk[1] = pack_bf16(v[2] + b[2], v[3] + b[3]);
+        *reinterpret_cast<u32x2*>(o) = pk;
+      } else {
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          if (n + r < a.N) o[r] = (uint16_t)(pack_bf16(v[r] + b[r], 0.f) & 0xffffu);
+      }
+    }
+  }
+}
+
+template <int MT>
+void launch_gemm(const GemmArgs& a, hipStream_t stream) {
+  GemmArgs b = a;
+  b.tiles_m = (a.M + Tile<MT>::kBM - 1) / Tile<MT>::kBM;
+  const int tiles_n = (a.N + kBN - 1) / kBN;
+  const dim3 grid(b.tiles_m * tiles_n), block(kThreads);
+  if (a.wsc == nullptr || a.bh % 64 == 0)
+    hipLaunchKernelGGL((fp8_gemm_kernel<MT, true>), grid, block, 0, stream, b);
+  else
+    hipLaunchKernelGGL((fp8_gemm_kernel<MT, false>), grid, block, 0, stream, b);
+}
+
+}  // namespace
+}  // namespace tfa
+
+extern "C" {
+
+int32_t tf_fp8_act_quant(const void* x, int32_t x_dtype, int64_t rows, int64_t cols,
+                         int64_t x_row_stride, void* xq, int64_t xq_row_stride,
+                         float* x_scale, void* workspace, int64_t workspace_bytes,
+                         tf_stream_t stream) {
+  using namespace tfa;
+  clear_error();
+  if (x_dtype != TF_DTYPE_BF16)
+    return fail(TF_ERR_UNSUPPORTED, "fp8_act_quant: x must be bf16 (dtype %d)", x_dtype);
+  if (rows < 0 || cols <= 0 || cols % 8 || x_row_stride < cols || xq_row_stride < cols)
+    return fail(TF_ERR_INVALID, "fp8_act_quant: rows=%lld cols=%lld (a multiple of 8) strides %lld/%lld",
+                (long long)rows, (long long)cols, (long long)x_row_stride,
+                (long long)xq_row_stride);
+  if (x_row_stride % 8 || xq_row_stride % 8)
+    return fail(TF_ERR_INVALID, "fp8_act_quant: row strides must be multiples of 8");
+  if (rows * (cols / 8) > (int64_t)UINT32_MAX / 2 || rows * x_row_stride > INT64_MAX / 4)
+    return fail(TF_ERR_UNSUPPORTED, "fp8_act_quant: %lld x %lld is too large", (long long)rows,
+                (long long)cols);
+  if ((rows > 0 && (!x || !xq)) || !x_scale || !workspace)
+    return fail(TF_ERR_INVALID, "fp8_act_quant: null pointer");
+  if (!aligned16(x) || !aligned8(xq) || (reinterpret_cast<uintptr_t>(workspace) & 3u))
+    return fail(TF_ERR_INVALID, "fp8_act_quant: x must be 16-byte and xq 8-byte aligned");
+  if (workspace_bytes < TF_FP8_QUANT_WORKSPACE_BYTES)
+    return fail(TF_ERR_INVALID, "fp8_act_quant: workspace of %lld bytes (needs %d)",
+                (long long)workspace_bytes, TF_FP8_QUANT_WORKSPACE_BYTES);
+  QuantArgs a;
+  a.x = static_cast<const uint16_t*>(x);
+  a.xs = x_row_stride;
+  a.rows = (uint32_t)rows;
+  a.c8 = (uint32_t)(cols / 8);
+  a.xq = static_cast<uint8_t*>(xq);
+  a.qs = xq_row_stride;
+  a.partial = static_cast<uint32_t*>(workspace);
+  a.scale_out = x_scale;
+  const int64_t chunks = rows * (cols / 8);
+  // ~8 chunks (128 B of x) per thread, at most kQuantMaxBlocks workgroups
+  const int64_t want = (chunks + 8 * kThreads - 1) / (8 * kThreads);
+  a.nblocks = (uint32_t)std::max<int64_t>(1, std::min<int64_t>(want, kQuantMaxBlocks));
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  hipLaunchKernelGGL(act_amax_kernel, dim3(a.nblocks), dim3(kThreads), 0, s, a);
+  hipLaunchKernelGGL(act_quant_kernel, dim3(a.nblocks), dim3(kThreads), 0, s, a);
+  return launch_status("tf_fp8_act_quant launch");
+}
+
+int32_t tf_fp8_block_gemm(const void* xq, int64_t xq_row_stride, const float* x_scale,
+                          const void* w, int64_t w_row_stride, const float* w_scale,
+                          int64_t w_scale_row_stride, int64_t w_scale_col_stride,
+                          int32_t block_h, int32_t block_w, const void* bias, int64_t m,
+                          int64_t n, int64_t k, void* out, int64_t out_row_stride,
+                          tf_stream_t stream) {
+  using namespace tfa;
+  clear_error();
+  if (m < 0 || n <= 0 || k <= 0 || k % kKSlice)
+    return fail(TF_ERR_INVALID, "fp8_block_gemm: m=%lld n=%lld k=%lld (k a multiple of 128)",
+                (long long)m, (long long)n, (long long)k);
+  if (m > INT32_MAX / 2 || n > INT32_MAX / 2 || k > INT32_MAX / 2)
+    return fail(TF_ERR_UNSUPPORTED, "fp8_block_gemm: dimensions too large");
+  if (xq_row_stride < k || w_row_stride < k || out_row_stride < n || xq_row_stride % 16 ||
+      w_row_stride % 16 || out_row_stride % 4)
+    return fail(TF_ERR_INVALID,
+                "fp8_block_gemm: row strides %lld/%lld/%lld (fp8 rows 16-byte, out rows "
+                "8-byte multiples)",
+                (long long)xq_row_stride, (long long)w_row_stride, (long long)out_row_stride);
+  if (!w || !x_scale || (m > 0 && (!xq || !out)))
+    return fail(TF_ERR_INVALID, "fp8_block_gemm: null pointer");
+  if (!aligned16(xq) || !aligned16(w) || !aligned8(out) ||
+      (reinterpret_cast<uintptr_t>(bias) & 1u))
+    return fail(TF_ERR_INVALID, "fp8_block_gemm: xq / w 16-byte, out 8-byte aligned");
+  if (w_scale && (block_h <= 0 || block_w <= 0 || block_w % kKSlice))
+    return fail(TF_ERR_UNSUPPORTED,
+                "fp8_block_gemm: block_h=%d block_w=%d (block_w a multiple of 128)", block_h,
+                block_w);
+  if (m == 0) return TF_OK;
+  if ((m - 1) * xq_row_stride + k > (int64_t)UINT32_MAX ||
+      (n - 1) * w_row_stride + k > (int64_t)UINT32_MAX ||
+      (w_scale && ((n - 1) / block_h) * w_scale_row_stride > (int64_t)(UINT32_MAX / 4)))
+    return fail(TF_ERR_UNSUPPORTED, "fp8_block_gemm: xq, w or w_scale spans more than 4 GiB");
+  GemmArgs a;
+  a.xq = static_cast<const uint8_t*>(xq);
+  a.xs = xq_row_stride;
+  a.x_scale = x_scale;
+  a.w = static_cast<const uint8_t*>(w);
+  a.wrs = w_row_stride;
+  a.wsc = w_scale;
+  a.sn = w_scale_row_stride;
+  a.sk = w_scale_col_stride;
+  a.bh = w_scale ? block_h : 1;
+  a.bw_slices = w_scale ? block_w / kKSlice : 1;
+  a.bias = static_cast<const uint16_t*>(bias);
+  a.out = static_cast<uint16_t*>(out);
+  a.os = out_row_stride;
+  a.M = (int32_t)m;
+  a.N = (int32_t)n;
+  a.KB = (int32_t)(k / kKSlice);
+  a.tiles_m = 0;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  if (m <= 32)
+    launch_gemm<1>(a, s);
+  else if (m <= 64)
+    launch_gemm<2>(a, s);
+  else if (m <= 128)
+    launch_gemm<4>(a, s);
+  else
+    launch_gemm<8>(a, s);
+  return launch_status("tf_fp8_block_gemm launch");
+}
+
+}  // extern "C"

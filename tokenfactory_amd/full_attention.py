@@ -16,9 +16,11 @@ kernel (``tf_qk_norm_rope_kv_write``); ``RMSNorm`` / ``PartialRoPE`` below hold
 their parameters and state the same math in PyTorch. The ``attn * silu(gate)``
 output gate (``full_attention.py:157-159``) is fused into the attention
 kernels' output write (the gate is passed as a strided view of the q
-projection). The q/k/v/o projections stay PyTorch ops (plain bf16
-``nn.Linear`` here; the reference's block-FP8 linears are a separate
-component).
+projection). With an FP8 ``quantization_config`` (``quant_method == "fp8"``,
+``weight_block_size``; ``qwen3_8/fp8_linear.py:27-40``) the q/k/v/o
+projections are ``Fp8Linear`` (dynamic e4m3 activations x block-scaled e4m3
+weights on the gfx950 FP8 GEMM, like the reference's Triton path); otherwise
+plain bf16 ``nn.Linear``.
 """
 from __future__ import annotations
 
@@ -28,6 +30,16 @@ import torch
 import torch.nn as nn
 
 from .attention import qk_norm_rope_kv_write, slot_based_attention
+from .fp8_linear import Fp8Linear
+
+
+def _fp8_block_size(config):
+    """``weight_block_size`` when the config asks for block-FP8 linears
+    (``fp8_linear.py:27-40``), else None."""
+    q = getattr(config, "quantization_config", None)
+    if isinstance(q, dict) and q.get("quant_method") == "fp8":
+        return tuple(q.get("weight_block_size", [128, 128]))
+    return None
 
 
 class RMSNorm(nn.Module):
@@ -112,10 +124,18 @@ class FullAttention(nn.Module):
         hidden = config.hidden_size
         bias = getattr(config, "attention_bias", False)
         q_out = self.num_heads * self.head_dim * (2 if self.attn_output_gate else 1)
-        self.q_proj = nn.Linear(hidden, q_out, bias=bias, dtype=dtype)
-        self.k_proj = nn.Linear(hidden, self.num_kv_heads * self.head_dim, bias=bias, dtype=dtype)
-        self.v_proj = nn.Linear(hidden, self.num_kv_heads * self.head_dim, bias=bias, dtype=dtype)
-        self.o_proj = nn.Linear(self.num_heads * self.head_dim, hidden, bias=bias, dtype=dtype)
+        block = _fp8_block_size(config)
+        if block is not None:
+            def linear(i, o):
+                return Fp8Linear(i, o, bias=bias, block_size=block)
+        else:
+            def linear(i, o):
+                return nn.Linear(i, o, bias=bias, dtype=dtype)
+        kv_out = self.num_kv_heads * self.head_dim
+        self.q_proj = linear(hidden, q_out)
+        self.k_proj = linear(hidden, kv_out)
+        self.v_proj = linear(hidden, kv_out)
+        self.o_proj = linear(self.num_heads * self.head_dim, hidden)
         eps = getattr(config, "rms_norm_eps", 1e-6)
         self.q_norm = RMSNorm(self.head_dim, eps)
         self.k_norm = RMSNorm(self.head_dim, eps)
