@@ -119,6 +119,12 @@ def test_gemm_oproj_shape(gpu, m):
     gemm_case(gpu, m, 5120, 6144, seed=m)
 
 
+@pytest.mark.parametrize("m,n", [(1025, 640), (1500, 320), (2048, 5120)])
+def test_gemm_large_m(gpu, m, n):
+    # the 8-wave 256 x 256 tiles for large M, ragged in M and in N tiles
+    gemm_case(gpu, m, n, 6144 if n < 5120 else 1536, bias=n == 320, seed=m)
+
+
 @pytest.mark.parametrize("k", [128, 256, 384])
 def test_gemm_short_k(gpu, k):
     # one, two and three 128-wide K slices: the staging pipeline's edge cases

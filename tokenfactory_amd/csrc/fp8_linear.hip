@@ -15,16 +15,17 @@
 // per-workgroup maxima of |x| (as bf16 bit patterns, so NaN wins like torch's
 // max), act_quant_kernel reduces them, forms x_scale and writes e4m3 rows.
 //
-// GEMM (fp8_gemm_kernel<MT>): out^T tiles D[n][m] = sum_k w[n][k] xq[m][k] with
+// GEMM (fp8_gemm_kernel): out^T tiles D[n][m] = sum_k w[n][k] xq[m][k] with
 // v_mfma_f32_16x16x128_f8f6f4 (one instruction covers a whole 128-wide scale
-// block).  A workgroup owns 128 output columns x 32 MT rows; its four waves
-// split that 2 x 2, a wave holding 64 columns x 16 MT rows (4 x MT 16x16
-// tiles).  Each MFMA starts from zero and its product is folded into the fp32
+// block).  A workgroup of 2 x WN waves owns 64 WN output columns x 32 MT rows,
+// a wave holding 64 columns x 16 MT rows (4 x MT 16x16 tiles): 4 waves
+// (128 columns, three K slices in LDS, one wave per SIMD) up to M = 1024,
+// 8 waves (256 x 256, two slices in LDS, two waves per SIMD) above.  Each MFMA starts from zero and its product is folded into the fp32
 // accumulator with that block's scale, acc += p * s, one FMA per accumulator
 // element per 128 of K.  Per 128-wide K slice the workgroup stages the weight
-// tile (128 rows), the activation tile (32 MT rows) and the 128 column scales
+// tile (64 WN rows), the activation tile (32 MT rows) and the column scales
 // straight from global memory into LDS (global_load_lds_dwordx4 /
-// global_load_lds_dword), two slices ahead of the MFMAs, three stages deep.
+// global_load_lds_dword), STAGES - 1 slices ahead of the MFMAs.
 // Rows are 128 bytes; a row's 16-byte chunk c is stored at chunk
 // c ^ swz(row) so the operand reads (16 rows x 16 bytes per 16 lanes) hit 16
 // distinct bank groups.  The transposed product makes each lane own four
@@ -40,7 +41,7 @@ namespace {
 typedef int32_t i32x8 __attribute__((ext_vector_type(8)));
 typedef __attribute__((address_space(3))) void lds_void;
 
-constexpr int kThreads = 256;
+constexpr int kThreads = 256;          // quantisation kernels
 constexpr int kQuantMaxBlocks = TF_FP8_QUANT_WORKSPACE_BYTES / 4;
 constexpr float kFp8Max = 448.f;
 
@@ -122,18 +123,28 @@ __global__ void __launch_bounds__(kThreads) act_quant_kernel(QuantArgs a) {
 }
 
 // ---------------------------------------------------------------- GEMM
-constexpr int kStages = 3;            // K slices resident in LDS (2 staged ahead)
-constexpr int kBN = 128;              // output columns per workgroup
 constexpr int kKSlice = 128;          // K per slice = one weight-scale block
-constexpr int kWBytes = kBN * kKSlice;
-constexpr int kSBytes = 1024;         // 128 column scales, twice
 
-template <int MT>
+// A workgroup of 2 x WN waves owns 32 MT activation rows x 64 WN output
+// columns; wave (wm, wn) holds rows 16 MT wm .. and columns 64 wn .., i.e.
+// 4 x MT 16x16 tiles.  STAGES K slices are resident in LDS, STAGES - 1 staged
+// ahead of the MFMAs.
+template <int MT, int WN, int STAGES>
 struct Tile {
-  static constexpr int kBM = 32 * MT;             // activation rows per workgroup
+  static constexpr int kWaves = 2 * WN;
+  static constexpr int kThreads = kWave * kWaves;
+  static constexpr int kBM = 32 * MT;                       // activation rows
+  static constexpr int kBN = 64 * WN;                       // output columns
   static constexpr int kXBytes = kBM * kKSlice;
+  static constexpr int kWBytes = kBN * kKSlice;
+  static constexpr int kSBytes = kWaves * 256;              // 64 scales per wave
   static constexpr int kStage = kXBytes + kWBytes + kSBytes;
-  static constexpr int kLoads = MT + 4 + 1;       // staging instructions per thread per slice
+  static constexpr int kRowsPerInst = kThreads / 8;         // tile rows per staging instruction
+  static constexpr int kXInst = kBM / kRowsPerInst;
+  static constexpr int kWInst = kBN / kRowsPerInst;
+  static constexpr int kLoads = kXInst + kWInst + 1;        // per thread per slice
+  static constexpr int kAhead = STAGES - 1;
+  static_assert(kBM % kRowsPerInst == 0 && kBN % kRowsPerInst == 0, "staging rows");
 };
 
 struct GemmArgs {
@@ -198,35 +209,38 @@ __device__ __forceinline__ f32x4 mfma_fp8(const i32x8& w, const i32x8& x) {
 
 // kUni: block_h is a multiple of 64, so the 64 columns of a wave share one
 // weight-scale row and the slice's scale is one value per wave.
-template <int MT, bool kUni>
-__global__ void __launch_bounds__(kThreads) fp8_gemm_kernel(GemmArgs a) {
-  using T = Tile<MT>;
-  __shared__ __attribute__((aligned(16))) uint8_t smem[kStages * T::kStage];
+template <int MT, int WN, int STAGES, bool kUni>
+__global__ void __launch_bounds__(2 * kWave * WN)
+fp8_gemm_kernel(GemmArgs a) {
+  using T = Tile<MT, WN, STAGES>;
+  __shared__ __attribute__((aligned(16))) uint8_t smem[STAGES * T::kStage];
   const int t = threadIdx.x, w = wave_id(), l = t & 63;
-  const int wm = w >> 1, wn = w & 1;
+  const int wm = w / WN, wn = w % WN;
   const int m0 = (blockIdx.x % a.tiles_m) * T::kBM;
-  const int n0 = (blockIdx.x / a.tiles_m) * kBN;
+  const int n0 = (blockIdx.x / a.tiles_m) * T::kBN;
 
   const float xsc = *a.x_scale;
   asm volatile("" :: "v"(xsc));   // land the scale before any staging load is in flight
 
-  // Staging: thread t moves 16-byte chunk t % 8 of row 32 i + t / 8 of a tile
-  // (instruction i), fetched from chunk (t % 8) ^ swz(row) of the source row;
-  // rows past the matrix repeat its last row.  Byte offsets fit 32 bits.
+  // Staging: thread t moves 16-byte chunk t % 8 of row kRowsPerInst i + t / 8
+  // of a tile (instruction i), fetched from chunk (t % 8) ^ swz(row) of the
+  // source row (swz(row) depends on t only); rows past the matrix repeat its
+  // last row.  Byte offsets fit 32 bits.
   const int srow = t >> 3;
   const uint32_t cb = 16 * ((t & 7) ^ swz(srow));
-  uint32_t xo[MT], wo[4];
+  uint32_t xo[T::kXInst], wo[T::kWInst];
 #pragma unroll
-  for (int i = 0; i < MT; ++i)
-    xo[i] = (uint32_t)min(m0 + 32 * i + srow, a.M - 1) * (uint32_t)a.xs + cb;
+  for (int i = 0; i < T::kXInst; ++i)
+    xo[i] = (uint32_t)min(m0 + T::kRowsPerInst * i + srow, a.M - 1) * (uint32_t)a.xs + cb;
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
-    wo[i] = (uint32_t)min(n0 + 32 * i + srow, a.N - 1) * (uint32_t)a.wrs + cb;
+  for (int i = 0; i < T::kWInst; ++i)
+    wo[i] = (uint32_t)min(n0 + T::kRowsPerInst * i + srow, a.N - 1) * (uint32_t)a.wrs + cb;
   // Without block scales every lane stages x_scale itself and the staged value
-  // is used as is; otherwise the staged weight scale times x_scale.
+  // is used as is; otherwise the staged weight scale times x_scale.  Wave w
+  // stages the scales of columns 64 (w % WN) ..; waves w >= WN stage a copy.
   const bool ones = a.wsc == nullptr;
   const float sfac = ones ? 1.f : xsc;
-  const int scol = min(n0 + 64 * (w & 1) + l, a.N - 1);
+  const int scol = min(n0 + 64 * wn + l, a.N - 1);
   const uint32_t so = ones ? 0u : (uint32_t)((scol / a.bh) * a.sn) * 4u;
   const uint32_t lds0 = lds_addr(smem);
 
@@ -235,11 +249,12 @@ __global__ void __launch_bounds__(kThreads) fp8_gemm_kernel(GemmArgs a) {
     const uint8_t* xb = a.xq + (int64_t)kb * kKSlice;
     const uint8_t* wb = a.w + (int64_t)kb * kKSlice;
 #pragma unroll
-    for (int i = 0; i < MT; ++i) dma16(xb, xo[i], sb + i * 4096);
+    for (int i = 0; i < T::kXInst; ++i) dma16(xb, xo[i], sb + i * 16 * T::kThreads);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) dma16(wb, wo[i], sb + T::kXBytes + i * 4096);
+    for (int i = 0; i < T::kWInst; ++i)
+      dma16(wb, wo[i], sb + T::kXBytes + i * 16 * T::kThreads);
     const float* sbase = ones ? a.x_scale : a.wsc + (int64_t)(kb / a.bw_slices) * a.sk;
-    dma4(sbase, so, lds0 + st * T::kStage + T::kXBytes + kWBytes + w * 256);
+    dma4(sbase, so, lds0 + st * T::kStage + T::kXBytes + T::kWBytes + w * 256);
   };
 
   // Fragment reads: row l % 16 of a 16-row tile, chunks 2g and 2g + 1.
@@ -258,16 +273,19 @@ __global__ void __launch_bounds__(kThreads) fp8_gemm_kernel(GemmArgs a) {
   // Slices past the last are never read; their stage is refilled with the last
   // slice so that every step issues (and waits for) the same loads.
   const int KB = a.KB;
-  issue(0, 0);
-  issue(min(1, KB - 1), 1);
-  vm_wait<T::kLoads>();
+#pragma unroll
+  for (int i = 0; i < T::kAhead; ++i) issue(min(i, KB - 1), i);
+  if constexpr (T::kAhead == 2)
+    vm_wait<T::kLoads>();
+  else
+    vm_wait<0>();
   __syncthreads();
 
   int st = 0;
   for (int j = 0; j < KB; ++j) {
-    issue(min(j + 2, KB - 1), st == 0 ? 2 : st - 1);
+    issue(min(j + T::kAhead, KB - 1), st == 0 ? STAGES - 1 : st - 1);
     const uint8_t* sp = smem + st * T::kStage;
-    const uint8_t* ssp = sp + T::kXBytes + kWBytes;
+    const uint8_t* ssp = sp + T::kXBytes + T::kWBytes;
     f32x4 s4[4];
     if constexpr (kUni) {
       const float s1 = sfac * *reinterpret_cast<const float*>(ssp + 4 * (wn * 64));
@@ -280,7 +298,8 @@ __global__ void __launch_bounds__(kThreads) fp8_gemm_kernel(GemmArgs a) {
     }
     i32x8 wf[4];
 #pragma unroll
-    for (int tn = 0; tn < 4; ++tn) wf[tn] = frag(sp + T::kXBytes + (wrow + 16 * tn) * kKSlice, o0, o1);
+    for (int tn = 0; tn < 4; ++tn)
+      wf[tn] = frag(sp + T::kXBytes + (wrow + 16 * tn) * kKSlice, o0, o1);
     // Row tm's products are folded in while row tm + 1's MFMAs run.
     f32x4 p[MT][4];
 #pragma unroll
@@ -294,9 +313,12 @@ __global__ void __launch_bounds__(kThreads) fp8_gemm_kernel(GemmArgs a) {
     }
 #pragma unroll
     for (int tn = 0; tn < 4; ++tn) acc[MT - 1][tn] += p[MT - 1][tn] * s4[tn];
-    vm_wait<T::kLoads>();
+    if constexpr (T::kAhead == 2)
+      vm_wait<T::kLoads>();
+    else
+      vm_wait<0>();
     __syncthreads();
-    st = st == kStages - 1 ? 0 : st + 1;
+    st = st == STAGES - 1 ? 0 : st + 1;
   }
   vm_wait<0>();   // the refills of the last steps land before the workgroup ends
 
@@ -330,16 +352,17 @@ __global__ void __launch_bounds__(kThreads) fp8_gemm_kernel(GemmArgs a) {
   }
 }
 
-template <int MT>
+template <int MT, int WN, int STAGES>
 void launch_gemm(const GemmArgs& a, hipStream_t stream) {
+  using T = Tile<MT, WN, STAGES>;
   GemmArgs b = a;
-  b.tiles_m = (a.M + Tile<MT>::kBM - 1) / Tile<MT>::kBM;
-  const int tiles_n = (a.N + kBN - 1) / kBN;
-  const dim3 grid(b.tiles_m * tiles_n), block(kThreads);
+  b.tiles_m = (a.M + T::kBM - 1) / T::kBM;
+  const int tiles_n = (a.N + T::kBN - 1) / T::kBN;
+  const dim3 grid(b.tiles_m * tiles_n), block(T::kThreads);
   if (a.wsc == nullptr || a.bh % 64 == 0)
-    hipLaunchKernelGGL((fp8_gemm_kernel<MT, true>), grid, block, 0, stream, b);
+    hipLaunchKernelGGL((fp8_gemm_kernel<MT, WN, STAGES, true>), grid, block, 0, stream, b);
   else
-    hipLaunchKernelGGL((fp8_gemm_kernel<MT, false>), grid, block, 0, stream, b);
+    hipLaunchKernelGGL((fp8_gemm_kernel<MT, WN, STAGES, false>), grid, block, 0, stream, b);
 }
 
 }  // namespace
@@ -443,13 +466,15 @@ int32_t tf_fp8_block_gemm(const void* xq, int64_t xq_row_stride, const float* x_
   a.tiles_m = 0;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   if (m <= 32)
-    launch_gemm<1>(a, s);
+    launch_gemm<1, 2, 3>(a, s);
   else if (m <= 64)
-    launch_gemm<2>(a, s);
+    launch_gemm<2, 2, 3>(a, s);
   else if (m <= 128)
-    launch_gemm<4>(a, s);
-  else
-    launch_gemm<8>(a, s);
+    launch_gemm<4, 2, 3>(a, s);
+  else if (m <= 1024)
+    launch_gemm<8, 2, 3>(a, s);
+  else   // 8 waves, 256 x 256 tiles, 2 waves per SIMD
+    launch_gemm<8, 4, 2>(a, s);
   return launch_status("tf_fp8_block_gemm launch");
 }
 
