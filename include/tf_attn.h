@@ -316,6 +316,46 @@ int32_t tf_fp8_block_gemm(const void* xq, int64_t xq_row_stride, const float* x_
                           int64_t n, int64_t k, void* out, int64_t out_row_stride,
                           tf_stream_t stream);
 
+/* ------------------------------------------------------------------ Gated DeltaNet decode
+ * One-token step of the linear-attention (Gated DeltaNet) layers for a batch
+ * whose requests all extend by one token: Qwen3_8LinearAttention.
+ * _batched_decode_step (qwen3_8/linear_attention.py:244-298) followed by the
+ * gated RMSNorm (:325, rms_norm_gated.py:26-40); out_proj is left to the caller.
+ *
+ * Request b reads state slot r = req_indices[b] (requests with r outside
+ * [0, n_slots) are skipped and their output rows left untouched):
+ *   conv: y = bf16(silu(bf16(sum_i conv_weight[c][i] * [conv_state[r][c][0..2], qkv[b][c]][i])))
+ *         conv_state[r][c] <- [conv_state[r][c][1..2], qkv[b][c]]
+ *   q, k, v = split(y, [Hk*128, Hk*128, Hv*128]); q = normalize(q) / sqrt(128);
+ *   k = normalize(k); value head h uses key head h / (Hv / Hk);
+ *   alpha = exp(-exp(a_log[h]) * softplus(a[b][h] + dt_bias[h])), beta = sigmoid(b[b][h]);
+ *   S = alpha * ssm_state[r][h]; S += k (beta (v - S^T k))^T; ssm_state[r][h] = S;
+ *   o = bf16(S^T q);  out[b] = bf16(norm_weight * o / rms_head(o) * silu(z[b])).
+ * qkv: bf16 [B, 2*Hk*128 + Hv*128]; a, b: bf16 [B, Hv] (common row stride);
+ * z: bf16 [B, Hv*128]; conv_weight: fp32 [conv_dim, 4] (16-byte aligned);
+ * a_log, dt_bias: fp32 [Hv]; norm_weight: fp32 [Hv*128];
+ * conv_state: bf16 [slots, conv_dim, 3]; ssm_state: fp32 [slots, Hv, 128, 128]
+ * (16-byte aligned), both updated in place, slot strides in elements;
+ * out (and the optional core_out, the pre-norm o): bf16 [B, Hv*128].
+ * workspace: device scratch of tf_gdn_decode_workspace_bytes(B, Hk, Hv) bytes
+ * (the bf16 conv outputs between the two launches; no initialisation needed).
+ * head_k_dim = head_v_dim = 128, conv_kernel = 4.  Requests of one call must
+ * use distinct slots.
+ */
+int64_t tf_gdn_decode_workspace_bytes(int32_t batch_size, int32_t num_k_heads,
+                                      int32_t num_v_heads);
+
+int32_t tf_gdn_decode(const void* qkv, int64_t qkv_row_stride, const void* a, const void* b,
+                      int64_t ab_row_stride, const void* z, int64_t z_row_stride,
+                      const float* conv_weight, const float* a_log, const float* dt_bias,
+                      const float* norm_weight, float eps, void* conv_state,
+                      int64_t conv_slot_stride, float* ssm_state, int64_t ssm_slot_stride,
+                      const int64_t* req_indices, int32_t batch_size, int64_t n_slots,
+                      int32_t num_k_heads, int32_t num_v_heads, int32_t head_k_dim,
+                      int32_t head_v_dim, int32_t conv_kernel, void* out,
+                      int64_t out_row_stride, void* core_out, int64_t core_row_stride,
+                      void* workspace, int64_t workspace_bytes, tf_stream_t stream);
+
 /* ------------------------------------------------------------------ gather
  * Padded slot gather of the batched branches (full_attention.py:216-220):
  * out[b, t] = pool[max(req_to_token[req_pool_indices[b], t], 0)] for

@@ -16,6 +16,9 @@ Modules
     (explicit per request / per query / per head softmax over the visible keys).
 ``kv_quant``
     fp8-e4m3fn per-tensor quantisation of KV rows and its exact dequantisation.
+``gdn``
+    The Gated DeltaNet layer: decode step, chunked WY prefill, causal conv and
+    gated RMSNorm of ``qwen3_8/linear_attention.py`` / ``rms_norm_gated.py``.
 ``fp8_linear``
     The block-FP8 linear (o_proj): dynamic activation quantisation and the
     block-scaled GEMM of ``qwen3_8/fp8_triton.py:17-98, 127-130``.

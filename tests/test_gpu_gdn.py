@@ -1,0 +1,178 @@
+"""Gated DeltaNet decode step on the GPU against the oracle.
+
+Each case runs three consecutive decode steps on the GPU (``tf_gdn_decode``)
+and in the oracle from the same random conv / SSM states, slots scattered over
+a larger pool, and checks after every step:
+
+* conv state: bit-exact (it is a shift of bf16 values);
+* slots no request uses: bit-identical to before;
+* SSM state (fp32): the kernel sums S^T k and S^T q in another order and fuses
+  multiply-adds, and a conv output can round to the neighbouring bf16 value
+  (exp and division are 1-ulp accurate on both sides), which then feeds the
+  update; allowed: |diff| <= 1e-5 max|S| on all but 1e-3 of the elements and
+  <= 1e-2 max|S| everywhere;
+* outputs (bf16, pre-norm and normed): the bf16 bar of 2e-2 absolute /
+  1e-2 relative, with at most 1e-3 of the elements off by more than one
+  bf16 ulp.
+"""
+import pytest
+import torch
+
+from oracle import gdn as og
+from tokenfactory_amd.linear_attention import gdn_decode_step
+
+pytestmark = pytest.mark.gpu
+
+
+def make_params(hk, hv, seed):
+    g = torch.Generator().manual_seed(seed)
+    conv_dim = 2 * hk * 128 + hv * 128
+    # bf16-valued conv taps (the model's dtype): the four-tap sums are exact in fp32
+    conv_w = (torch.randn((conv_dim, 4), generator=g) * 0.5).to(torch.bfloat16).float()
+    a_log = (torch.rand((hv,), generator=g) * 2 - 2.5).to(torch.bfloat16).float()
+    dt_bias = torch.rand((hv,), generator=g).to(torch.bfloat16).float()
+    norm_w = (1 + 0.1 * torch.randn((hv * 128,), generator=g)).to(torch.bfloat16).float()
+    return conv_w, a_log, dt_bias, norm_w
+
+
+def make_step(bsz, hk, hv, seed):
+    g = torch.Generator().manual_seed(seed)
+    conv_dim = 2 * hk * 128 + hv * 128
+    qkv = torch.randn((bsz, conv_dim), generator=g).to(torch.bfloat16)
+    a = torch.randn((bsz, hv), generator=g).to(torch.bfloat16)
+    b = torch.randn((bsz, hv), generator=g).to(torch.bfloat16)
+    z = torch.randn((bsz, hv * 128), generator=g).to(torch.bfloat16)
+    return qkv, a, b, z
+
+
+def close_fraction(got, want, tight, loose, frac, what):
+    d = (got - want).abs()
+    bad = int((d > tight).sum())
+    assert float(d.max()) <= loose, f"{what}: max diff {float(d.max()):.3e} > {loose:.3e}"
+    assert bad <= max(1, int(frac * d.numel())), f"{what}: {bad} of {d.numel()} above {tight:.3e}"
+
+
+def check_outputs(got, want, what):
+    g, w = got.float(), want.float()
+    assert torch.allclose(g, w, atol=2e-2, rtol=1e-2), what
+    ulp = w.abs().clamp_min(2.0 ** -126) * 2.0 ** -7
+    bad = int(((g - w).abs() > ulp).sum())
+    assert bad <= max(1, g.numel() // 1000), f"{what}: {bad} elements off by more than 1 ulp"
+
+
+@pytest.mark.parametrize("bsz,hk,hv", [(1, 16, 48), (7, 16, 48), (64, 16, 48), (9, 4, 12)])
+def test_decode_steps_match_oracle(gpu, bsz, hk, hv):
+    print(f"[gdn] B={bsz} Hk={hk} Hv={hv}", flush=True)
+    n_slots = bsz + 5
+    conv_dim = 2 * hk * 128 + hv * 128
+    g = torch.Generator().manual_seed(bsz * 100 + hk)
+    conv_state = torch.randn((n_slots, conv_dim, 3), generator=g).to(torch.bfloat16)
+    ssm_state = torch.randn((n_slots, hv, 128, 128), generator=g) * 0.2
+    req = torch.randperm(n_slots, generator=g)[:bsz].to(torch.int64)
+    params = make_params(hk, hv, bsz + hv)
+    cs_gpu, ss_gpu = conv_state.to(gpu), ssm_state.to(gpu)
+    gp = [p.to(gpu) for p in params]
+    untouched = torch.ones(n_slots, dtype=torch.bool)
+    untouched[req] = False
+    for step in range(3):
+        qkv, a, b, z = make_step(bsz, hk, hv, 1000 * step + bsz)
+        out, core = gdn_decode_step(qkv.to(gpu), b.to(gpu), a.to(gpu), z.to(gpu), *gp, 1e-6,
+                                    cs_gpu, ss_gpu, req.to(gpu), hk, hv, return_core=True)
+        want_out, want_core = og.gdn_decode(qkv, a, b, z, *params, 1e-6, conv_state, ssm_state,
+                                            req, hk, hv)
+        torch.cuda.synchronize()
+        what = f"B={bsz} Hk={hk} Hv={hv} step {step}"
+        assert torch.equal(cs_gpu.cpu(), conv_state), f"{what}: conv state"
+        ss = ss_gpu.cpu()
+        assert torch.equal(ss[untouched], ssm_state[untouched]), f"{what}: untouched slots"
+        scale = float(ssm_state.abs().max())
+        close_fraction(ss[~untouched], ssm_state[~untouched], 1e-5 * scale, 1e-2 * scale, 1e-3,
+                       f"{what}: ssm state")
+        check_outputs(core.cpu(), want_core, f"{what}: pre-norm output")
+        check_outputs(out.cpu(), want_out, f"{what}: normed output")
+        print(f"[gdn] {what}: max |dS| {float((ss - ssm_state).abs().max()):.2e}", flush=True)
+
+
+def test_out_of_pool_slots_are_skipped(gpu):
+    hk, hv, n_slots = 4, 12, 6
+    conv_dim = 2 * hk * 128 + hv * 128
+    cs = torch.randn((n_slots, conv_dim, 3)).to(torch.bfloat16).to(gpu)
+    ss = torch.randn((n_slots, hv, 128, 128), device=gpu)
+    cs0, ss0 = cs.clone(), ss.clone()
+    qkv, a, b, z = make_step(3, hk, hv, 7)
+    req = torch.tensor([-1, n_slots, 2], dtype=torch.int64, device=gpu)
+    params = [p.to(gpu) for p in make_params(hk, hv, 3)]
+    gdn_decode_step(qkv.to(gpu), b.to(gpu), a.to(gpu), z.to(gpu), *params, 1e-6, cs, ss, req,
+                    hk, hv)
+    torch.cuda.synchronize()
+    keep = torch.tensor([True, True, False, True, True, True])
+    assert torch.equal(cs[keep.to(gpu)], cs0[keep.to(gpu)])
+    assert torch.equal(ss[keep.to(gpu)], ss0[keep.to(gpu)])
+    assert not torch.equal(ss[2], ss0[2])
+
+
+def test_layout_checks(gpu):
+    hk, hv = 4, 12
+    params = [p.to(gpu) for p in make_params(hk, hv, 3)]
+    qkv, a, b, z = (x.to(gpu) for x in make_step(2, hk, hv, 7))
+    cs = torch.zeros((4, 2 * hk * 128 + hv * 128, 3), dtype=torch.bfloat16, device=gpu)
+    ss = torch.zeros((4, hv, 128, 128), device=gpu)
+    req = torch.tensor([0, 1], device=gpu)
+    with pytest.raises(ValueError):
+        gdn_decode_step(qkv, b, a, z, *params, 1e-6, cs, ss.half(), req, hk, hv)
+    ss10 = torch.zeros((4, 10, 128, 128), device=gpu)
+    with pytest.raises(ValueError):            # value heads not a multiple of key heads
+        gdn_decode_step(qkv, b, a, z, *params, 1e-6, cs, ss10, req, 3, 10)
+
+
+class _StatePool:
+    def __init__(self, cs, ss):
+        self.cs, self.ss = cs, ss
+
+    def get_linear_states(self, layer_idx):
+        return self.cs, self.ss
+
+
+def test_linear_attention_module_decode(gpu):
+    """``LinearAttention.forward`` on an all-decode batch equals its own
+    projections -> the oracle's decode step -> its out_proj; an extend batch is
+    refused."""
+    from types import SimpleNamespace
+    from tokenfactory_amd.forward_batch import ForwardBatch
+    from tokenfactory_amd.linear_attention import LinearAttention
+
+    cfg = SimpleNamespace(hidden_size=256, linear_num_key_heads=2, linear_num_value_heads=6,
+                          linear_key_head_dim=128, linear_value_head_dim=128,
+                          linear_conv_kernel_dim=4, rms_norm_eps=1e-6, tp_size=1)
+    torch.manual_seed(0)
+    mod = LinearAttention(cfg, layer_idx=0).to(gpu)
+    with torch.no_grad():
+        for p in mod.parameters():
+            p.copy_((torch.randn_like(p.float()) * 0.1).to(p.dtype))
+        mod.A_log.fill_(-1.0)
+    bsz, n_slots = 5, 9
+    cs = torch.randn((n_slots, mod.conv_dim, 3)).to(torch.bfloat16)
+    ss = torch.randn((n_slots, 6, 128, 128)) * 0.2
+    pool = _StatePool(cs.to(gpu), ss.to(gpu))
+    req = torch.tensor([7, 0, 3, 8, 2], dtype=torch.int64)
+    batch = ForwardBatch(batch_size=bsz, req_pool_indices=req.to(gpu),
+                         seq_lens=torch.full((bsz,), 10, device=gpu),
+                         prefix_lens=torch.full((bsz,), 9, device=gpu), extend_lens=[1] * bsz,
+                         out_cache_loc=torch.zeros((bsz,), dtype=torch.int64, device=gpu),
+                         req_to_token=torch.zeros((n_slots, 16), dtype=torch.int64, device=gpu),
+                         is_prefill=False)
+    hidden = (torch.randn((bsz, 256)) * 0.5).to(torch.bfloat16).to(gpu)
+    with torch.no_grad():
+        got = mod(hidden, pool, batch)
+        qkv, z = mod.in_proj_qkv(hidden), mod.in_proj_z(hidden)
+        b, a = mod.in_proj_b(hidden), mod.in_proj_a(hidden)
+        conv_w, a_log, dt_bias, norm_w = (t.cpu() for t in mod._kernel_params())
+        core_out, _ = og.gdn_decode(qkv.cpu(), a.cpu(), b.cpu(), z.cpu(), conv_w, a_log, dt_bias,
+                                    norm_w, 1e-6, cs, ss, req, 2, 6)
+        want = mod.out_proj(core_out.to(gpu))
+    torch.cuda.synchronize()
+    assert torch.allclose(got.float(), want.float(), atol=2e-2, rtol=1e-2)
+    assert torch.equal(pool.cs.cpu(), cs)
+    batch.extend_lens = [1, 1, 2, 1, 1]
+    with pytest.raises(NotImplementedError):
+        mod(hidden, pool, batch)

@@ -19,7 +19,7 @@ CSRC = PKG_DIR / "csrc"
 LIB_DIR = PKG_DIR / "_lib"
 LIB_PATH = LIB_DIR / "libtf_attn.so"
 SOURCES = ["abi.hip", "decode.hip", "extend.hip", "extend_bf16.hip", "fp8_linear.hip",
-           "kv_ops.hip", "plan.hip", "qk_prep.hip"]
+           "gdn.hip", "kv_ops.hip", "plan.hip", "qk_prep.hip"]
 ARCH = "gfx950"
 
 

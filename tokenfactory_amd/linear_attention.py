@@ -1,0 +1,161 @@
+"""Gated DeltaNet (linear-attention) decode step on the gfx950 kernel.
+
+``gdn_decode_step`` is the native counterpart of
+``Qwen3_8LinearAttention._batched_decode_step`` (``qwen3_8/linear_attention.py:244-298``)
+followed by ``self.norm(attn_out, z)`` (``:325``): one fused launch
+(``tf_gdn_decode``) does the causal-conv step, q/k normalisation, the gated
+delta-rule state update, the readout and the gated RMSNorm, updating the
+layer's conv and SSM states in place.
+
+``LinearAttention`` mirrors ``Qwen3_8LinearAttention``'s parameters
+(``:29-107``: ``in_proj_qkv``, ``in_proj_z``, ``in_proj_b``, ``in_proj_a``,
+``conv1d``, ``A_log``, ``dt_bias``, ``norm.weight``, ``out_proj``) and its
+``forward(hidden_states, cache_pool, forward_batch)`` for batches whose
+requests all extend by one token. The chunked prefill of longer extends has no
+native kernel here; such batches raise ``NotImplementedError`` rather than
+running anything else.
+"""
+from __future__ import annotations
+
+from typing import Optional
+
+import torch
+import torch.nn as nn
+
+from . import _native
+from .fp8_linear import Fp8Linear
+
+HEAD_DIM = 128
+CONV_KERNEL = 4
+
+
+def _ptr(t: Optional[torch.Tensor]) -> int:
+    return 0 if t is None else t.data_ptr()
+
+
+def _rows(t: torch.Tensor, name: str) -> int:
+    if t.dim() != 2 or t.stride(1) != 1:
+        raise ValueError(f"gdn_decode_step: {name} must be 2-D with contiguous rows")
+    return t.stride(0)
+
+
+def gdn_decode_step(qkv: torch.Tensor, b: torch.Tensor, a: torch.Tensor, z: torch.Tensor,
+                    conv_weight: torch.Tensor, a_log: torch.Tensor, dt_bias: torch.Tensor,
+                    norm_weight: torch.Tensor, eps: float, layer_conv_state: torch.Tensor,
+                    layer_ssm_state: torch.Tensor, req_indices: torch.Tensor,
+                    num_k_heads: int, num_v_heads: int, return_core: bool = False,
+                    stream=None):
+    """One decode step of a Gated DeltaNet layer for B requests (one token each).
+
+    qkv bf16 [B, 2*Hk*128 + Hv*128], b / a bf16 [B, Hv], z bf16 [B, Hv*128];
+    conv_weight fp32 [conv_dim, 4]; a_log, dt_bias fp32 [Hv]; norm_weight fp32
+    [Hv*128]; layer_conv_state bf16 [slots, conv_dim, 3] and layer_ssm_state
+    fp32 [slots, Hv, 128, 128] (updated in place); req_indices int64 [B] (distinct).
+    Returns the normed bf16 output [B, Hv*128] (and the pre-norm output)."""
+    bsz = qkv.shape[0]
+    value_dim = num_v_heads * HEAD_DIM
+    for name, t, dt in (("qkv", qkv, torch.bfloat16), ("b", b, torch.bfloat16),
+                        ("a", a, torch.bfloat16), ("z", z, torch.bfloat16),
+                        ("conv_weight", conv_weight, torch.float32),
+                        ("a_log", a_log, torch.float32), ("dt_bias", dt_bias, torch.float32),
+                        ("norm_weight", norm_weight, torch.float32),
+                        ("layer_conv_state", layer_conv_state, torch.bfloat16),
+                        ("layer_ssm_state", layer_ssm_state, torch.float32),
+                        ("req_indices", req_indices, torch.int64)):
+        if t.dtype != dt or not t.is_cuda:
+            raise ValueError(f"gdn_decode_step: {name} must be a {dt} CUDA tensor")
+    if a.stride() != b.stride() or a.shape != b.shape:
+        raise ValueError("gdn_decode_step: a and b must share shape and strides")
+    for name, t in (("conv_weight", conv_weight), ("a_log", a_log), ("dt_bias", dt_bias),
+                    ("norm_weight", norm_weight), ("req_indices", req_indices)):
+        if not t.is_contiguous():
+            raise ValueError(f"gdn_decode_step: {name} must be contiguous")
+    cs, ss = layer_conv_state, layer_ssm_state
+    if cs.dim() != 3 or cs.stride(2) != 1 or cs.stride(1) != CONV_KERNEL - 1:
+        raise ValueError("gdn_decode_step: conv state must be [slots, conv_dim, 3] with dense rows")
+    if ss.dim() != 4 or ss[0].numel() != value_dim * HEAD_DIM or not ss[0].is_contiguous():
+        raise ValueError("gdn_decode_step: ssm state must be [slots, Hv, 128, 128], dense per slot")
+    out = torch.empty((bsz, value_dim), dtype=torch.bfloat16, device=qkv.device)
+    core = torch.empty_like(out) if return_core else None
+    ws = torch.empty((bsz, 2 * num_k_heads * HEAD_DIM + value_dim), dtype=torch.bfloat16,
+                     device=qkv.device)
+    s = stream if stream is not None else torch.cuda.current_stream(qkv.device)
+    _native.call("tf_gdn_decode", _ptr(qkv), _rows(qkv, "qkv"), _ptr(a), _ptr(b),
+                 _rows(a, "a"), _ptr(z), _rows(z, "z"), _ptr(conv_weight), _ptr(a_log),
+                 _ptr(dt_bias), _ptr(norm_weight), float(eps), _ptr(cs), cs.stride(0), _ptr(ss),
+                 ss.stride(0), _ptr(req_indices), bsz, cs.shape[0], num_k_heads, num_v_heads,
+                 HEAD_DIM, HEAD_DIM, CONV_KERNEL, _ptr(out), out.stride(0), _ptr(core),
+                 0 if core is None else core.stride(0), _ptr(ws), ws.numel() * 2,
+                 s.cuda_stream)
+    return (out, core) if return_core else out
+
+
+class LinearAttention(nn.Module):
+    """Gated DeltaNet layer with ``Qwen3_8LinearAttention``'s parameter names and
+    shapes (one TP rank's share; ``qwen3_8/linear_attention.py:29-107``)."""
+
+    def __init__(self, config, layer_idx: int, dtype: torch.dtype = torch.bfloat16):
+        super().__init__()
+        tp = getattr(config, "tp_size", 1)
+        self.layer_idx = layer_idx
+        self.num_k_heads = config.linear_num_key_heads // tp
+        self.num_v_heads = config.linear_num_value_heads // tp
+        if (config.linear_key_head_dim != HEAD_DIM or config.linear_value_head_dim != HEAD_DIM
+                or config.linear_conv_kernel_dim != CONV_KERNEL):
+            raise NotImplementedError("LinearAttention: head dims 128 and conv kernel 4 only")
+        self.key_dim = self.num_k_heads * HEAD_DIM
+        self.value_dim = self.num_v_heads * HEAD_DIM
+        self.conv_dim = 2 * self.key_dim + self.value_dim
+        self.eps = getattr(config, "rms_norm_eps", 1e-6)
+        hidden = config.hidden_size
+        q = getattr(config, "quantization_config", None)
+        if isinstance(q, dict) and q.get("quant_method") == "fp8":
+            block = tuple(q.get("weight_block_size", [128, 128]))
+            self.in_proj_qkv = Fp8Linear(hidden, self.conv_dim, block_size=block)
+            self.in_proj_z = Fp8Linear(hidden, self.value_dim, block_size=block)
+            self.out_proj = Fp8Linear(self.value_dim, hidden, block_size=block)
+        else:
+            self.in_proj_qkv = nn.Linear(hidden, self.conv_dim, bias=False, dtype=dtype)
+            self.in_proj_z = nn.Linear(hidden, self.value_dim, bias=False, dtype=dtype)
+            self.out_proj = nn.Linear(self.value_dim, hidden, bias=False, dtype=dtype)
+        self.in_proj_b = nn.Linear(hidden, self.num_v_heads, bias=False, dtype=dtype)
+        self.in_proj_a = nn.Linear(hidden, self.num_v_heads, bias=False, dtype=dtype)
+        self.conv1d = nn.Conv1d(self.conv_dim, self.conv_dim, kernel_size=CONV_KERNEL,
+                                groups=self.conv_dim, padding=CONV_KERNEL - 1, bias=False,
+                                dtype=dtype)
+        self.A_log = nn.Parameter(torch.zeros(self.num_v_heads, dtype=dtype))
+        self.dt_bias = nn.Parameter(torch.ones(self.num_v_heads, dtype=dtype))
+        self.norm = nn.Module()
+        self.norm.weight = nn.Parameter(torch.ones(self.value_dim, dtype=dtype))
+        self._packed = None
+        self._packed_key = None
+
+    def _kernel_params(self):
+        """fp32 copies of the conv taps, A_log, dt_bias and norm weight (exact
+        for bf16 parameters), rebuilt when a parameter changes."""
+        params = (self.conv1d.weight, self.A_log, self.dt_bias, self.norm.weight)
+        key = tuple((p.data_ptr(), p._version, p.device) for p in params)
+        if self._packed_key != key:
+            self._packed = (
+                self.conv1d.weight.detach().float().reshape(self.conv_dim, CONV_KERNEL).contiguous(),
+                self.A_log.detach().float().contiguous(),
+                self.dt_bias.detach().float().contiguous(),
+                self.norm.weight.detach().float().contiguous())
+            self._packed_key = key
+        return self._packed
+
+    def forward(self, hidden_states: torch.Tensor, cache_pool, forward_batch) -> torch.Tensor:
+        if not all(e == 1 for e in forward_batch.extend_lens):
+            raise NotImplementedError(
+                "LinearAttention: only all-decode batches run natively (the chunked "
+                "Gated DeltaNet prefill has no kernel here)")
+        qkv = self.in_proj_qkv(hidden_states)
+        z = self.in_proj_z(hidden_states)
+        b = self.in_proj_b(hidden_states)
+        a = self.in_proj_a(hidden_states)
+        conv_state, ssm_state = cache_pool.get_linear_states(self.layer_idx)
+        conv_w, a_log, dt_bias, norm_w = self._kernel_params()
+        attn = gdn_decode_step(qkv, b, a, z, conv_w, a_log, dt_bias, norm_w, self.eps,
+                               conv_state, ssm_state, forward_batch.req_pool_indices,
+                               self.num_k_heads, self.num_v_heads)
+        return self.out_proj(attn)
