@@ -342,10 +342,29 @@ def bench_gdn(torch, args):
     ref_ms = time_steps(torch, [None], steps, max(1, args.warmup), lambda c: [ref_ops])
     log(f"gdn decode B={bsz}: fused kernel {t*1e3:.1f} us = {gbps:.0f} GB/s "
         f"({gbps * 1e9 / HBM_PEAK * 100:.1f}% of HBM peak); reference ops {ref_ms*1e3:.1f} us")
-    return {"workload": "Gated DeltaNet decode step: 64 requests, 16 key / 48 value heads of "
-                        "128, fp32 128x128 states scattered in a 256-slot pool, bf16 conv state",
-            "kernel_ms": t, "bytes_per_launch": state_bytes + other, "gbps": gbps,
-            "frac_of_hbm_peak": gbps * 1e9 / HBM_PEAK, "reference_ops_ms": ref_ms}
+    res = {"workload": "Gated DeltaNet decode step: 64 requests, 16 key / 48 value heads of "
+                       "128, fp32 128x128 states scattered in a 256-slot pool, bf16 conv state",
+           "kernel_ms": t, "bytes_per_launch": state_bytes + other, "gbps": gbps,
+           "frac_of_hbm_peak": gbps * 1e9 / HBM_PEAK, "reference_ops_ms": ref_ms}
+
+    # the mixed step's shape: 4 requests extending by 2048 tokens + 128 decodes
+    from tokenfactory_amd.linear_attention import gdn_extend_step
+    lens = [2048] * 4 + [1] * 128
+    n_tok = sum(lens)
+    req = torch.randperm(slots, device="cuda", generator=g)[:len(lens)]
+    qkv = rnd(n_tok, conv_dim).to(torch.bfloat16)
+    a, b = rnd(n_tok, hv).to(torch.bfloat16), rnd(n_tok, hv).to(torch.bfloat16)
+    z = rnd(n_tok, hv * 128).to(torch.bfloat16)
+    ext = lambda _: gdn_extend_step(qkv, b, a, z, conv_w, a_log, dt_bias, norm_w, 1e-6, cs, ss,
+                                    req, lens, hk, hv)
+    time_kernel(torch, [None], 2, ext)
+    te = time_kernel(torch, [None], max(3, steps // 4), ext)
+    log(f"gdn extend (4 x 2048 + 128 x 1 tokens): {te*1e3:.1f} us, "
+        f"{n_tok / (te * 1e-3) / 1e6:.2f} M tokens/s, {te * 1e6 / 2048:.0f} ns per token of "
+        f"the longest request")
+    res["extend_mixed"] = {"workload": "4 requests x 2048 new tokens + 128 decodes, same heads",
+                           "ms": te, "tokens_per_s": n_tok / (te * 1e-3)}
+    return res
 
 
 def bench_plan(torch, workloads, SlotAttentionCall, args):

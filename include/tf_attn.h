@@ -356,6 +356,41 @@ int32_t tf_gdn_decode(const void* qkv, int64_t qkv_row_stride, const void* a, co
                       int64_t out_row_stride, void* core_out, int64_t core_row_stride,
                       void* workspace, int64_t workspace_bytes, tf_stream_t stream);
 
+/* ------------------------------------------------------------------ Gated DeltaNet extend
+ * The same layer for a batch with any extend lengths: the reference's
+ * per-request loop (linear_attention.py:328-364: _causal_conv1d_step,
+ * _gated_delta_rule_step, then the gated norm).  Request b owns the token rows
+ * token_offsets[b] .. token_offsets[b + 1] - 1 of qkv, a, b, z and out
+ * (device int32 [batch_size + 1], non-decreasing, clamped into [0, n_tokens]);
+ * max_extend_len: the largest extend length (host int; longer requests are
+ * only partly convolved);
+ * its conv runs over [conv_state, its tokens] and its state is carried through
+ * its tokens in order.  The chunked WY update of the reference (:194-242) and
+ * the token-by-token recurrence computed here are the same recurrence (equal
+ * up to fp32 rounding).  Five launches: the conv for every (token, channel)
+ * in parallel, the conv-state shift, normalised q / k and the gates for every
+ * token in parallel, the recurrence (one workgroup per request and value head,
+ * its state in registers from first token to last) and the gated norm for
+ * every token in parallel.  Other arguments as for tf_gdn_decode, with rows =
+ * tokens; workspace: tf_gdn_extend_workspace_bytes(n_tokens, Hk, Hv) bytes,
+ * 16-byte aligned.
+ */
+int64_t tf_gdn_extend_workspace_bytes(int64_t n_tokens, int32_t num_k_heads,
+                                      int32_t num_v_heads);
+
+int32_t tf_gdn_extend(const void* qkv, int64_t qkv_row_stride, const void* a, const void* b,
+                      int64_t ab_row_stride, const void* z, int64_t z_row_stride,
+                      const float* conv_weight, const float* a_log, const float* dt_bias,
+                      const float* norm_weight, float eps, void* conv_state,
+                      int64_t conv_slot_stride, float* ssm_state, int64_t ssm_slot_stride,
+                      const int64_t* req_indices, const int32_t* token_offsets,
+                      int32_t batch_size, int64_t n_tokens, int32_t max_extend_len,
+                      int64_t n_slots,
+                      int32_t num_k_heads, int32_t num_v_heads, int32_t head_k_dim,
+                      int32_t head_v_dim, int32_t conv_kernel, void* out,
+                      int64_t out_row_stride, void* core_out, int64_t core_row_stride,
+                      void* workspace, int64_t workspace_bytes, tf_stream_t stream);
+
 /* ------------------------------------------------------------------ gather
  * Padded slot gather of the batched branches (full_attention.py:216-220):
  * out[b, t] = pool[max(req_to_token[req_pool_indices[b], t], 0)] for

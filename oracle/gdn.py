@@ -161,3 +161,41 @@ def gdn_decode(qkv, a, b, z, conv_weight, a_log, dt_bias, norm_weight, eps, conv
     core = torch.stack(outs).reshape(bsz, num_v_heads * DV).to(torch.bfloat16)
     out = rms_norm_gated(core, z.cpu(), norm_weight.cpu(), eps)
     return out, core
+
+
+def gdn_extend(qkv, a, b, z, conv_weight, a_log, dt_bias, norm_weight, eps, conv_state,
+               ssm_state, req_indices, extend_lens, num_k_heads, num_v_heads):
+    """The reference's per-request loop for a batch with any extend lengths
+    (``linear_attention.py:328-364``): ``_causal_conv1d_step`` and
+    ``_gated_delta_rule_step`` (chunked WY for ``ext_len > 1``, the one-step
+    formula for ``ext_len == 1``) per request, then the gated norm over all rows.
+    States are updated in place (CPU tensors). Returns ``(out, core)``."""
+    key_dim = num_k_heads * DK
+    vpk = num_v_heads // num_k_heads
+    outs, off = [], 0
+    for i, e in enumerate(extend_lens):
+        r = int(req_indices[i])
+        rows = slice(off, off + e)
+        off += e
+        conv_out, new_state = causal_conv_prefill(qkv[rows].cpu(), conv_state[r],
+                                                  conv_weight.cpu())
+        conv_state[r] = new_state
+        q, k, v = conv_out.split([key_dim, key_dim, num_v_heads * DV], dim=-1)
+        q = q.view(e, num_k_heads, DK)
+        k = k.view(e, num_k_heads, DK)
+        v = v.view(e, num_v_heads, DV)
+        if e == 1:                           # :184-192
+            qn, kn = normalize_qk(q[0], k[0])
+            decay, beta = gates(a[rows].cpu()[0], b[rows].cpu()[0], a_log.cpu(), dt_bias.cpu())
+            o, s = delta_rule_decode(torch.repeat_interleave(qn, vpk, 0),
+                                     torch.repeat_interleave(kn, vpk, 0), v[0],
+                                     torch.exp(decay), beta, ssm_state[r])
+            ssm_state[r] = s
+            o = o.unsqueeze(0)
+        else:
+            o = gated_delta_rule_chunked(q, k, v, b[rows].cpu(), a[rows].cpu(), ssm_state[r],
+                                         a_log.cpu(), dt_bias.cpu(), vpk)
+        outs.append(o.reshape(e, num_v_heads * DV).to(torch.bfloat16))
+    core = torch.cat(outs, dim=0)
+    return rms_norm_gated(core, z.cpu(), norm_weight.cpu(), eps), core
+

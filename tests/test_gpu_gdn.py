@@ -19,7 +19,7 @@ import pytest
 import torch
 
 from oracle import gdn as og
-from tokenfactory_amd.linear_attention import gdn_decode_step
+from tokenfactory_amd.linear_attention import gdn_decode_step, gdn_extend_step
 
 pytestmark = pytest.mark.gpu
 
@@ -93,6 +93,60 @@ def test_decode_steps_match_oracle(gpu, bsz, hk, hv):
         print(f"[gdn] {what}: max |dS| {float((ss - ssm_state).abs().max()):.2e}", flush=True)
 
 
+@pytest.mark.parametrize("lens,hk,hv", [([5], 16, 48), ([1, 70, 3, 130], 16, 48),
+                                         ([200, 1, 1, 64, 2], 4, 12)])
+def test_extend_matches_oracle(gpu, lens, hk, hv):
+    """Mixed extend lengths against the oracle's per-request loop (chunked WY
+    update for ext > 1): two consecutive calls, the second with other lengths.
+    The kernel carries the state token by token; against the chunked form the
+    fp32 state agrees to ~1e-4 relative (allowed: 2e-4 max|S| on all but 1e-3 of
+    the elements)."""
+    print(f"[gdn extend] lens={lens} Hk={hk} Hv={hv}", flush=True)
+    n_slots = len(lens) + 3
+    conv_dim = 2 * hk * 128 + hv * 128
+    g = torch.Generator().manual_seed(sum(lens) + hk)
+    conv_state = torch.randn((n_slots, conv_dim, 3), generator=g).to(torch.bfloat16)
+    ssm_state = torch.randn((n_slots, hv, 128, 128), generator=g) * 0.2
+    req = torch.randperm(n_slots, generator=g)[:len(lens)].to(torch.int64)
+    params = make_params(hk, hv, len(lens) + hv)
+    cs_gpu, ss_gpu = conv_state.to(gpu), ssm_state.to(gpu)
+    gp = [p.to(gpu) for p in params]
+    for call, ls in enumerate((lens, [max(1, e // 2) for e in reversed(lens)])):
+        qkv, a, b, z = make_step(sum(ls), hk, hv, 77 + call)
+        out, core = gdn_extend_step(qkv.to(gpu), b.to(gpu), a.to(gpu), z.to(gpu), *gp, 1e-6,
+                                    cs_gpu, ss_gpu, req.to(gpu), ls, hk, hv, return_core=True)
+        want_out, want_core = og.gdn_extend(qkv, a, b, z, *params, 1e-6, conv_state, ssm_state,
+                                            req, ls, hk, hv)
+        torch.cuda.synchronize()
+        what = f"lens={ls} call {call}"
+        assert torch.equal(cs_gpu.cpu(), conv_state), f"{what}: conv state"
+        scale = float(ssm_state.abs().max())
+        close_fraction(ss_gpu.cpu(), ssm_state, 2e-4 * scale, 1e-2 * scale, 1e-3,
+                       f"{what}: ssm state")
+        check_outputs(core.cpu(), want_core, f"{what}: pre-norm output")
+        check_outputs(out.cpu(), want_out, f"{what}: normed output")
+
+
+def test_extend_of_single_tokens_equals_decode(gpu):
+    hk, hv, bsz = 16, 48, 6
+    conv_dim = 2 * hk * 128 + hv * 128
+    g = torch.Generator().manual_seed(11)
+    cs = torch.randn((bsz + 2, conv_dim, 3), generator=g).to(torch.bfloat16).to(gpu)
+    ss = (torch.randn((bsz + 2, hv, 128, 128), generator=g) * 0.2).to(gpu)
+    cs2, ss2 = cs.clone(), ss.clone()
+    req = torch.tensor([3, 0, 7, 1, 5, 2], device=gpu)
+    gp = [p.to(gpu) for p in make_params(hk, hv, 4)]
+    qkv, a, b, z = (x.to(gpu) for x in make_step(bsz, hk, hv, 12))
+    o1 = gdn_decode_step(qkv, b, a, z, *gp, 1e-6, cs, ss, req, hk, hv)
+    o2 = gdn_extend_step(qkv, b, a, z, *gp, 1e-6, cs2, ss2, req, [1] * bsz, hk, hv)
+    torch.cuda.synchronize()
+    # same math; the two recurrence kernels split the row reductions differently
+    assert torch.equal(cs, cs2)
+    scale = float(ss.abs().max())
+    close_fraction(ss2.cpu(), ss.cpu(), 1e-6 * scale, 1e-5 * scale, 1e-3, "ssm state")
+    check_outputs(o2.cpu(), o1.cpu(), "output")
+
+
 def test_out_of_pool_slots_are_skipped(gpu):
     hk, hv, n_slots = 4, 12, 6
     conv_dim = 2 * hk * 128 + hv * 128
@@ -134,9 +188,8 @@ class _StatePool:
 
 
 def test_linear_attention_module_decode(gpu):
-    """``LinearAttention.forward`` on an all-decode batch equals its own
-    projections -> the oracle's decode step -> its out_proj; an extend batch is
-    refused."""
+    """``LinearAttention.forward`` equals its own projections -> the oracle's
+    step -> its out_proj, on an all-decode batch and then on a mixed batch."""
     from types import SimpleNamespace
     from tokenfactory_amd.forward_batch import ForwardBatch
     from tokenfactory_amd.linear_attention import LinearAttention
@@ -173,6 +226,17 @@ def test_linear_attention_module_decode(gpu):
     torch.cuda.synchronize()
     assert torch.allclose(got.float(), want.float(), atol=2e-2, rtol=1e-2)
     assert torch.equal(pool.cs.cpu(), cs)
-    batch.extend_lens = [1, 1, 2, 1, 1]
-    with pytest.raises(NotImplementedError):
-        mod(hidden, pool, batch)
+    # a mixed batch: the extend path, against the oracle's per-request loop
+    lens = [1, 4, 1, 9, 2]
+    hidden = (torch.randn((sum(lens), 256)) * 0.5).to(torch.bfloat16).to(gpu)
+    batch.extend_lens = lens
+    with torch.no_grad():
+        got = mod(hidden, pool, batch)
+        qkv, z = mod.in_proj_qkv(hidden), mod.in_proj_z(hidden)
+        b, a = mod.in_proj_b(hidden), mod.in_proj_a(hidden)
+        core_out, _ = og.gdn_extend(qkv.cpu(), a.cpu(), b.cpu(), z.cpu(), conv_w, a_log,
+                                    dt_bias, norm_w, 1e-6, cs, ss, req, lens, 2, 6)
+        want = mod.out_proj(core_out.to(gpu))
+    torch.cuda.synchronize()
+    assert torch.allclose(got.float(), want.float(), atol=2e-2, rtol=1e-2)
+    assert torch.equal(pool.cs.cpu(), cs)

@@ -12,7 +12,7 @@ from pathlib import Path
 from typing import Optional
 
 LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libtf_attn.so"
-ABI_VERSION = 7
+ABI_VERSION = 8
 
 TF_DTYPE_BF16 = 0
 TF_DTYPE_FP8_E4M3 = 1
@@ -110,6 +110,18 @@ SIGNATURES = {
         _p, _i64, _p,                  # workspace, workspace_bytes, stream
     ]),
     "tf_gdn_decode_workspace_bytes": (_i64, [_i32, _i32, _i32]),
+    "tf_gdn_extend": (_i32, [
+        _p, _i64, _p, _p, _i64,        # qkv, qkv_row_stride, a, b, ab_row_stride
+        _p, _i64,                      # z, z_row_stride
+        _p, _p, _p, _p, _f32,          # conv_weight, a_log, dt_bias, norm_weight, eps
+        _p, _i64, _p, _i64,            # conv_state, its slot stride, ssm_state, its slot stride
+        _p, _p, _i32, _i64, _i32, _i64,  # req_indices, token_offsets, batch, n_tokens,
+                                         # max_extend_len, n_slots
+        _i32, _i32, _i32, _i32, _i32,  # num_k_heads, num_v_heads, head_k/v_dim, conv_kernel
+        _p, _i64, _p, _i64,            # out, out_row_stride, core_out, core_row_stride
+        _p, _i64, _p,                  # workspace, workspace_bytes, stream
+    ]),
+    "tf_gdn_extend_workspace_bytes": (_i64, [_i64, _i32, _i32]),
     "tf_gather_kv": (_i32, [
         _p, _i32, _i64, _i64,          # pool, kv_dtype, pool_slots, row_elems
         _p, _i64, _i64, _i64,          # req_to_token, rtt_rows, rtt_row_stride, rtt_cols

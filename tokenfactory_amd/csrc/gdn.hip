@@ -56,7 +56,13 @@ struct GdnArgs {
   const int64_t* req;
   int64_t n_slots;
   int32_t batch, hv, vpk, key_dim, conv_dim;
-  uint16_t* ws;          // bf16 [B, conv_dim]: conv + SiLU outputs
+  int32_t hk;
+  float* wqk;            // extend: fp32 [rows, Hk, 256] normalised q then k, rows permuted
+  float* wg;             // extend: fp32 [rows, Hv, 2] alpha, beta
+  uint16_t* wcore;       // extend: bf16 [rows, Hv * Dv] recurrence output
+  const int32_t* tok;    // extend: request b owns token rows tok[b] .. tok[b + 1] - 1
+  int32_t rows;          // token rows of qkv / a / b / z / out (offsets are clamped to it)
+  uint16_t* ws;          // bf16 [rows, conv_dim]: conv + SiLU outputs
   uint16_t* out;         // bf16 [B, Hv * Dv]
   int64_t out_rs;
   uint16_t* core;        // optional bf16 [B, Hv * Dv]: o before the norm
@@ -185,6 +191,233 @@ __global__ void __launch_bounds__(kThreads) gdn_recur_kernel(GdnArgs a) {
   }
 }
 
+// ---------------------------------------------------------------- extend
+// Requests with several new tokens (the reference's per-request loop,
+// linear_attention.py:328-364): the conv walks each request's tokens with a
+// sliding window (one thread per (request, channel), so the channel's conv
+// state is read and written by that thread alone), and the recurrence walks
+// them with the head's state held in registers from the first token to the
+// last (one state read and one write per request and head).  The token
+// recurrence is the reference's chunked WY update (:194-242) computed one
+// token at a time; both are the same linear recurrence.
+
+constexpr int kConvTokens = 16;   // tokens per thread in the extend conv
+
+// Conv + SiLU of kConvTokens consecutive tokens of one request for one channel
+// per thread (grid: channel blocks x requests x token blocks).  The window
+// before the request's first token comes from the conv state, which this
+// kernel only reads; gdn_conv_state_kernel shifts it afterwards.
+__global__ void __launch_bounds__(kThreads) gdn_conv_ext_kernel(GdnArgs a) {
+  const int c = blockIdx.x * kThreads + threadIdx.x, bi = blockIdx.y;
+  if (c >= a.conv_dim) return;
+  const int64_t r = a.req[bi];
+  if (r < 0 || r >= a.n_slots) return;
+  const int t0 = min(max(a.tok[bi], 0), a.rows), t1 = min(max(a.tok[bi + 1], t0), a.rows);
+  const int tb = t0 + blockIdx.z * kConvTokens;
+  if (tb >= t1) return;
+  const uint16_t* st = a.conv_state + r * a.conv_ss + 3 * (int64_t)c;
+  uint16_t x[kConvTokens + 3];
+#pragma unroll
+  for (int i = 0; i < 3; ++i) {
+    const int tt = tb - 3 + i;
+    x[i] = tt >= t0 ? a.qkv[tt * a.qkv_rs + c] : st[tt - t0 + 3];
+  }
+#pragma unroll
+  for (int i = 0; i < kConvTokens; ++i)
+    x[3 + i] = tb + i < t1 ? a.qkv[(tb + i) * a.qkv_rs + c] : (uint16_t)0;
+  const f32x4 w = *reinterpret_cast<const f32x4*>(a.conv_w + 4 * (int64_t)c);
+#pragma unroll
+  for (int i = 0; i < kConvTokens; ++i) {
+    if (tb + i >= t1) break;
+    const float acc = w[0] * bf(x[i]) + w[1] * bf(x[i + 1]) + w[2] * bf(x[i + 2]) +
+                      w[3] * bf(x[i + 3]);
+    const float y = round_bf(acc);
+    a.ws[(int64_t)(tb + i) * a.conv_dim + c] = to_bf(y / (1.f + expf(-y)));
+  }
+}
+
+// Conv state <- the last 3 inputs of each request (after gdn_conv_ext_kernel
+// has read the old state).
+__global__ void __launch_bounds__(kThreads) gdn_conv_state_kernel(GdnArgs a) {
+  const int c = blockIdx.x * kThreads + threadIdx.x, bi = blockIdx.y;
+  if (c >= a.conv_dim) return;
+  const int64_t r = a.req[bi];
+  if (r < 0 || r >= a.n_slots) return;
+  const int t0 = min(max(a.tok[bi], 0), a.rows), t1 = min(max(a.tok[bi + 1], t0), a.rows);
+  uint16_t* st = a.conv_state + r * a.conv_ss + 3 * (int64_t)c;
+  uint16_t x[3];
+#pragma unroll
+  for (int i = 0; i < 3; ++i) {
+    const int tt = t1 - 3 + i;           // position in [state, tokens]
+    x[i] = tt >= t0 ? a.qkv[tt * a.qkv_rs + c] : st[tt - t0 + 3];
+  }
+#pragma unroll
+  for (int i = 0; i < 3; ++i) st[i] = x[i];
+}
+
+// Per (token, key head): q / k of the head normalised (F.normalize, eps
+// 1e-12; q also scaled by dk^-0.5) as fp32, and per value head of the group
+// alpha = exp(decay) and beta.  None of it depends on the state, so it runs for
+// all tokens in parallel ahead of the recurrence.
+__global__ void __launch_bounds__(kThreads) gdn_qk_ext_kernel(GdnArgs a) {
+  __shared__ float s_sum[2][4];
+  const int tok = blockIdx.x, t = threadIdx.x;
+  const uint16_t* y = a.ws + (int64_t)tok * a.conv_dim;
+  const int j = t & (kDk - 1);
+  for (int hk = 0; hk < a.hk; ++hk) {
+    const int p = hk & 1;   // alternating sum buffers: one barrier per head
+    const float x = bf(t < kDk ? y[hk * kDk + t] : y[a.key_dim + hk * kDk + (t - kDk)]);
+    float v2 = x * x;
+#pragma unroll
+    for (int d = 32; d >= 1; d >>= 1) v2 += __shfl_xor(v2, d, kWave);
+    if ((t & (kWave - 1)) == 0) s_sum[p][t / kWave] = v2;
+    __syncthreads();
+    const float n = sqrtf(t < kDk ? s_sum[p][0] + s_sum[p][1] : s_sum[p][2] + s_sum[p][3]);
+    const float xn = x / fmaxf(n, 1e-12f);
+    // Row j of q (or k) is stored at (j % 8) 16 + j / 8, so the recurrence
+    // thread that owns rows g, g + 8, ... reads them as 16 consecutive floats.
+    float* qk = a.wqk + ((int64_t)tok * a.hk + hk) * (2 * kDk);
+    qk[(t & kDk) + (j % kRowGroups) * 16 + j / kRowGroups] =
+        t < kDk ? xn * 0.08838834764831845f : xn;     // q (x 128 ** -0.5), then k
+  }
+  for (int h = t; h < a.hv; h += kThreads) {
+    const float xa = bf(a.a[tok * a.ab_rs + h]) + a.dt_bias[h];
+    const float sp = xa > 20.f ? xa : log1pf(expf(xa));        // F.softplus
+    float* gt = a.wg + ((int64_t)tok * a.hv + h) * 2;
+    gt[0] = expf(-expf(a.a_log[h]) * sp);
+    gt[1] = 1.f / (1.f + expf(-bf(a.b[tok * a.ab_rs + h])));
+  }
+}
+
+// The recurrence of one (request, value head) over the request's tokens, the
+// state in registers throughout.  Per token only the state-dependent work is
+// serial: S = alpha S, S^T k (reduced through LDS), delta, S += k delta^T,
+// S^T q (reduced through LDS), o = bf16(S^T q).  The two reductions use
+// separate LDS buffers, so one barrier after each suffices; the next token's
+// inputs (this thread's 16 rows of q and k, 4 values of v, alpha, beta) are
+// loaded while the current token runs.
+__global__ void __launch_bounds__(kThreads) gdn_recur_ext_kernel(GdnArgs a) {
+  __shared__ float s_vp[kRowGroups][kDv], s_op[kRowGroups][kDv];
+  const int bi = blockIdx.x / a.hv, h = blockIdx.x % a.hv;
+  const int hk = h / a.vpk;
+  const int t = threadIdx.x;
+  const int64_t r = a.req[bi];
+  if (r < 0 || r >= a.n_slots) return;
+  const int t0 = min(max(a.tok[bi], 0), a.rows), t1 = min(max(a.tok[bi + 1], t0), a.rows);
+  if (t1 <= t0) return;
+
+  const int d0 = 4 * (t & 31), g = t >> 5;
+  float* S = a.ssm + r * a.ssm_ss + (int64_t)h * kDk * kDv;
+  f32x4 s[16];
+#pragma unroll
+  for (int i = 0; i < 16; ++i)
+    s[i] = *reinterpret_cast<const f32x4*>(S + (g + kRowGroups * i) * kDv + d0);
+
+  struct In {
+    float q[16], k[16];
+    u32x2 v;
+    float alpha, beta;
+  };
+  auto fetch = [&](int tok) {
+    In in;
+    const float* qk = a.wqk + ((int64_t)tok * a.hk + hk) * (2 * kDk) + g * 16;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const f32x4 q4 = *reinterpret_cast<const f32x4*>(qk + 4 * i);
+      const f32x4 k4 = *reinterpret_cast<const f32x4*>(qk + kDk + 4 * i);
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        in.q[4 * i + c] = q4[c];
+        in.k[4 * i + c] = k4[c];
+      }
+    }
+    const uint16_t* y = a.ws + (int64_t)tok * a.conv_dim;
+    in.v = *reinterpret_cast<const u32x2*>(y + 2 * a.key_dim + h * kDv + d0);
+    const float2 gt = *reinterpret_cast<const float2*>(a.wg + ((int64_t)tok * a.hv + h) * 2);
+    in.alpha = gt.x;
+    in.beta = gt.y;
+    return in;
+  };
+  In nxt = fetch(t0);
+  for (int tok = t0; tok < t1; ++tok) {
+    const In cur = nxt;
+    // Unconditional (the last token re-reads itself): a branch here makes the
+    // compiler wait for these loads right after issuing them.
+    nxt = fetch(min(tok + 1, t1 - 1));
+    f32x4 vp = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      s[i] *= cur.alpha;
+      vp += s[i] * cur.k[i];
+    }
+    *reinterpret_cast<f32x4*>(&s_vp[g][d0]) = vp;
+    __syncthreads();
+    const f32x4 vv = {bf16_lo(cur.v[0]), bf16_hi(cur.v[0]), bf16_lo(cur.v[1]),
+                      bf16_hi(cur.v[1])};
+    f32x4 delta;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      float v_pred = 0.f;
+#pragma unroll
+      for (int q = 0; q < kRowGroups; ++q) v_pred += s_vp[q][d0 + c];
+      delta[c] = cur.beta * (vv[c] - v_pred);
+    }
+    f32x4 op = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      s[i] += cur.k[i] * delta;
+      op += s[i] * cur.q[i];
+    }
+    *reinterpret_cast<f32x4*>(&s_op[g][d0]) = op;
+    __syncthreads();
+    if (t < kDv) {
+      float o = 0.f;
+#pragma unroll
+      for (int q = 0; q < kRowGroups; ++q) o += s_op[q][t];
+      a.wcore[(int64_t)tok * (a.hv * kDv) + h * kDv + t] = to_bf(o);   // .to(orig_dtype)
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < 16; ++i)
+    *reinterpret_cast<f32x4*>(S + (g + kRowGroups * i) * kDv + d0) = s[i];
+}
+
+// Gated RMSNorm (rms_norm_gated.py:26-40) of every value head of one token
+// from the bf16 recurrence output, two heads per pass (one per 128 threads);
+// also copies the recurrence output to core_out when asked.
+__global__ void __launch_bounds__(kThreads) gdn_norm_ext_kernel(GdnArgs a) {
+  __shared__ float s_sum[2][4];
+  const int tok = blockIdx.x, t = threadIdx.x;
+  // The request owning this row (last b with offset <= tok); rows of requests
+  // whose slot is outside the pool are left untouched, as in the recurrence.
+  int lo = 0, hi = a.batch - 1;
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) >> 1;
+    if (min(max(a.tok[mid], 0), a.rows) <= tok) lo = mid; else hi = mid - 1;
+  }
+  const int64_t r = a.req[lo];
+  if (r < 0 || r >= a.n_slots) return;
+  const int half = t / kDv, d = t % kDv;
+  for (int h0 = 0; h0 < a.hv; h0 += 2) {
+    const int h = h0 + half, p = (h0 >> 1) & 1;
+    const bool act = h < a.hv;
+    const uint16_t ob = act ? a.wcore[(int64_t)tok * (a.hv * kDv) + h * kDv + d] : (uint16_t)0;
+    if (act && a.core) a.core[tok * a.core_rs + h * kDv + d] = ob;
+    const float o = bf(ob);
+    float v2 = o * o;
+#pragma unroll
+    for (int s2 = 32; s2 >= 1; s2 >>= 1) v2 += __shfl_xor(v2, s2, kWave);
+    if ((t & (kWave - 1)) == 0) s_sum[p][t / kWave] = v2;
+    __syncthreads();
+    const float var = (s_sum[p][2 * half] + s_sum[p][2 * half + 1]) / (float)kDv;
+    if (act) {
+      const float zz = bf(a.z[tok * a.z_rs + h * kDv + d]);
+      a.out[tok * a.out_rs + h * kDv + d] =
+          to_bf(a.norm_w[h * kDv + d] * (o * rsqrtf(var + a.eps)) * (zz / (1.f + expf(-zz))));
+    }
+  }
+}
+
 }  // namespace
 }  // namespace tfa
 
@@ -199,6 +432,95 @@ int64_t tf_gdn_decode_workspace_bytes(int32_t batch_size, int32_t num_k_heads,
   return (int64_t)batch_size * conv_dim * 2;
 }
 
+namespace tfa {
+// Extend workspace bytes per token row: conv outputs (bf16), normalised q / k
+// (fp32), gates (fp32) and the recurrence output (bf16).
+int64_t gdn_ext_row_bytes(int32_t hk, int32_t hv) {
+  const int64_t conv_dim = 2LL * hk * kDk + (int64_t)hv * kDv;
+  return conv_dim * 2 + (int64_t)hk * 2 * kDk * 4 + (int64_t)hv * 2 * 4 + (int64_t)hv * kDv * 2;
+}
+}  // namespace tfa
+
+namespace {
+
+// Validates the arguments shared by the decode and extend entry points and
+// fills the kernel arguments; rows = tokens (extend) or requests (decode).
+int32_t gdn_setup(const char* fn, const void* qkv, int64_t qkv_row_stride, const void* a,
+                  const void* b, int64_t ab_row_stride, const void* z, int64_t z_row_stride,
+                  const float* conv_weight, const float* a_log, const float* dt_bias,
+                  const float* norm_weight, float eps, void* conv_state,
+                  int64_t conv_slot_stride, float* ssm_state, int64_t ssm_slot_stride,
+                  const int64_t* req_indices, int32_t batch_size, int64_t rows, int64_t n_slots,
+                  int32_t num_k_heads, int32_t num_v_heads, int32_t head_k_dim,
+                  int32_t head_v_dim, int32_t conv_kernel, void* out, int64_t out_row_stride,
+                  void* core_out, int64_t core_row_stride, void* workspace,
+                  int64_t workspace_bytes, tfa::GdnArgs* g) {
+  using namespace tfa;
+  if (head_k_dim != kDk || head_v_dim != kDv || conv_kernel != 4)
+    return fail(TF_ERR_UNSUPPORTED,
+                "%s: head_k_dim=%d head_v_dim=%d conv_kernel=%d (128 / 128 / 4 only)", fn,
+                head_k_dim, head_v_dim, conv_kernel);
+  if (num_k_heads <= 0 || num_v_heads <= 0 || num_v_heads % num_k_heads)
+    return fail(TF_ERR_INVALID, "%s: %d value heads over %d key heads", fn, num_v_heads,
+                num_k_heads);
+  if (batch_size < 0 || n_slots <= 0 || rows < 0)
+    return fail(TF_ERR_INVALID, "%s: batch_size=%d n_slots=%lld", fn, batch_size,
+                (long long)n_slots);
+  const int64_t key_dim = (int64_t)num_k_heads * kDk, value_dim = (int64_t)num_v_heads * kDv;
+  const int64_t conv_dim = 2 * key_dim + value_dim;
+  if (!qkv || !a || !b || !z || !conv_weight || !a_log || !dt_bias || !norm_weight ||
+      !conv_state || !ssm_state || !req_indices || !out || !workspace)
+    return fail(TF_ERR_INVALID, "%s: null pointer", fn);
+  if (workspace_bytes < rows * conv_dim * 2 || (reinterpret_cast<uintptr_t>(workspace) & 1u))
+    return fail(TF_ERR_INVALID, "%s: workspace of %lld bytes (needs %lld)", fn,
+                (long long)workspace_bytes, (long long)(rows * conv_dim * 2));
+  if (qkv_row_stride < conv_dim || ab_row_stride < num_v_heads || z_row_stride < value_dim ||
+      out_row_stride < value_dim || (core_out && core_row_stride < value_dim) ||
+      conv_slot_stride < 3 * conv_dim || ssm_slot_stride < value_dim * kDk)
+    return fail(TF_ERR_INVALID, "%s: a row or slot stride is too small", fn);
+  if (!aligned16(conv_weight) || !aligned16(ssm_state) || ssm_slot_stride % 4)
+    return fail(TF_ERR_INVALID, "%s: conv_weight / ssm_state must be 16-byte aligned", fn);
+  if (rows * conv_dim > INT32_MAX || rows * qkv_row_stride > INT64_MAX / 4)
+    return fail(TF_ERR_UNSUPPORTED, "%s: too many rows", fn);
+  g->qkv = static_cast<const uint16_t*>(qkv);
+  g->qkv_rs = qkv_row_stride;
+  g->a = static_cast<const uint16_t*>(a);
+  g->b = static_cast<const uint16_t*>(b);
+  g->ab_rs = ab_row_stride;
+  g->z = static_cast<const uint16_t*>(z);
+  g->z_rs = z_row_stride;
+  g->conv_w = conv_weight;
+  g->a_log = a_log;
+  g->dt_bias = dt_bias;
+  g->norm_w = norm_weight;
+  g->eps = eps;
+  g->conv_state = static_cast<uint16_t*>(conv_state);
+  g->conv_ss = conv_slot_stride;
+  g->ssm = ssm_state;
+  g->ssm_ss = ssm_slot_stride;
+  g->req = req_indices;
+  g->n_slots = n_slots;
+  g->batch = batch_size;
+  g->hv = num_v_heads;
+  g->vpk = num_v_heads / num_k_heads;
+  g->key_dim = (int32_t)key_dim;
+  g->conv_dim = (int32_t)conv_dim;
+  g->tok = nullptr;
+  g->rows = (int32_t)rows;
+  g->hk = num_k_heads;
+  g->wqk = nullptr;
+  g->wg = nullptr;
+  g->wcore = nullptr;
+  g->ws = static_cast<uint16_t*>(workspace);
+  g->out = static_cast<uint16_t*>(out);
+  g->out_rs = out_row_stride;
+  g->core = static_cast<uint16_t*>(core_out);
+  g->core_rs = core_row_stride;
+  return TF_OK;
+}
+
+}  // namespace
+
 int32_t tf_gdn_decode(const void* qkv, int64_t qkv_row_stride, const void* a, const void* b,
                       int64_t ab_row_stride, const void* z, int64_t z_row_stride,
                       const float* conv_weight, const float* a_log, const float* dt_bias,
@@ -211,70 +533,88 @@ int32_t tf_gdn_decode(const void* qkv, int64_t qkv_row_stride, const void* a, co
                       void* workspace, int64_t workspace_bytes, tf_stream_t stream) {
   using namespace tfa;
   clear_error();
-  if (head_k_dim != kDk || head_v_dim != kDv || conv_kernel != 4)
-    return fail(TF_ERR_UNSUPPORTED,
-                "gdn_decode: head_k_dim=%d head_v_dim=%d conv_kernel=%d (128 / 128 / 4 only)",
-                head_k_dim, head_v_dim, conv_kernel);
-  if (num_k_heads <= 0 || num_v_heads <= 0 || num_v_heads % num_k_heads)
-    return fail(TF_ERR_INVALID, "gdn_decode: %d value heads over %d key heads", num_v_heads,
-                num_k_heads);
-  if (batch_size < 0 || n_slots <= 0)
-    return fail(TF_ERR_INVALID, "gdn_decode: batch_size=%d n_slots=%lld", batch_size,
-                (long long)n_slots);
   if (batch_size == 0) return TF_OK;
-  const int64_t key_dim = (int64_t)num_k_heads * kDk, value_dim = (int64_t)num_v_heads * kDv;
-  const int64_t conv_dim = 2 * key_dim + value_dim;
-  if (!qkv || !a || !b || !z || !conv_weight || !a_log || !dt_bias || !norm_weight ||
-      !conv_state || !ssm_state || !req_indices || !out || !workspace)
-    return fail(TF_ERR_INVALID, "gdn_decode: null pointer");
-  if (workspace_bytes < (int64_t)batch_size * conv_dim * 2 ||
-      (reinterpret_cast<uintptr_t>(workspace) & 1u))
-    return fail(TF_ERR_INVALID, "gdn_decode: workspace of %lld bytes (needs %lld)",
-                (long long)workspace_bytes, (long long)(batch_size * conv_dim * 2));
-  if (qkv_row_stride < conv_dim || ab_row_stride < num_v_heads || z_row_stride < value_dim ||
-      out_row_stride < value_dim || (core_out && core_row_stride < value_dim) ||
-      conv_slot_stride < 3 * conv_dim || ssm_slot_stride < value_dim * kDk)
-    return fail(TF_ERR_INVALID, "gdn_decode: a row or slot stride is too small");
-  if (!aligned16(conv_weight) || !aligned16(ssm_state) || ssm_slot_stride % 4)
-    return fail(TF_ERR_INVALID, "gdn_decode: conv_weight / ssm_state must be 16-byte aligned");
-  if ((int64_t)batch_size * conv_dim > INT32_MAX)
-    return fail(TF_ERR_UNSUPPORTED, "gdn_decode: batch too large");
   GdnArgs g;
-  g.qkv = static_cast<const uint16_t*>(qkv);
-  g.qkv_rs = qkv_row_stride;
-  g.a = static_cast<const uint16_t*>(a);
-  g.b = static_cast<const uint16_t*>(b);
-  g.ab_rs = ab_row_stride;
-  g.z = static_cast<const uint16_t*>(z);
-  g.z_rs = z_row_stride;
-  g.conv_w = conv_weight;
-  g.a_log = a_log;
-  g.dt_bias = dt_bias;
-  g.norm_w = norm_weight;
-  g.eps = eps;
-  g.conv_state = static_cast<uint16_t*>(conv_state);
-  g.conv_ss = conv_slot_stride;
-  g.ssm = ssm_state;
-  g.ssm_ss = ssm_slot_stride;
-  g.req = req_indices;
-  g.n_slots = n_slots;
-  g.batch = batch_size;
-  g.hv = num_v_heads;
-  g.vpk = num_v_heads / num_k_heads;
-  g.key_dim = (int32_t)key_dim;
-  g.conv_dim = (int32_t)conv_dim;
-  g.ws = static_cast<uint16_t*>(workspace);
-  g.out = static_cast<uint16_t*>(out);
-  g.out_rs = out_row_stride;
-  g.core = static_cast<uint16_t*>(core_out);
-  g.core_rs = core_row_stride;
+  const int32_t rc = gdn_setup(
+      "gdn_decode", qkv, qkv_row_stride, a, b, ab_row_stride, z, z_row_stride, conv_weight,
+      a_log, dt_bias, norm_weight, eps, conv_state, conv_slot_stride, ssm_state,
+      ssm_slot_stride, req_indices, batch_size, batch_size, n_slots, num_k_heads, num_v_heads,
+      head_k_dim, head_v_dim, conv_kernel, out, out_row_stride, core_out, core_row_stride,
+      workspace, workspace_bytes, &g);
+  if (rc != TF_OK) return rc;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-  const int64_t n_conv = (int64_t)batch_size * conv_dim;
+  const int64_t n_conv = (int64_t)batch_size * g.conv_dim;
   hipLaunchKernelGGL(gdn_conv_kernel, dim3((n_conv + kThreads - 1) / kThreads), dim3(kThreads),
                      0, s, g);
   hipLaunchKernelGGL(gdn_recur_kernel, dim3((int64_t)batch_size * num_v_heads), dim3(kThreads), 0,
                      s, g);
   return launch_status("tf_gdn_decode launch");
+}
+
+int64_t tf_gdn_extend_workspace_bytes(int64_t n_tokens, int32_t num_k_heads,
+                                      int32_t num_v_heads) {
+  tfa::clear_error();
+  if (n_tokens < 0 || num_k_heads <= 0 || num_v_heads <= 0)
+    return tfa::fail(TF_ERR_INVALID, "gdn_extend_workspace_bytes: bad arguments");
+  return n_tokens * tfa::gdn_ext_row_bytes(num_k_heads, num_v_heads);
+}
+
+int32_t tf_gdn_extend(const void* qkv, int64_t qkv_row_stride, const void* a, const void* b,
+                      int64_t ab_row_stride, const void* z, int64_t z_row_stride,
+                      const float* conv_weight, const float* a_log, const float* dt_bias,
+                      const float* norm_weight, float eps, void* conv_state,
+                      int64_t conv_slot_stride, float* ssm_state, int64_t ssm_slot_stride,
+                      const int64_t* req_indices, const int32_t* token_offsets,
+                      int32_t batch_size, int64_t n_tokens, int32_t max_extend_len,
+                      int64_t n_slots,
+                      int32_t num_k_heads, int32_t num_v_heads, int32_t head_k_dim,
+                      int32_t head_v_dim, int32_t conv_kernel, void* out,
+                      int64_t out_row_stride, void* core_out, int64_t core_row_stride,
+                      void* workspace, int64_t workspace_bytes, tf_stream_t stream) {
+  using namespace tfa;
+  clear_error();
+  if (batch_size == 0 || n_tokens == 0) return TF_OK;
+  if (!token_offsets) return fail(TF_ERR_INVALID, "gdn_extend: null token_offsets");
+  if (max_extend_len < 0 || max_extend_len > n_tokens)
+    return fail(TF_ERR_INVALID, "gdn_extend: max_extend_len=%d", max_extend_len);
+  if (max_extend_len > 65535 * 16)
+    return fail(TF_ERR_UNSUPPORTED, "gdn_extend: max_extend_len=%d too large", max_extend_len);
+  if (batch_size > 65535) return fail(TF_ERR_UNSUPPORTED, "gdn_extend: batch_size > 65535");
+  GdnArgs g;
+  const int32_t rc = gdn_setup(
+      "gdn_extend", qkv, qkv_row_stride, a, b, ab_row_stride, z, z_row_stride, conv_weight,
+      a_log, dt_bias, norm_weight, eps, conv_state, conv_slot_stride, ssm_state,
+      ssm_slot_stride, req_indices, batch_size, n_tokens, n_slots, num_k_heads, num_v_heads,
+      head_k_dim, head_v_dim, conv_kernel, out, out_row_stride, core_out, core_row_stride,
+      workspace, workspace_bytes, &g);
+  if (rc != TF_OK) return rc;
+  if (workspace_bytes < n_tokens * gdn_ext_row_bytes(num_k_heads, num_v_heads) ||
+      (reinterpret_cast<uintptr_t>(workspace) & 15u))
+    return fail(TF_ERR_INVALID, "gdn_extend: workspace of %lld bytes (needs %lld, 16-byte aligned)",
+                (long long)workspace_bytes,
+                (long long)(n_tokens * gdn_ext_row_bytes(num_k_heads, num_v_heads)));
+  if (n_tokens > 65535LL * 65535LL) return fail(TF_ERR_UNSUPPORTED, "gdn_extend: too many tokens");
+  g.tok = token_offsets;
+  uint8_t* w = static_cast<uint8_t*>(workspace);
+  const int64_t conv_bytes = n_tokens * g.conv_dim * 2;
+  const int64_t qk_bytes = n_tokens * num_k_heads * 2 * kDk * 4;
+  const int64_t gate_bytes = n_tokens * num_v_heads * 2 * 4;
+  g.wqk = reinterpret_cast<float*>(w + ((conv_bytes + 15) & ~15LL));
+  g.wg = reinterpret_cast<float*>(reinterpret_cast<uint8_t*>(g.wqk) + qk_bytes);
+  g.wcore = reinterpret_cast<uint16_t*>(reinterpret_cast<uint8_t*>(g.wg) + gate_bytes);
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  const uint32_t cblocks = (g.conv_dim + kThreads - 1) / kThreads;
+  const uint32_t tblocks = (uint32_t)((max_extend_len + kConvTokens - 1) / kConvTokens);
+  if (tblocks > 0) {
+    hipLaunchKernelGGL(gdn_conv_ext_kernel, dim3(cblocks, batch_size, tblocks), dim3(kThreads),
+                       0, s, g);
+  }
+  hipLaunchKernelGGL(gdn_conv_state_kernel, dim3(cblocks, batch_size), dim3(kThreads), 0, s, g);
+  hipLaunchKernelGGL(gdn_qk_ext_kernel, dim3((uint32_t)n_tokens), dim3(kThreads), 0, s, g);
+  hipLaunchKernelGGL(gdn_recur_ext_kernel, dim3((int64_t)batch_size * num_v_heads),
+                     dim3(kThreads), 0, s, g);
+  hipLaunchKernelGGL(gdn_norm_ext_kernel, dim3((uint32_t)n_tokens), dim3(kThreads), 0, s, g);
+  return launch_status("tf_gdn_extend launch");
 }
 
 }  // extern "C"

@@ -10,14 +10,14 @@ layer's conv and SSM states in place.
 ``LinearAttention`` mirrors ``Qwen3_8LinearAttention``'s parameters
 (``:29-107``: ``in_proj_qkv``, ``in_proj_z``, ``in_proj_b``, ``in_proj_a``,
 ``conv1d``, ``A_log``, ``dt_bias``, ``norm.weight``, ``out_proj``) and its
-``forward(hidden_states, cache_pool, forward_batch)`` for batches whose
-requests all extend by one token. The chunked prefill of longer extends has no
-native kernel here; such batches raise ``NotImplementedError`` rather than
-running anything else.
+``forward(hidden_states, cache_pool, forward_batch)``: all-decode batches run
+``gdn_decode_step``; batches with longer extends run ``gdn_extend_step``
+(``tf_gdn_extend``), the reference's per-request conv + chunked-update loop
+computed token by token with each head's state held in registers.
 """
 from __future__ import annotations
 
-from typing import Optional
+from typing import Optional, Sequence
 
 import torch
 import torch.nn as nn
@@ -39,6 +39,32 @@ def _rows(t: torch.Tensor, name: str) -> int:
     return t.stride(0)
 
 
+def _check_common(qkv, b, a, z, conv_weight, a_log, dt_bias, norm_weight, layer_conv_state,
+                  layer_ssm_state, req_indices, num_v_heads):
+    value_dim = num_v_heads * HEAD_DIM
+    for name, t, dt in (("qkv", qkv, torch.bfloat16), ("b", b, torch.bfloat16),
+                        ("a", a, torch.bfloat16), ("z", z, torch.bfloat16),
+                        ("conv_weight", conv_weight, torch.float32),
+                        ("a_log", a_log, torch.float32), ("dt_bias", dt_bias, torch.float32),
+                        ("norm_weight", norm_weight, torch.float32),
+                        ("layer_conv_state", layer_conv_state, torch.bfloat16),
+                        ("layer_ssm_state", layer_ssm_state, torch.float32),
+                        ("req_indices", req_indices, torch.int64)):
+        if t.dtype != dt or not t.is_cuda:
+            raise ValueError(f"gdn step: {name} must be a {dt} CUDA tensor")
+    if a.stride() != b.stride() or a.shape != b.shape:
+        raise ValueError("gdn step: a and b must share shape and strides")
+    for name, t in (("conv_weight", conv_weight), ("a_log", a_log), ("dt_bias", dt_bias),
+                    ("norm_weight", norm_weight), ("req_indices", req_indices)):
+        if not t.is_contiguous():
+            raise ValueError(f"gdn step: {name} must be contiguous")
+    cs, ss = layer_conv_state, layer_ssm_state
+    if cs.dim() != 3 or cs.stride(2) != 1 or cs.stride(1) != CONV_KERNEL - 1:
+        raise ValueError("gdn step: conv state must be [slots, conv_dim, 3] with dense rows")
+    if ss.dim() != 4 or ss[0].numel() != value_dim * HEAD_DIM or not ss[0].is_contiguous():
+        raise ValueError("gdn step: ssm state must be [slots, Hv, 128, 128], dense per slot")
+
+
 def gdn_decode_step(qkv: torch.Tensor, b: torch.Tensor, a: torch.Tensor, z: torch.Tensor,
                     conv_weight: torch.Tensor, a_log: torch.Tensor, dt_bias: torch.Tensor,
                     norm_weight: torch.Tensor, eps: float, layer_conv_state: torch.Tensor,
@@ -54,27 +80,9 @@ def gdn_decode_step(qkv: torch.Tensor, b: torch.Tensor, a: torch.Tensor, z: torc
     Returns the normed bf16 output [B, Hv*128] (and the pre-norm output)."""
     bsz = qkv.shape[0]
     value_dim = num_v_heads * HEAD_DIM
-    for name, t, dt in (("qkv", qkv, torch.bfloat16), ("b", b, torch.bfloat16),
-                        ("a", a, torch.bfloat16), ("z", z, torch.bfloat16),
-                        ("conv_weight", conv_weight, torch.float32),
-                        ("a_log", a_log, torch.float32), ("dt_bias", dt_bias, torch.float32),
-                        ("norm_weight", norm_weight, torch.float32),
-                        ("layer_conv_state", layer_conv_state, torch.bfloat16),
-                        ("layer_ssm_state", layer_ssm_state, torch.float32),
-                        ("req_indices", req_indices, torch.int64)):
-        if t.dtype != dt or not t.is_cuda:
-            raise ValueError(f"gdn_decode_step: {name} must be a {dt} CUDA tensor")
-    if a.stride() != b.stride() or a.shape != b.shape:
-        raise ValueError("gdn_decode_step: a and b must share shape and strides")
-    for name, t in (("conv_weight", conv_weight), ("a_log", a_log), ("dt_bias", dt_bias),
-                    ("norm_weight", norm_weight), ("req_indices", req_indices)):
-        if not t.is_contiguous():
-            raise ValueError(f"gdn_decode_step: {name} must be contiguous")
+    _check_common(qkv, b, a, z, conv_weight, a_log, dt_bias, norm_weight, layer_conv_state,
+                  layer_ssm_state, req_indices, num_v_heads)
     cs, ss = layer_conv_state, layer_ssm_state
-    if cs.dim() != 3 or cs.stride(2) != 1 or cs.stride(1) != CONV_KERNEL - 1:
-        raise ValueError("gdn_decode_step: conv state must be [slots, conv_dim, 3] with dense rows")
-    if ss.dim() != 4 or ss[0].numel() != value_dim * HEAD_DIM or not ss[0].is_contiguous():
-        raise ValueError("gdn_decode_step: ssm state must be [slots, Hv, 128, 128], dense per slot")
     out = torch.empty((bsz, value_dim), dtype=torch.bfloat16, device=qkv.device)
     core = torch.empty_like(out) if return_core else None
     ws = torch.empty((bsz, 2 * num_k_heads * HEAD_DIM + value_dim), dtype=torch.bfloat16,
@@ -87,6 +95,46 @@ def gdn_decode_step(qkv: torch.Tensor, b: torch.Tensor, a: torch.Tensor, z: torc
                  HEAD_DIM, HEAD_DIM, CONV_KERNEL, _ptr(out), out.stride(0), _ptr(core),
                  0 if core is None else core.stride(0), _ptr(ws), ws.numel() * 2,
                  s.cuda_stream)
+    return (out, core) if return_core else out
+
+
+def gdn_extend_step(qkv: torch.Tensor, b: torch.Tensor, a: torch.Tensor, z: torch.Tensor,
+                    conv_weight: torch.Tensor, a_log: torch.Tensor, dt_bias: torch.Tensor,
+                    norm_weight: torch.Tensor, eps: float, layer_conv_state: torch.Tensor,
+                    layer_ssm_state: torch.Tensor, req_indices: torch.Tensor,
+                    extend_lens: Sequence[int], num_k_heads: int, num_v_heads: int,
+                    return_core: bool = False, stream=None):
+    """The layer for a batch with any extend lengths (the reference's per-request
+    loop, ``linear_attention.py:328-364``): request i owns the next
+    ``extend_lens[i]`` token rows of qkv / a / b / z. Same tensors as
+    ``gdn_decode_step`` with rows = tokens; returns ``[T, Hv*128]`` bf16."""
+    n_tok = qkv.shape[0]
+    lens = [int(e) for e in extend_lens]
+    if len(lens) != req_indices.numel() or sum(lens) != n_tok or min(lens, default=1) < 0:
+        raise ValueError("gdn_extend_step: extend_lens must cover the token rows, one per request")
+    _check_common(qkv, b, a, z, conv_weight, a_log, dt_bias, norm_weight, layer_conv_state,
+                  layer_ssm_state, req_indices, num_v_heads)
+    offsets = [0]
+    for e in lens:
+        offsets.append(offsets[-1] + e)
+    tok = torch.tensor(offsets, dtype=torch.int32).to(qkv.device, non_blocking=True)
+    value_dim = num_v_heads * HEAD_DIM
+    out = torch.empty((n_tok, value_dim), dtype=torch.bfloat16, device=qkv.device)
+    core = torch.empty_like(out) if return_core else None
+    ws_bytes = _native.load().tf_gdn_extend_workspace_bytes(n_tok, num_k_heads, num_v_heads)
+    if ws_bytes < 0:
+        raise ValueError("gdn_extend_step: bad head counts")
+    ws = torch.empty((max(ws_bytes, 1),), dtype=torch.uint8, device=qkv.device)
+    s = stream if stream is not None else torch.cuda.current_stream(qkv.device)
+    cs, ss = layer_conv_state, layer_ssm_state
+    _native.call("tf_gdn_extend", _ptr(qkv), _rows(qkv, "qkv"), _ptr(a), _ptr(b),
+                 _rows(a, "a"), _ptr(z), _rows(z, "z"), _ptr(conv_weight), _ptr(a_log),
+                 _ptr(dt_bias), _ptr(norm_weight), float(eps), _ptr(cs), cs.stride(0), _ptr(ss),
+                 ss.stride(0), _ptr(req_indices), _ptr(tok), len(lens), n_tok, max(lens),
+                 cs.shape[0],
+                 num_k_heads, num_v_heads, HEAD_DIM, HEAD_DIM, CONV_KERNEL, _ptr(out),
+                 out.stride(0), _ptr(core), 0 if core is None else core.stride(0), _ptr(ws),
+                 ws.numel(), s.cuda_stream)
     return (out, core) if return_core else out
 
 
@@ -145,17 +193,19 @@ class LinearAttention(nn.Module):
         return self._packed
 
     def forward(self, hidden_states: torch.Tensor, cache_pool, forward_batch) -> torch.Tensor:
-        if not all(e == 1 for e in forward_batch.extend_lens):
-            raise NotImplementedError(
-                "LinearAttention: only all-decode batches run natively (the chunked "
-                "Gated DeltaNet prefill has no kernel here)")
         qkv = self.in_proj_qkv(hidden_states)
         z = self.in_proj_z(hidden_states)
         b = self.in_proj_b(hidden_states)
         a = self.in_proj_a(hidden_states)
         conv_state, ssm_state = cache_pool.get_linear_states(self.layer_idx)
         conv_w, a_log, dt_bias, norm_w = self._kernel_params()
-        attn = gdn_decode_step(qkv, b, a, z, conv_w, a_log, dt_bias, norm_w, self.eps,
-                               conv_state, ssm_state, forward_batch.req_pool_indices,
-                               self.num_k_heads, self.num_v_heads)
+        if all(e == 1 for e in forward_batch.extend_lens):     # :316-326
+            attn = gdn_decode_step(qkv, b, a, z, conv_w, a_log, dt_bias, norm_w, self.eps,
+                                   conv_state, ssm_state, forward_batch.req_pool_indices,
+                                   self.num_k_heads, self.num_v_heads)
+        else:                                                    # :328-364
+            attn = gdn_extend_step(qkv, b, a, z, conv_w, a_log, dt_bias, norm_w, self.eps,
+                                   conv_state, ssm_state, forward_batch.req_pool_indices,
+                                   forward_batch.extend_lens, self.num_k_heads,
+                                   self.num_v_heads)
         return self.out_proj(attn)
