@@ -301,6 +301,13 @@ int32_t tf_qk_norm_rope_kv_write(const void* q, int64_t q_token_stride, int64_t 
  * scales (weight_scale_inv None: every scale 1).  bias: bf16 [n] or NULL.
  * out: bf16 [m, n], row stride out_row_stride elements (a multiple of 4),
  * 8-byte aligned.
+ * workspace (optional, NULL allowed): when m is small (up to 512) the output
+ * tiles alone leave most compute units idle and the call splits K over
+ * several workgroups per tile if it gets tf_fp8_block_gemm_workspace_bytes(m,
+ * n, k) bytes of 16-byte aligned scratch (fp32 partials, no initialisation
+ * needed; the partials are summed in a fixed order, so results do not depend
+ * on timing).  Without it (or when the size query returns 0) one workgroup
+ * covers each output tile.
  */
 #define TF_FP8_QUANT_WORKSPACE_BYTES 4096
 
@@ -314,7 +321,9 @@ int32_t tf_fp8_block_gemm(const void* xq, int64_t xq_row_stride, const float* x_
                           int64_t w_scale_row_stride, int64_t w_scale_col_stride,
                           int32_t block_h, int32_t block_w, const void* bias, int64_t m,
                           int64_t n, int64_t k, void* out, int64_t out_row_stride,
-                          tf_stream_t stream);
+                          void* workspace, int64_t workspace_bytes, tf_stream_t stream);
+
+int64_t tf_fp8_block_gemm_workspace_bytes(int64_t m, int64_t n, int64_t k);
 
 /* ------------------------------------------------------------------ Gated DeltaNet decode
  * One-token step of the linear-attention (Gated DeltaNet) layers for a batch

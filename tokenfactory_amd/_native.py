@@ -12,7 +12,7 @@ from pathlib import Path
 from typing import Optional
 
 LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libtf_attn.so"
-ABI_VERSION = 8
+ABI_VERSION = 9
 
 TF_DTYPE_BF16 = 0
 TF_DTYPE_FP8_E4M3 = 1
@@ -97,8 +97,10 @@ SIGNATURES = {
         _p, _i64,                      # w, w_row_stride
         _p, _i64, _i64, _i32, _i32,    # w_scale, its row / col strides, block_h, block_w
         _p, _i64, _i64, _i64,          # bias, m, n, k
-        _p, _i64, _p,                  # out, out_row_stride, stream
+        _p, _i64,                      # out, out_row_stride
+        _p, _i64, _p,                  # workspace, workspace_bytes, stream
     ]),
+    "tf_fp8_block_gemm_workspace_bytes": (_i64, [_i64, _i64, _i64]),
     "tf_gdn_decode": (_i32, [
         _p, _i64, _p, _p, _i64,        # qkv, qkv_row_stride, a, b, ab_row_stride
         _p, _i64,                      # z, z_row_stride

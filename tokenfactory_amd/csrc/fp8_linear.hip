@@ -160,6 +160,8 @@ struct GemmArgs {
   uint16_t* out;          // bf16 [M, N], row stride os elements
   int64_t os;
   int32_t M, N, KB, tiles_m;
+  int32_t tiles, splits;  // split-K: workgroup = (split, tile), K slices split evenly
+  float* part;            // split-K: fp32 [splits, M, N] partial products (NULL: no split)
 };
 
 __device__ __forceinline__ int swz(int r) { return (r & 7) ^ ((r >> 3) & 1); }
@@ -216,8 +218,12 @@ fp8_gemm_kernel(GemmArgs a) {
   __shared__ __attribute__((aligned(16))) uint8_t smem[STAGES * T::kStage];
   const int t = threadIdx.x, w = wave_id(), l = t & 63;
   const int wm = w / WN, wn = w % WN;
-  const int m0 = (blockIdx.x % a.tiles_m) * T::kBM;
-  const int n0 = (blockIdx.x / a.tiles_m) * T::kBN;
+  const int tile = blockIdx.x % a.tiles, split = blockIdx.x / a.tiles;
+  const int m0 = (tile % a.tiles_m) * T::kBM;
+  const int n0 = (tile / a.tiles_m) * T::kBN;
+  // This workgroup's K slices [kb0, kb0 + KB) (all of them without split-K).
+  const int kb0 = (int)((int64_t)a.KB * split / a.splits);
+  const int KB = (int)((int64_t)a.KB * (split + 1) / a.splits) - kb0;
 
   const float xsc = *a.x_scale;
   asm volatile("" :: "v"(xsc));   // land the scale before any staging load is in flight
@@ -272,9 +278,8 @@ fp8_gemm_kernel(GemmArgs a) {
 
   // Slices past the last are never read; their stage is refilled with the last
   // slice so that every step issues (and waits for) the same loads.
-  const int KB = a.KB;
 #pragma unroll
-  for (int i = 0; i < T::kAhead; ++i) issue(min(i, KB - 1), i);
+  for (int i = 0; i < T::kAhead; ++i) issue(kb0 + min(i, KB - 1), i);
   if constexpr (T::kAhead == 2)
     vm_wait<T::kLoads>();
   else
@@ -283,7 +288,7 @@ fp8_gemm_kernel(GemmArgs a) {
 
   int st = 0;
   for (int j = 0; j < KB; ++j) {
-    issue(min(j + T::kAhead, KB - 1), st == 0 ? STAGES - 1 : st - 1);
+    issue(kb0 + min(j + T::kAhead, KB - 1), st == 0 ? STAGES - 1 : st - 1);
     const uint8_t* sp = smem + st * T::kStage;
     const uint8_t* ssp = sp + T::kXBytes + T::kWBytes;
     f32x4 s4[4];
@@ -323,6 +328,20 @@ fp8_gemm_kernel(GemmArgs a) {
   vm_wait<0>();   // the refills of the last steps land before the workgroup ends
 
   // Epilogue: lane holds D[n0 + wn 64 + 16 tn + 4 g + r][m0 + wm 16 MT + 16 tm + rr].
+  if (a.part) {   // split-K: fp32 partials, bias and rounding in splitk_reduce_kernel
+#pragma unroll
+    for (int tn = 0; tn < 4; ++tn) {
+      const int n = n0 + scol4 + 16 * tn;
+      if (n >= a.N) continue;   // N % 4 == 0: four columns in or out together
+#pragma unroll
+      for (int tm = 0; tm < MT; ++tm) {
+        const int m = m0 + xrow + 16 * tm;
+        if (m < a.M)
+          *reinterpret_cast<f32x4*>(a.part + ((int64_t)split * a.M + m) * a.N + n) = acc[tm][tn];
+      }
+    }
+    return;
+  }
 #pragma unroll
   for (int tn = 0; tn < 4; ++tn) {
     const int n = n0 + scol4 + 16 * tn;
@@ -352,17 +371,65 @@ fp8_gemm_kernel(GemmArgs a) {
   }
 }
 
+// out = bf16(sum over splits of the fp32 partials (in split order) + bias);
+// one thread per four consecutive columns (N % 4 == 0).
+__global__ void __launch_bounds__(kThreads) splitk_reduce_kernel(GemmArgs a) {
+  const int64_t e = 4 * ((int64_t)blockIdx.x * kThreads + threadIdx.x);
+  const int64_t mn = (int64_t)a.M * a.N;
+  if (e >= mn) return;
+  const int m = (int)(e / a.N), n = (int)(e - (int64_t)m * a.N);
+  f32x4 v = *reinterpret_cast<const f32x4*>(a.part + e);
+  for (int sp = 1; sp < a.splits; ++sp) v += *reinterpret_cast<const f32x4*>(a.part + sp * mn + e);
+  float b[4] = {0.f, 0.f, 0.f, 0.f};
+  if (a.bias) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) b[r] = __uint_as_float((uint32_t)a.bias[n + r] << 16);
+  }
+  u32x2 pk;
+  pk[0] = pack_bf16(v[0] + b[0], v[1] + b[1]);
+  pk[1] = pack_bf16(v[2] + b[2], v[3] + b[3]);
+  *reinterpret_cast<u32x2*>(a.out + (int64_t)m * a.os + n) = pk;
+}
+
+// Tile shape by M: (MT, WN, STAGES).
+struct Shape {
+  int mt, wn;
+};
+Shape gemm_shape(int64_t m) {
+  if (m <= 32) return {1, 2};
+  if (m <= 64) return {2, 2};
+  if (m <= 128) return {4, 2};
+  if (m <= 1024) return {8, 2};
+  return {8, 4};   // 8 waves, 256 x 256 tiles, 2 waves per SIMD
+}
+
+// Split-K factor: when the output tiles alone leave most CUs idle (M up to 512,
+// the weight-streaming regime), K is split until ~320 workgroups stream it.
+int gemm_splits(int64_t m, int64_t n, int64_t k) {
+  const Shape sh = gemm_shape(m);
+  if (m > 512 || n % 4) return 1;
+  const int64_t tiles = ((m + 32 * sh.mt - 1) / (32 * sh.mt)) * ((n + 64 * sh.wn - 1) / (64 * sh.wn));
+  const int64_t kb = k / kKSlice;
+  if (tiles >= 128 || kb < 4) return 1;
+  return (int)std::max<int64_t>(1, std::min<int64_t>({kb / 2, (320 + tiles - 1) / tiles, 16}));
+}
+
 template <int MT, int WN, int STAGES>
 void launch_gemm(const GemmArgs& a, hipStream_t stream) {
   using T = Tile<MT, WN, STAGES>;
   GemmArgs b = a;
   b.tiles_m = (a.M + T::kBM - 1) / T::kBM;
   const int tiles_n = (a.N + T::kBN - 1) / T::kBN;
-  const dim3 grid(b.tiles_m * tiles_n), block(T::kThreads);
+  b.tiles = b.tiles_m * tiles_n;
+  const dim3 grid(b.tiles * b.splits), block(T::kThreads);
   if (a.wsc == nullptr || a.bh % 64 == 0)
     hipLaunchKernelGGL((fp8_gemm_kernel<MT, WN, STAGES, true>), grid, block, 0, stream, b);
   else
     hipLaunchKernelGGL((fp8_gemm_kernel<MT, WN, STAGES, false>), grid, block, 0, stream, b);
+  if (b.part) {
+    const int64_t groups = ((int64_t)a.M * a.N / 4 + kThreads - 1) / kThreads;
+    hipLaunchKernelGGL(splitk_reduce_kernel, dim3((uint32_t)groups), dim3(kThreads), 0, stream, b);
+  }
 }
 
 }  // namespace
@@ -418,7 +485,7 @@ int32_t tf_fp8_block_gemm(const void* xq, int64_t xq_row_stride, const float* x_
                           int64_t w_scale_row_stride, int64_t w_scale_col_stride,
                           int32_t block_h, int32_t block_w, const void* bias, int64_t m,
                           int64_t n, int64_t k, void* out, int64_t out_row_stride,
-                          tf_stream_t stream) {
+                          void* workspace, int64_t workspace_bytes, tf_stream_t stream) {
   using namespace tfa;
   clear_error();
   if (m < 0 || n <= 0 || k <= 0 || k % kKSlice)
@@ -464,18 +531,40 @@ int32_t tf_fp8_block_gemm(const void* xq, int64_t xq_row_stride, const float* x_
   a.N = (int32_t)n;
   a.KB = (int32_t)(k / kKSlice);
   a.tiles_m = 0;
+  a.tiles = 0;
+  a.splits = 1;
+  a.part = nullptr;
+  // Split-K when a large enough 16-byte aligned workspace comes with the call;
+  // otherwise (or when it does not pay) one workgroup per output tile.
+  const int splits = gemm_splits(m, n, k);
+  if (splits > 1 && workspace && !(reinterpret_cast<uintptr_t>(workspace) & 15u) &&
+      workspace_bytes >= (int64_t)splits * m * n * 4) {
+    a.splits = splits;
+    a.part = static_cast<float*>(workspace);
+  }
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-  if (m <= 32)
+  const Shape sh = gemm_shape(m);
+  if (sh.mt == 1)
     launch_gemm<1, 2, 3>(a, s);
-  else if (m <= 64)
+  else if (sh.mt == 2)
     launch_gemm<2, 2, 3>(a, s);
-  else if (m <= 128)
+  else if (sh.mt == 4)
     launch_gemm<4, 2, 3>(a, s);
-  else if (m <= 1024)
+  else if (sh.wn == 2)
     launch_gemm<8, 2, 3>(a, s);
-  else   // 8 waves, 256 x 256 tiles, 2 waves per SIMD
+  else
     launch_gemm<8, 4, 2>(a, s);
   return launch_status("tf_fp8_block_gemm launch");
+}
+
+int64_t tf_fp8_block_gemm_workspace_bytes(int64_t m, int64_t n, int64_t k) {
+  using namespace tfa;
+  clear_error();
+  if (m < 0 || n <= 0 || k <= 0 || k % kKSlice)
+    return fail(TF_ERR_INVALID, "fp8_block_gemm_workspace_bytes: m=%lld n=%lld k=%lld",
+                (long long)m, (long long)n, (long long)k);
+  const int splits = gemm_splits(m, n, k);
+  return splits > 1 ? (int64_t)splits * m * n * 4 : 0;
 }
 
 }  // extern "C"

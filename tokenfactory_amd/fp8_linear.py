@@ -120,11 +120,16 @@ def block_fp8_gemm(xq: torch.Tensor, x_scale: torch.Tensor, weight: torch.Tensor
         xq, weight = _pad_cols(xq, kp), _pad_cols(weight, kp)
         if ws is None:        # one all-ones block over the true K (fp8_triton.py:132-135)
             block_w = kp
+    # split-K scratch for small m (0 bytes when the call does not split)
+    nbytes = _native.load().tf_fp8_block_gemm_workspace_bytes(m, n, kp) if m > 0 else 0
+    if nbytes < 0:
+        raise ValueError("block_fp8_gemm: bad shape")
+    scratch = torch.empty((nbytes,), dtype=torch.uint8, device=xq.device) if nbytes else None
     _native.call("tf_fp8_block_gemm", _ptr(xq), xq.stride(0), _ptr(x_scale),
                  _ptr(weight), weight.stride(0), _ptr(ws),
                  0 if ws is None else ws.stride(0), 0 if ws is None else ws.stride(1),
                  block_h, block_w, _ptr(bias), m, n, kp, _ptr(out), out.stride(0),
-                 _stream_ptr(stream, xq.device))
+                 _ptr(scratch), nbytes, _stream_ptr(stream, xq.device))
     return out
 
 
