@@ -35,6 +35,7 @@ constexpr int kDk = 128;
 constexpr int kDv = 128;
 constexpr int kThreads = 256;
 constexpr int kRowGroups = kThreads / 32;   // 8 row groups of 16 rows
+constexpr int kColBlk = kDv / (kThreads / kWave);   // extend: state columns per wave (32)
 
 struct GdnArgs {
   const uint16_t* qkv;   // bf16 [B, conv_dim]
@@ -275,7 +276,7 @@ __global__ void __launch_bounds__(kThreads) gdn_qk_ext_kernel(GdnArgs a) {
     const float n = sqrtf(t < kDk ? s_sum[p][0] + s_sum[p][1] : s_sum[p][2] + s_sum[p][3]);
     const float xn = x / fmaxf(n, 1e-12f);
     // Row j of q (or k) is stored at (j % 8) 16 + j / 8, so the recurrence
-    // thread that owns rows g, g + 8, ... reads them as 16 consecutive floats.
+    // lane that owns rows rg, rg + 8, ... reads them as 16 consecutive floats.
     float* qk = a.wqk + ((int64_t)tok * a.hk + hk) * (2 * kDk);
     qk[(t & kDk) + (j % kRowGroups) * 16 + j / kRowGroups] =
         t < kDk ? xn * 0.08838834764831845f : xn;     // q (x 128 ** -0.5), then k
@@ -289,97 +290,153 @@ __global__ void __launch_bounds__(kThreads) gdn_qk_ext_kernel(GdnArgs a) {
   }
 }
 
+// global_load_lds_dword{,x4} with a scalar base and a 32-bit lane offset: lane
+// l's 4 / 16 bytes land at LDS address M0 + 4 l / 16 l.  The compiler does not
+// count these loads: readers wait with an explicit s_waitcnt vmcnt and a
+// barrier.
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
+}
+__device__ __forceinline__ void dma4(const void* sbase, uint32_t voff, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dword %0, %1"
+               :: "v"(voff), "s"(sbase), "s"(lds) : "m0");
+}
+__device__ __forceinline__ void dma16(const void* sbase, uint32_t voff, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1"
+               :: "v"(voff), "s"(sbase), "s"(lds) : "m0");
+}
+
 // The recurrence of one (request, value head) over the request's tokens, the
-// state in registers throughout.  Per token only the state-dependent work is
-// serial: S = alpha S, S^T k (reduced through LDS), delta, S += k delta^T,
-// S^T q (reduced through LDS), o = bf16(S^T q).  The two reductions use
-// separate LDS buffers, so one barrier after each suffices; the next token's
-// inputs (this thread's 16 rows of q and k, 4 values of v, alpha, beta) are
-// loaded while the current token runs.
+// state in registers throughout.  Every per-token quantity is column-local
+// (S^T k, the delta-rule update, S^T q), so each wave owns 32 state columns
+// and runs independently: lane (rg, cq) = (lane / 8, lane % 8) holds rows
+// rg + 8 i (i < 16) of columns 32 w + 4 cq .. + 3, and the two row sums per
+// token are shuffle reductions over the wave's 8 row groups.  Token inputs
+// (normalised q / k, v, gates) reach LDS by DMA 16 tokens at a time, one
+// block ahead, two buffers; a barrier per block, none per token.
+constexpr int kBlkTok = 16;
+struct ExtBuf {
+  float qk[kBlkTok][2 * kDk];          // 16 KB, rows permuted as written by gdn_qk_ext_kernel
+  uint16_t v[kBlkTok][kDv];            // 4 KB
+  float gates[kThreads / kWave][64];   // 1 KB: per wave, token j's alpha, beta at 2 j
+};
+
+// Sum over lanes l, l ^ 8, l ^ 16, ..., l ^ 56 (the wave's 8 row groups), all
+// in VALU exchanges: DPP row_ror:8 (l ^ 8 within a 16-lane row), then
+// v_permlane16_swap (l ^ 16) and v_permlane32_swap (l ^ 32), each of which
+// returns the lane's own value and its partner's.
+__device__ __forceinline__ float sum8(float x) {
+  x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x128, 0xf, 0xf, false));
+  const auto p16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false,
+                                                    false);
+  x = __uint_as_float(p16[0]) + __uint_as_float(p16[1]);
+  const auto p32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false,
+                                                    false);
+  return __uint_as_float(p32[0]) + __uint_as_float(p32[1]);
+}
+__device__ __forceinline__ f32x4 sum_row_groups(f32x4 v) {
+  return f32x4{sum8(v[0]), sum8(v[1]), sum8(v[2]), sum8(v[3])};
+}
+
 __global__ void __launch_bounds__(kThreads) gdn_recur_ext_kernel(GdnArgs a) {
-  __shared__ float s_vp[kRowGroups][kDv], s_op[kRowGroups][kDv];
+  __shared__ __attribute__((aligned(16))) ExtBuf sb[2];
   const int bi = blockIdx.x / a.hv, h = blockIdx.x % a.hv;
   const int hk = h / a.vpk;
-  const int t = threadIdx.x;
+  const int lane = threadIdx.x & (kWave - 1), w = wave_id();
   const int64_t r = a.req[bi];
   if (r < 0 || r >= a.n_slots) return;
   const int t0 = min(max(a.tok[bi], 0), a.rows), t1 = min(max(a.tok[bi + 1], t0), a.rows);
   if (t1 <= t0) return;
+  const int last = t1 - 1;
+  const int nblk = (t1 - t0 + kBlkTok - 1) / kBlkTok;
 
-  const int d0 = 4 * (t & 31), g = t >> 5;
+  const int rg = lane >> 3, cq = lane & 7;
+  const int d0 = kColBlk * w + 4 * cq;         // first of this lane's 4 columns
   float* S = a.ssm + r * a.ssm_ss + (int64_t)h * kDk * kDv;
   f32x4 s[16];
 #pragma unroll
   for (int i = 0; i < 16; ++i)
-    s[i] = *reinterpret_cast<const f32x4*>(S + (g + kRowGroups * i) * kDv + d0);
+    s[i] = *reinterpret_cast<const f32x4*>(S + (rg + kRowGroups * i) * kDv + d0);
 
-  struct In {
-    float q[16], k[16];
-    u32x2 v;
-    float alpha, beta;
-  };
-  auto fetch = [&](int tok) {
-    In in;
-    const float* qk = a.wqk + ((int64_t)tok * a.hk + hk) * (2 * kDk) + g * 16;
+  // Block bl (tokens t0 + 16 bl ..; past the last token: the last token) into
+  // buffer bf.  Per thread: 4 + 1 + 1 loads.
+  const uint8_t* qk_base = reinterpret_cast<const uint8_t*>(a.wqk) + (int64_t)hk * 2 * kDk * 4;
+  const uint8_t* v_base = reinterpret_cast<const uint8_t*>(a.ws) + ((int64_t)2 * a.key_dim + h * kDv) * 2;
+  const uint8_t* g_base = reinterpret_cast<const uint8_t*>(a.wg) + (int64_t)h * 8;
+  auto issue = [&](int bl, int bf) {
+    const int tb = t0 + kBlkTok * bl;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const f32x4 q4 = *reinterpret_cast<const f32x4*>(qk + 4 * i);
-      const f32x4 k4 = *reinterpret_cast<const f32x4*>(qk + kDk + 4 * i);
+      const int j = 4 * i + w;
+      const int tok = min(tb + j, last);
+      dma16(qk_base + (int64_t)tok * a.hk * 2 * kDk * 4, 16 * lane, lds_addr(&sb[bf].qk[j][0]));
+    }
+    {
+      const int tok = min(tb + 4 * w + lane / 16, last);
+      dma16(v_base, (uint32_t)tok * (uint32_t)a.conv_dim * 2u + 16u * (lane & 15),
+            lds_addr(&sb[bf].v[4 * w][0]));
+    }
+    {
+      const int d = lane & 31;
+      const int tok = min(tb + d / 2, last);
+      dma4(g_base, (uint32_t)tok * (uint32_t)a.hv * 8u + 4u * (d & 1),
+           lds_addr(&sb[bf].gates[w][0]));
+    }
+  };
+  issue(0, 0);
+  issue(min(1, nblk - 1), 1);
+  asm volatile("s_waitcnt vmcnt(6)" ::: "memory");
+  __syncthreads();
+
+  for (int bl = 0; bl < nblk; ++bl) {
+    const ExtBuf& B = sb[bl & 1];
+    const int tb = t0 + kBlkTok * bl;
+    const int ntok = min(kBlkTok, t1 - tb);
+    for (int j = 0; j < ntok; ++j) {
+      const float* qk = &B.qk[j][rg * 16];
+      const float2 gt = *reinterpret_cast<const float2*>(&B.gates[w][2 * j]);
+      f32x4 vp[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};   // two chains
 #pragma unroll
-      for (int c = 0; c < 4; ++c) {
-        in.q[4 * i + c] = q4[c];
-        in.k[4 * i + c] = k4[c];
+      for (int i4 = 0; i4 < 4; ++i4) {
+        const f32x4 k4 = *reinterpret_cast<const f32x4*>(qk + kDk + 4 * i4);
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          s[4 * i4 + c] *= gt.x;
+          vp[c & 1] += s[4 * i4 + c] * k4[c];
+        }
+      }
+      const f32x4 v_pred = sum_row_groups(vp[0] + vp[1]);
+      const u32x2 vb = *reinterpret_cast<const u32x2*>(&B.v[j][d0]);
+      const f32x4 vv = {bf16_lo(vb[0]), bf16_hi(vb[0]), bf16_lo(vb[1]), bf16_hi(vb[1])};
+      const f32x4 delta = gt.y * (vv - v_pred);
+      f32x4 op[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
+#pragma unroll
+      for (int i4 = 0; i4 < 4; ++i4) {
+        const f32x4 k4 = *reinterpret_cast<const f32x4*>(qk + kDk + 4 * i4);
+        const f32x4 q4 = *reinterpret_cast<const f32x4*>(qk + 4 * i4);
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          s[4 * i4 + c] += k4[c] * delta;
+          op[c & 1] += s[4 * i4 + c] * q4[c];
+        }
+      }
+      const f32x4 o = sum_row_groups(op[0] + op[1]);
+      if (rg == 0) {
+        u32x2 pk;
+        pk[0] = pack_bf16(o[0], o[1]);   // .to(orig_dtype)
+        pk[1] = pack_bf16(o[2], o[3]);
+        *reinterpret_cast<u32x2*>(a.wcore + (int64_t)(tb + j) * (a.hv * kDv) + h * kDv + d0) = pk;
       }
     }
-    const uint16_t* y = a.ws + (int64_t)tok * a.conv_dim;
-    in.v = *reinterpret_cast<const u32x2*>(y + 2 * a.key_dim + h * kDv + d0);
-    const float2 gt = *reinterpret_cast<const float2*>(a.wg + ((int64_t)tok * a.hv + h) * 2);
-    in.alpha = gt.x;
-    in.beta = gt.y;
-    return in;
-  };
-  In nxt = fetch(t0);
-  for (int tok = t0; tok < t1; ++tok) {
-    const In cur = nxt;
-    // Unconditional (the last token re-reads itself): a branch here makes the
-    // compiler wait for these loads right after issuing them.
-    nxt = fetch(min(tok + 1, t1 - 1));
-    f32x4 vp = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      s[i] *= cur.alpha;
-      vp += s[i] * cur.k[i];
-    }
-    *reinterpret_cast<f32x4*>(&s_vp[g][d0]) = vp;
+    __syncthreads();                              // every wave is done with this buffer
+    issue(min(bl + 2, nblk - 1), bl & 1);          // refill it (a re-read past the end)
+    asm volatile("s_waitcnt vmcnt(6)" ::: "memory");   // block bl + 1 has landed
     __syncthreads();
-    const f32x4 vv = {bf16_lo(cur.v[0]), bf16_hi(cur.v[0]), bf16_lo(cur.v[1]),
-                      bf16_hi(cur.v[1])};
-    f32x4 delta;
-#pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      float v_pred = 0.f;
-#pragma unroll
-      for (int q = 0; q < kRowGroups; ++q) v_pred += s_vp[q][d0 + c];
-      delta[c] = cur.beta * (vv[c] - v_pred);
-    }
-    f32x4 op = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      s[i] += cur.k[i] * delta;
-      op += s[i] * cur.q[i];
-    }
-    *reinterpret_cast<f32x4*>(&s_op[g][d0]) = op;
-    __syncthreads();
-    if (t < kDv) {
-      float o = 0.f;
-#pragma unroll
-      for (int q = 0; q < kRowGroups; ++q) o += s_op[q][t];
-      a.wcore[(int64_t)tok * (a.hv * kDv) + h * kDv + t] = to_bf(o);   // .to(orig_dtype)
-    }
   }
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 #pragma unroll
   for (int i = 0; i < 16; ++i)
-    *reinterpret_cast<f32x4*>(S + (g + kRowGroups * i) * kDv + d0) = s[i];
+    *reinterpret_cast<f32x4*>(S + (rg + kRowGroups * i) * kDv + d0) = s[i];
 }
 
 // Gated RMSNorm (rms_norm_gated.py:26-40) of every value head of one token
