@@ -9,29 +9,33 @@
 // Work item (from tf_attn_plan_extend): (request b, kv head hk, row0).  The
 // rows of a (b, hk) pair are the ext_b * G flattened (token t, q head h) pairs
 // of the kv head's q-head group, row = t * G + h; an item covers 256 of them,
-// 64 per wave as two 32-row MFMA blocks, so all G heads of a GQA group share
-// every K/V tile and every K or V fragment read from LDS feeds two MFMAs.
+// 32 per wave (one 32-row MFMA block) over 8 waves, so all G heads of a GQA
+// group share every K/V tile staged in LDS.
 // Row (t, h) attends to context positions 0 .. P + t, P = L - ext.
 //
-// Per 32-key tile each wave computes, with v_mfma_f32_32x32x16_bf16 and for
-// both of its row blocks,
+// Per 32-key tile each wave computes, with v_mfma_f32_32x32x16_bf16,
 //   S^T[key, row] = K Q^T        (Q^T register-resident, K from LDS),
 //   the online softmax per row (a row's 32 scores live in lanes n and n + 32),
 //   O^T[dim, row] += V^T P^T     (V^T read from row-major V in LDS with
 //                                 ds_read_b64_tr_b16, P^T packed from S^T),
-// so each lane owns one row per block: its max, sum and 128 output dims.
-// Two row blocks per wave halve the LDS bytes per MFMA FLOP: at the MFMA peak
-// rate the 4 waves of a CU read 64 B/clk of K and V fragments.
+// so each lane owns one row: its max, sum and 128 output dims.
+//
+// Two waves per SIMD, half a step apart.  O^T (128 registers) and Q^T (64)
+// of a 32-row block leave room for a second wave on each SIMD.  Waves 0-3
+// ("lead") run QK^T(j), softmax(j), PV(j) between barriers j - 1 and j; waves
+// 4-7 ("trail", one per SIMD beside a lead wave) run PV(j - 1), QK^T(j),
+// softmax(j).  So while one wave of a SIMD works through its softmax the other
+// issues MFMAs, and each wave's waits (LDS, barrier, MFMA results) are covered
+// by the other wave's work.
 //
 // Staging: K and V rows go from global memory straight into LDS
-// (global_load_lds_dwordx4, 1 KB = two keys per instruction, 4 + 4 per wave
-// per tile) two tiles ahead, into 3 K stages and 4 V stages (V is read one
-// tile later than K), one pair per QK^T MFMA; one barrier per tile.  Slot ids
-// reach LDS the same way, 1024 keys at a time (the low dword of each
-// req_to_token entry).  Each tile's softmax runs beside the neighbouring
-// tiles' MFMAs (see "one step" below).
-// The running max is raised lazily: the accumulators are rescaled only when a
-// row's max grows by more than 2^8 (exact in exact arithmetic; p <= 2^8).
+// (global_load_lds_dwordx4, 1 KB = two keys per instruction, 2 + 2 per wave
+// per tile) two tiles ahead, into 3 K stages and 4 V stages (the trailing
+// waves read V one tile later than K), one barrier per tile.  Slot ids reach
+// LDS the same way, 1024 keys at a time (the low dword of each req_to_token
+// entry).  The running max is raised lazily: the accumulators are rescaled
+// only when a row's max grows by more than 2^8 (exact in exact arithmetic;
+// p <= 2^8).
 #include <math.h>
 
 #include "tf_common.h"
@@ -45,9 +49,10 @@ typedef short i16x4 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
 
 constexpr int kD = 256;
-constexpr int kWaves = 4;
+constexpr int kWaves = 8;
+constexpr int kLeadWaves = kWaves / 2;
 constexpr int kThreads = kWaves * kWave;
-constexpr int kRowsPerWave = 64;                     // two 32-row MFMA blocks
+constexpr int kRowsPerWave = 32;                     // one 32-row MFMA block
 static_assert(kWaves * kRowsPerWave == kExtendItemRows, "item rows");
 constexpr int kBN = 32;                              // keys per tile
 constexpr int kRowBytes = 2 * kD;                    // 512
@@ -61,15 +66,15 @@ constexpr int kKStage = (kBN / 2) * kKPair;          // 16896
 // vswz(n) = 10 (n & 1) + 4 ((n >> 1) & 1), which makes every transposing read
 // (4 keys x 64 B per 32 lanes) conflict-free.
 constexpr int kVStage = kBN * kRowBytes;             // 16384
-constexpr int kAhead = 2;                            // tiles staged ahead of QK^T
+constexpr int kAhead = 2;                            // tiles staged ahead
 constexpr int kStages = kAhead + 1;                  // K stages
 constexpr int kVStages = kAhead + 2;                 // V stages (read one tile later)
 constexpr int kSlotChunk = 1024;
 constexpr int kSlotMask = 2 * kSlotChunk - 1;
 constexpr int kTilesPerSlotChunk = kSlotChunk / kBN;
 constexpr float kRescaleLog2 = 8.f;
-constexpr int kQkAhead = 4;                          // K fragments in flight
-constexpr int kPvAhead = 4;                          // V fragments in flight
+constexpr int kQkAhead = 2;                          // K fragments in flight
+constexpr int kPvAhead = 2;                          // V fragments in flight
 
 struct __attribute__((aligned(16))) Smem {
   uint8_t k[kStages * kKStage];
@@ -96,33 +101,21 @@ __device__ __forceinline__ void dma16(const void* gptr, uint32_t lds) {
                :: "v"(gptr), "s"(lds) : "m0");
 }
 
-// End of step j: tile j + 1 (issued at step j + 1 - kAhead) must have landed;
-// the 8 loads per tile of the newer kAhead - 1 tiles may still be in flight.
+// End of a step: the tile issued one step earlier must have landed; the 4
+// loads per wave of the tile issued in this step may still be in flight.
 __device__ __forceinline__ void vm_wait_staged() {
-  static_assert(kAhead == 2 || kAhead == 3, "vmcnt immediates");
-  if (kAhead == 2)
-    asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
-  else
-    asm volatile("s_waitcnt vmcnt(16)" ::: "memory");
+  static_assert(kAhead == 2, "vmcnt immediate");
+  asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
 }
 
 // Slot ids of keys [chunk * 1024, +1024) clamped to [0, kend): wave w moves
-// 256 of them (4 dword instructions) into slot-buffer half chunk & 1.
+// 128 of them (2 dword instructions) into slot-buffer half chunk & 1.
 __device__ __forceinline__ void slot_issue(const int64_t* rtt, int chunk, int kend, int w,
                                            int lane, int32_t* slots) {
-  const int key0 = chunk * kSlotChunk + 256 * w;
-  const uint32_t dst = lds_addr(slots + (chunk & 1) * kSlotChunk + 256 * w);
+  const int key0 = chunk * kSlotChunk + 128 * w;
+  const uint32_t dst = lds_addr(slots + (chunk & 1) * kSlotChunk + 128 * w);
 #pragma unroll
-  for (int i = 0; i < 4; ++i) dma4(rtt + min(key0 + 64 * i + lane, kend - 1), dst + 256 * i);
-}
-
-// Wave w stages keys 8w .. 8w + 7 of a tile: instruction p moves keys
-// 8w + 2p + {0, 1}; lane l fills 16-byte position l % 32 of key 8w + 2p + l / 32.
-// The slot id is clamped into the pool where it is used, so that a stray
-// req_to_token entry can never address memory outside the pool.
-__device__ __forceinline__ int32_t stage_slot(const int32_t* slots, int tile, int w, int g,
-                                              int p) {
-  return slots[(tile * kBN + 8 * w + 2 * p + g) & kSlotMask];
+  for (int i = 0; i < 2; ++i) dma4(rtt + min(key0 + 64 * i + lane, kend - 1), dst + 256 * i);
 }
 
 // Per-lane global bases: lane l loads 16-byte chunk (l % 32) ^ (key & 1) of a
@@ -142,55 +135,39 @@ __device__ __forceinline__ StageBases stage_bases(const uint8_t* kb, const uint8
   return sb;
 }
 
-// Row `slot` (clamped into the pool) of K and V: one 32 x 32 -> 64-bit
-// multiply-add per address (slot ids and the slot stride fit 32 bits).
-__device__ __forceinline__ void kv_issue(const StageBases& sb, uint32_t slot_bytes, int32_t slot,
-                                         int32_t smax, int w, int p, uint8_t* kst, uint8_t* vst) {
-  const uint64_t off = (uint64_t)(uint32_t)min(max(slot, 0), smax) * slot_bytes;
-  dma16(sb.k + off, lds_addr(kst + (4 * w + p) * kKPair));
-  dma16(sb.v[p & 1] + off, lds_addr(vst + (8 * w + 2 * p) * kRowBytes));
-}
+// What one step stages: wave w moves keys 4w .. 4w + 3 of `tile`; instruction
+// p moves keys 4w + 2p + {0, 1}, lane l filling 16-byte position l % 32 of key
+// 4w + 2p + l / 32.  The slot id is clamped into the pool where it is used, so
+// that a stray req_to_token entry can never address memory outside the pool.
+struct Stager {
+  StageBases sb;
+  const int32_t* slots;
+  uint8_t* k_dst;
+  uint8_t* v_dst;
+  uint32_t slot_bytes;
+  int32_t smax;
+  int tile;
+  int w;
+  int g;
+
+  __device__ __forceinline__ int32_t slot(int p) const {
+    return slots[(tile * kBN + 4 * w + 2 * p + g) & kSlotMask];
+  }
+  // Row `slot` of K and V: one 32 x 32 -> 64-bit multiply-add per address
+  // (slot ids and the slot stride fit 32 bits).
+  __device__ __forceinline__ void issue(int32_t sl, int p) const {
+    const uint64_t off = (uint64_t)(uint32_t)min(max(sl, 0), smax) * slot_bytes;
+    dma16(sb.k + off, lds_addr(k_dst + (2 * w + p) * kKPair));
+    dma16(sb.v[p & 1] + off, lds_addr(v_dst + (4 * w + 2 * p) * kRowBytes));
+  }
+};
 
 // ---------------------------------------------------------------- MFMAs
-// Register files: O^T (2 blocks x 8 tiles x 16 fp32) fills all 256 AGPRs, so
-// S^T must come out of its MFMAs in VGPRs.  This file is compiled with
-// -mllvm --amdgpu-mfma-vgpr-form=1, which gives the builtin MFMAs (S^T = K Q^T)
-// VGPR results; the PV MFMAs are written as inline assembly with their
-// accumulator bound to AGPRs ("+a").  The hazard recognizer cannot see inside
-// that assembly, so it carries its own wait states: two ahead of each MFMA for
-// sources a VALU just wrote, and 20 (more than the 19 an XDL result needs)
-// after the last MFMA of a phase, inside the same statement, so that no copy
-// or read the compiler places after the phase can see an unfinished tile.
-// acc_settle() issues the same 20 where the accumulators are rewritten.
-template <bool kLast>
-__device__ __forceinline__ void mfma_acc(f32x16& d, const u32x4& a, const u32x4& b) {
-  if (kLast)
-    asm volatile("s_nop 1\n\tv_mfma_f32_32x32x16_bf16 %0, %1, %2, %0\n\t"
-                 "s_nop 7\n\ts_nop 7\n\ts_nop 3"
-                 : "+a"(d) : "v"(a), "v"(b));
-  else
-    asm volatile("s_nop 1\n\tv_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+a"(d) : "v"(a), "v"(b));
-}
-__device__ __forceinline__ void acc_settle() { asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 3"); }
-
-// Multiplies an accumulator tile held in AGPRs by a per-lane factor one
-// register at a time, so the tile never has to live in VGPRs.  The caller runs
-// it only when no MFMA has written the tile within the last 19 wait states,
-// and issues acc_settle() before an MFMA next reads it.
-__device__ __forceinline__ void scale_acc(f32x16& x, float f) {
-#pragma unroll
-  for (int i = 0; i < 16; ++i) {
-    float e = x[i];
-    float tmp;
-    asm volatile(
-        "v_accvgpr_read_b32 %1, %0\n\t"
-        "v_mul_f32 %1, %1, %2\n\t"
-        "v_accvgpr_write_b32 %0, %1"
-        : "+a"(e), "=&v"(tmp)
-        : "v"(f));
-    x[i] = e;
-  }
-}
+// Register file: at two waves per SIMD each wave has 256 registers; O^T
+// (8 tiles x 16 fp32), Q^T (64) and S^T (16) all live in VGPRs.  This file is
+// compiled with -mllvm --amdgpu-mfma-vgpr-form=1, which makes the builtin
+// MFMAs read and write their accumulators in VGPRs, so no AGPR copies are
+// needed and the compiler sees, and spaces, every MFMA dependency itself.
 // ---------------------------------------------------------------- PV operand
 // A operand of step q4 for output dims 32 mt + n: register j of lane (g, n)
 // is V[key 16 q4 + 8 (j / 4) + 4 g + j % 4][32 mt + n], the key order in which
@@ -209,11 +186,73 @@ __device__ __forceinline__ u32x4 v_frag(const uint8_t* vst, const int (&vaddr)[4
   return u32x4{lo[0], lo[1], hi[0], hi[1]};
 }
 
+// ---------------------------------------------------------------- phases
+// Each MFMA phase is one stream of 16 MFMAs with the other work placed one
+// item per MFMA (sched_barrier regions, MFMA first in each region): the
+// fragment reads kQkAhead / kPvAhead MFMAs ahead and, when the phase carries
+// the step's staging, the slot-id reads at MFMA 0 and the two K / V row pairs
+// at MFMAs 2 and 3.
+template <bool kStage>
+__device__ __forceinline__ void qk_phase(const uint8_t* kst, int kaddr, const u32x4 (&qf)[16],
+                                         f32x16& s, const Stager& st) {
+  u32x4 fr[kQkAhead + 1];
+  __builtin_amdgcn_s_setprio(1);
+#pragma unroll
+  for (int i = 0; i < kQkAhead; ++i) fr[i] = ld_s16(kst + kaddr + 32 * i);
+  int32_t ss[2];
+#pragma unroll
+  for (int kk = 0; kk < 16; ++kk) {
+    __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+    __builtin_amdgcn_sched_group_barrier(0x7f7, 64, 0);
+    if (kk + kQkAhead < 16)
+      fr[(kk + kQkAhead) % (kQkAhead + 1)] = ld_s16(kst + kaddr + 32 * (kk + kQkAhead));
+    s = mfma_32x32x16(fr[kk % (kQkAhead + 1)], qf[kk], kk == 0 ? f32x16{} : s);
+    if (kStage) {
+      if (kk == 0) {
+        ss[0] = st.slot(0);
+        ss[1] = st.slot(1);
+      } else if (kk == 2 || kk == 3) {
+        st.issue(ss[kk - 2], kk - 2);
+      }
+    }
+  }
+  __builtin_amdgcn_sched_barrier(0);
+}
+
+template <bool kStage>
+__device__ __forceinline__ void pv_phase(const uint8_t* vst, const int (&vaddr)[4],
+                                         f32x16 (&acc)[8], const u32x4 (&pt)[2],
+                                         const Stager& st) {
+  u32x4 fr[kPvAhead + 1];
+  __builtin_amdgcn_s_setprio(0);
+#pragma unroll
+  for (int f = 0; f < kPvAhead; ++f) fr[f] = v_frag(vst, vaddr, f);
+  int32_t ss[2];
+#pragma unroll
+  for (int f = 0; f < 16; ++f) {
+    __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+    __builtin_amdgcn_sched_group_barrier(0x7f7, 64, 0);
+    if (f + kPvAhead < 16) fr[(f + kPvAhead) % (kPvAhead + 1)] = v_frag(vst, vaddr, f + kPvAhead);
+    acc[f & 7] = mfma_32x32x16(fr[f % (kPvAhead + 1)], pt[f >> 3], acc[f & 7]);
+    if (kStage) {
+      if (f == 0) {
+        ss[0] = st.slot(0);
+        ss[1] = st.slot(1);
+      } else if (f == 2 || f == 3) {
+        st.issue(ss[f - 2], f - 2);
+      }
+    }
+  }
+  __builtin_amdgcn_sched_barrier(0);
+}
+
 // ---------------------------------------------------------------- softmax
-// Softmax state of the lane's two rows: reference max m (raw score units),
-// moff = m * sl2, running sum l of p = 2^(s sl2 - moff).
-struct Rows {
-  float m[2], moff[2], l[2];
+// Softmax state of the lane's row: reference max m (raw score units),
+// moff = m * sl2, running sum l of p = 2^(s sl2 - moff) (this lane's half).
+struct Row {
+  float m, moff, l;
 };
 
 __device__ __forceinline__ void mask_tile(f32x16& s, int k0, int g, int limit) {
@@ -229,149 +268,36 @@ __device__ __forceinline__ float half_swap_max(float v) {
   return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
 }
 
-// ---------------------------------------------------------------- one step
-// Step j runs three tiles at once, each phase one MFMA stream with the other
-// work placed one item per MFMA (sched_barrier regions):
-//   phase A: S^T(j) = K(j) Q^T (32 MFMAs) | staging of tile j + 2 (slot ids at
-//            MFMA 0, K and V rows 4-7) | second-half exps of tile j - 1
-//            (MFMAs 12-27);
-//   phase B: O^T += V(j - 1)^T P^T(j - 1) (32 MFMAs) | row max of tile j
-//            (MFMAs 0-7, lane-half swap 8, reference update 9) | first-half
-//            exps of tile j (10-25).
-// Row block rb's P^T operand for 16-key step q4 is pt[rb][q4], p[rb][8 q4 ..
-// 8 q4 + 7] packed to bf16; phase B overwrites pt[rb][0] (consumed by its
-// first 16 MFMAs) with tile j's values from MFMA 17 on.
-template <bool kQk, bool kExp>
-__device__ __forceinline__ void phase_a(const uint8_t* kst, int kaddr, const u32x4 (&qf)[2][16],
-                                        f32x16 (&s)[2], const int32_t* slots, int tile2, int w,
-                                        int lane, int32_t smax, const StageBases& sb,
-                                        uint32_t slot_bytes, uint8_t* k_dst, uint8_t* v_dst,
-                                        const float (&sh)[2][8], Rows& rows, float sl2,
-                                        u32x4 (&pt)[2][2]) {
-  auto kread = [&](int kk) { return ld_s16(kst + kaddr + 32 * kk); };
-  u32x4 fr[kQkAhead + 1];
-  if (kQk) {
+// Row max of the tile, the lazy reference-max update, and P^T packed to bf16:
+// pt[q4] holds p for keys 16 q4 + 8 (j / 4) + 4 g + j % 4, two per dword, the
+// B operand of PV step q4.  Returns whether any row of the wave raised its
+// reference max (alpha is then the lane's factor for the accumulators).
+__device__ __forceinline__ bool softmax_tile(const f32x16& s, Row& row, float sl2,
+                                             u32x4 (&pt)[2], float& alpha) {
+  float mx = s[0];
 #pragma unroll
-    for (int i = 0; i < kQkAhead; ++i) fr[i] = kread(i);
-  }
-  int32_t ss[4];
-  float p[2][8];
+  for (int r = 1; r < 16; ++r) mx = fmaxf(mx, s[r]);
+  mx = half_swap_max(mx);
+  // Lazy reference max, per row: raised only when the row outgrew it by more
+  // than 2^kRescaleLog2.  The wave-wide vote only decides whether the rescale
+  // runs at all.
+  const bool grow = (mx - row.m) * sl2 > kRescaleLog2;
+  const float mnew = grow ? mx : row.m;
+  alpha = grow ? fast_exp2((row.m - mnew) * sl2) : 1.f;
+  row.l *= alpha;
+  row.m = mnew;
+  row.moff = mnew * sl2;
 #pragma unroll
-  for (int i = 0; i < 32; ++i) {
-    const int kk = i >> 1, rb = i & 1;
-    // One region per MFMA: the MFMA issues first, this region's other work
-    // follows it and overlaps its 32 cycles.
-    __builtin_amdgcn_sched_barrier(0);
-    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-    __builtin_amdgcn_sched_group_barrier(0x7f7, 64, 0);
-    if (kQk) {
-      if (rb == 0 && kk + kQkAhead < 16) fr[(kk + kQkAhead) % (kQkAhead + 1)] = kread(kk + kQkAhead);
-      s[rb] = mfma_32x32x16(fr[kk % (kQkAhead + 1)], qf[rb][kk], kk == 0 ? f32x16{} : s[rb]);
-      if (i == 0) {
+  for (int q4 = 0; q4 < 2; ++q4) {
 #pragma unroll
-        for (int q = 0; q < 4; ++q) ss[q] = stage_slot(slots, tile2, w, lane >> 5, q);
-      } else if (i >= 4 && i < 8) {
-        kv_issue(sb, slot_bytes, ss[i - 4], smax, w, i - 4, k_dst, v_dst);
-      }
-    }
-    if (!kExp) continue;
-    if (i >= 12 && i < 28) {
-      // Exp e covers score r = e / 2 of block e % 2; each pair is packed as
-      // soon as it is complete.
-      const int e = i - 12, eb = e & 1, r = e >> 1;
-      p[eb][r] = fast_exp2(fmaf(sh[eb][r], sl2, -rows.moff[eb]));
-      if (r & 1) {
-        pt[eb][1][r >> 1] = pack_bf16(p[eb][r - 1], p[eb][r]);
-        rows.l[eb] += p[eb][r - 1] + p[eb][r];
-        // Pin the result here: otherwise it is sunk past the rescale branch
-        // into phase B's block, where it would run ahead of the PV MFMAs.
-        asm volatile("" : "+v"(pt[eb][1][r >> 1]));
-      }
-      if (e == 15) asm volatile("" : "+v"(rows.l[0]), "+v"(rows.l[1]));
+    for (int k = 0; k < 4; ++k) {
+      const float p0 = fast_exp2(fmaf(s[8 * q4 + 2 * k], sl2, -row.moff));
+      const float p1 = fast_exp2(fmaf(s[8 * q4 + 2 * k + 1], sl2, -row.moff));
+      pt[q4][k] = pack_bf16(p0, p1);
+      row.l += p0 + p1;
     }
   }
-  __builtin_amdgcn_sched_barrier(0);
-}
-
-// Phase B; returns, per row block, whether its reference max was raised (the
-// caller then rescales that block's accumulators by alpha).
-template <bool kPv, bool kSoftmax>
-__device__ __forceinline__ void phase_b(const uint8_t* vst, const int (&vaddr)[4],
-                                        f32x16 (&acc)[2][8], const f32x16 (&s)[2], Rows& rows,
-                                        float sl2, u32x4 (&pt)[2][2], float (&sh)[2][8],
-                                        bool (&grew)[2], float (&alpha)[2]) {
-  u32x4 fr[kPvAhead + 1];
-  if (kPv) {
-#pragma unroll
-    for (int f = 0; f < kPvAhead; ++f) fr[f] = v_frag(vst, vaddr, f);
-  }
-  float mx[2];
-  float p[2][8];
-  uint32_t p_pair[2][4];
-#pragma unroll
-  for (int i = 0; i < 32; ++i) {
-    const int f = i >> 1, rb = i & 1;
-    __builtin_amdgcn_sched_barrier(0);   // MFMA first, as in phase_a
-    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-    __builtin_amdgcn_sched_group_barrier(0x7f7, 64, 0);
-    if (kPv) {
-      if (rb == 0 && f + kPvAhead < 16)
-        fr[(f + kPvAhead) % (kPvAhead + 1)] = v_frag(vst, vaddr, f + kPvAhead);
-      if (i < 31)
-        mfma_acc<false>(acc[rb][f & 7], fr[f % (kPvAhead + 1)], pt[rb][f >> 3]);
-      else
-        mfma_acc<true>(acc[rb][f & 7], fr[f % (kPvAhead + 1)], pt[rb][f >> 3]);
-    }
-    if (kSoftmax) {
-      if (i < 8) {
-        const int mb = i >> 2, q = i & 3;
-        if (q == 0) mx[mb] = s[mb][0];
-#pragma unroll
-        for (int r = 4 * q; r < 4 * q + 4; ++r)
-          if (r > 0) mx[mb] = fmaxf(mx[mb], s[mb][r]);
-      } else if (i == 8) {
-#pragma unroll
-        for (int mb = 0; mb < 2; ++mb) mx[mb] = half_swap_max(mx[mb]);
-      } else if (i == 9) {
-        // Lazy reference max, per row: raised only when the row outgrew it by
-        // more than 2^kRescaleLog2 (exact in exact arithmetic; p <= 2^8).  The
-        // wave-wide vote only decides whether the rescale runs at all.
-#pragma unroll
-        for (int mb = 0; mb < 2; ++mb) {
-          const bool grow = (mx[mb] - rows.m[mb]) * sl2 > kRescaleLog2;
-          const float mnew = grow ? mx[mb] : rows.m[mb];
-          alpha[mb] = grow ? fast_exp2((rows.m[mb] - mnew) * sl2) : 1.f;
-          rows.l[mb] *= alpha[mb];
-          rows.m[mb] = mnew;
-          rows.moff[mb] = mnew * sl2;
-          grew[mb] = __ballot(grow) != 0;
-        }
-      } else if (i >= 10 && i < 26) {
-        const int e = i - 10, eb = e & 1, r = e >> 1;
-        p[eb][r] = fast_exp2(fmaf(s[eb][r], sl2, -rows.moff[eb]));
-        if (r & 1) {
-          p_pair[eb][r >> 1] = pack_bf16(p[eb][r - 1], p[eb][r]);
-          rows.l[eb] += p[eb][r - 1] + p[eb][r];
-        }
-      } else if (i == 26) {
-#pragma unroll
-        for (int b2 = 0; b2 < 2; ++b2) {
-#pragma unroll
-          for (int r = 0; r < 8; ++r) sh[b2][r] = s[b2][8 + r];
-        }
-      }
-      // pt[.][0] was last read by MFMA 15; pairs 0-1 are complete at MFMA 17,
-      // pairs 2-3 at MFMA 25.
-      if (i == 17 || i == 26) {
-        const int k0 = i == 17 ? 0 : 2;
-#pragma unroll
-        for (int b2 = 0; b2 < 2; ++b2)
-#pragma unroll
-          for (int k = k0; k < k0 + 2; ++k) pt[b2][0][k] = p_pair[b2][k];
-      }
-    }
-  }
-  __builtin_amdgcn_sched_barrier(0);
+  return __ballot(grow) != 0;
 }
 
 __global__ void __launch_bounds__(kThreads) extend_bf16_kernel(ExtendArgs a) {
@@ -402,14 +328,10 @@ __global__ void __launch_bounds__(kThreads) extend_bf16_kernel(ExtendArgs a) {
   const int64_t rrow = clamp_i64(a.rpi[b], 0, a.rtt_rows - 1);
   const int64_t* rtt = a.rtt + rrow * a.rtt_stride;
 
-  // This lane's row in each block; padding lanes (row_ok false) compute a
-  // valid duplicate row and never write it.
-  int limit[2];
-#pragma unroll
-  for (int rb = 0; rb < 2; ++rb) {
-    const int rho = min(row0 + kRowsPerWave * w + 32 * rb + n, rows_total - 1);
-    limit[rb] = P + rho / G;   // last visible key
-  }
+  // This lane's row; padding lanes compute a valid duplicate row and never
+  // write it.
+  const int rho_c = min(row0 + kRowsPerWave * w + n, rows_total - 1);
+  const int limit = P + rho_c / G;   // last visible key
 
   // Keys [0, kend) are needed by the item; keys below w_full are visible to
   // every row of this wave. Every wave runs all n_tiles tiles (keys past a
@@ -424,12 +346,21 @@ __global__ void __launch_bounds__(kThreads) extend_bf16_kernel(ExtendArgs a) {
   const int w_full = w_first < rows_total ? P + w_first / G + 1 : 0;
 
   const float sl2 = a.scale_log2;
-  const uint32_t slot_bytes = (uint32_t)a.hkv * kRowBytes;
-  const StageBases sb = stage_bases(a.k_pool + (int64_t)hk * kRowBytes,
-                                    a.v_pool + (int64_t)hk * kRowBytes, lane);
-  const int32_t smax = (int32_t)min(a.pool_slots - 1, (int64_t)INT32_MAX);
+  Stager st;
+  st.sb = stage_bases(a.k_pool + (int64_t)hk * kRowBytes, a.v_pool + (int64_t)hk * kRowBytes,
+                      lane);
+  st.slots = sm.slots;
+  st.slot_bytes = (uint32_t)a.hkv * kRowBytes;
+  st.smax = (int32_t)min(a.pool_slots - 1, (int64_t)INT32_MAX);
+  st.w = w;
+  st.g = g;
+  auto stage_for = [&](int j) {
+    st.tile = min(j + kAhead, last);
+    st.k_dst = sm.k + ((j + kAhead) % kStages) * kKStage;
+    st.v_dst = sm.v + ((j + kAhead) % kVStages) * kVStage;
+  };
 
-  // LDS read offsets of this lane (see kv_issue / v_frag).
+  // LDS read offsets of this lane (see Stager::issue / v_frag).
   const int kaddr = (n >> 1) * kKPair + (n & 1) * kRowBytes + 16 * (g ^ (n & 1));
   int vaddr[4];
   {
@@ -442,35 +373,23 @@ __global__ void __launch_bounds__(kThreads) extend_bf16_kernel(ExtendArgs a) {
     for (int m2 = 0; m2 < 4; ++m2) vaddr[m2] = base + 64 * (m2 ^ (sw >> 2));
   }
 
-  // Q^T fragments: lane (g, n) holds q[row n of block rb][16 kk + 8 g .. +8].
-  u32x4 qf[2][16];
-#pragma unroll
-  for (int rb = 0; rb < 2; ++rb) {
-    const int rho = min(row0 + kRowsPerWave * w + 32 * rb + n, rows_total - 1);
-    const int t = rho / G, h = rho - t * G;
+  // Q^T fragments: lane (g, n) holds q[row n][16 kk + 8 g .. +8].
+  u32x4 qf[16];
+  {
+    const int t = rho_c / G, h = rho_c - t * G;
     const __bf16* qp = a.q + (int64_t)(q_start + t) * a.q_stride + (int64_t)(hk * G + h) * kD;
 #pragma unroll
-    for (int kk = 0; kk < 16; ++kk) qf[rb][kk] = ld_g16(qp + 16 * kk + 8 * g);
+    for (int kk = 0; kk < 16; ++kk) qf[kk] = ld_g16(qp + 16 * kk + 8 * g);
   }
   // Consume Q here so that the compiler waits for these loads before the
   // loop; inside it, vmcnt belongs to the staging loads.
 #pragma unroll
-  for (int rb = 0; rb < 2; ++rb)
-#pragma unroll
-    for (int kk = 0; kk < 16; ++kk) asm volatile("" ::"v"(qf[rb][kk]));
+  for (int kk = 0; kk < 16; ++kk) asm volatile("" ::"v"(qf[kk]));
 
-  Rows rows;
+  Row row{-INFINITY, 0.f, 0.f};
+  f32x16 acc[8];
 #pragma unroll
-  for (int rb = 0; rb < 2; ++rb) {
-    rows.m[rb] = -INFINITY;
-    rows.moff[rb] = 0.f;
-    rows.l[rb] = 0.f;
-  }
-  f32x16 acc[2][8];
-#pragma unroll
-  for (int rb = 0; rb < 2; ++rb)
-#pragma unroll
-    for (int i = 0; i < 8; ++i) acc[rb][i] = f32x16{};
+  for (int i = 0; i < 8; ++i) acc[i] = f32x16{};
 
   // ---- prologue: slot ids of the first 1024 keys, then tiles 0 and 1 into
   // stages 0 and 1. Tiles past the last one are stand-ins for the last tile
@@ -481,115 +400,104 @@ __global__ void __launch_bounds__(kThreads) extend_bf16_kernel(ExtendArgs a) {
   __syncthreads();
 #pragma unroll
   for (int tl = 0; tl < kAhead; ++tl) {
-    const int tile = min(tl, last);
+    st.tile = min(tl, last);
+    st.k_dst = sm.k + tl * kKStage;
+    st.v_dst = sm.v + tl * kVStage;
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      kv_issue(sb, slot_bytes, stage_slot(sm.slots, tile, w, g, q), smax, w, q,
-               sm.k + tl * kKStage, sm.v + tl * kVStage);
-    }
+    for (int p = 0; p < 2; ++p) st.issue(st.slot(p), p);
   }
   vm_wait_staged();
   __syncthreads();
 
-  // K tile t lives in K stage t % 3, V tile t in V stage t % 4. Step j stages
-  // tile j + 2 while QK^T reads K(j) and PV reads V(j - 1); the stages it
-  // overwrites held tiles j - 1 (K) and j - 2 (V), finished before the
-  // previous barrier.
-  f32x16 s[2];
-  float sh[2][8];
-  u32x4 pt[2][2];
-  bool grew[2];
-  float alpha[2];
-  // Rescales O^T for the reference max raised in the previous step's phase B;
-  // runs between phase A and phase B, where O^T holds exactly the tiles
-  // before the one whose max raised it.
+  // K tile t lives in K stage t % 3, V tile t in V stage t % 4.  Between
+  // barriers j - 1 and j every wave stages tile j + 2; lead waves read K(j)
+  // and V(j), trailing waves V(j - 1) and K(j).  The stages tile j + 2
+  // overwrites held tiles j - 1 (K) and j - 2 (V), whose last reads came
+  // before barrier j - 1.
+  f32x16 s;
+  u32x4 pt[2];
+  float alpha;
+  auto slot_chunk = [&](int j) {
+    // Slot ids of the next 1024 keys: issued at tile 4 of chunk c into the
+    // half that served chunk c - 1 (last read when tile 32 c - 1 was staged,
+    // before barrier 32 c - 3), first read when tile 32 (c + 1) is staged.
+    if (j % kTilesPerSlotChunk == 4 && (j / kTilesPerSlotChunk + 1) * kSlotChunk < kend)
+      slot_issue(rtt, j / kTilesPerSlotChunk + 1, kend, w, lane, sm.slots);
+  };
+  // Softmax of tile j; `grew` records whether a row's reference max was
+  // raised, and rescale() then scales O^T, which must hold exactly the tiles
+  // before j (it runs right before PV(j)).
+  bool grew = false;
+  auto softmax_step = [&](int j) {
+    const int k0 = j * kBN;
+    if (k0 + kBN > w_full) mask_tile(s, k0, g, limit);
+    grew = softmax_tile(s, row, sl2, pt, alpha) && j > 0;
+  };
   auto rescale = [&]() {
-    if (grew[0] || grew[1]) {
+    if (grew) {
 #pragma unroll
-      for (int rb = 0; rb < 2; ++rb) {
-        if (grew[rb]) {
-#pragma unroll
-          for (int i = 0; i < 8; ++i) scale_acc(acc[rb][i], alpha[rb]);
-        }
-      }
-      acc_settle();
+      for (int i = 0; i < 8; ++i) acc[i] *= alpha;
     }
   };
   auto step_end = [&]() {
-    // Tile j + 1 was issued one step earlier: only this step's 8 tile loads
+    // Tile j + 1 was issued one step earlier: only this step's 4 tile loads
     // may still be in flight.
     vm_wait_staged();
     __syncthreads();
   };
 
-  // Step 0: S^T(0) and the max / first-half exps of tile 0 (no PV yet).
-  phase_a<true, false>(sm.k, kaddr, qf, s, sm.slots, min(kAhead, last), w, lane, smax, sb,
-                       slot_bytes, sm.k + kAhead * kKStage, sm.v + kAhead * kVStage, sh, rows,
-                       sl2, pt);
-  if (kBN > w_full) {
-#pragma unroll
-    for (int rb = 0; rb < 2; ++rb) mask_tile(s[rb], 0, g, limit[rb]);
-  }
-  phase_b<false, true>(sm.v, vaddr, acc, s, rows, sl2, pt, sh, grew, alpha);
-  step_end();
-
-  for (int j = 1; j < n_tiles; ++j) {
-    // Slot ids of the next 1024 keys: issued at tile 4 of chunk c into the
-    // half that served chunk c - 1 (last read when tile 32 c - 1 was staged,
-    // at step 32 c - 3), first read when tile 32 (c + 1) is staged.
-    if (j % kTilesPerSlotChunk == 4 && (j / kTilesPerSlotChunk + 1) * kSlotChunk < kend)
-      slot_issue(rtt, j / kTilesPerSlotChunk + 1, kend, w, lane, sm.slots);
-    const int kst = j % kStages, kst2 = (j + kAhead) % kStages;
-    const int vst = (j - 1) % kVStages, vst2 = (j + kAhead) % kVStages;
-
-    phase_a<true, true>(sm.k + kst * kKStage, kaddr, qf, s, sm.slots, min(j + kAhead, last), w, lane,
-                        smax, sb, slot_bytes, sm.k + kst2 * kKStage, sm.v + vst2 * kVStage, sh, rows, sl2,
-                  pt);
-    const int k0 = j * kBN;
-    if (k0 + kBN > w_full) {
-#pragma unroll
-      for (int rb = 0; rb < 2; ++rb) mask_tile(s[rb], k0, g, limit[rb]);
+  if (w < kLeadWaves) {
+    for (int j = 0; j < n_tiles; ++j) {
+      slot_chunk(j);
+      stage_for(j);
+      qk_phase<true>(sm.k + (j % kStages) * kKStage, kaddr, qf, s, st);
+      softmax_step(j);
+      rescale();
+      pv_phase<false>(sm.v + (j % kVStages) * kVStage, vaddr, acc, pt, st);
+      step_end();
+    }
+  } else {
+    stage_for(0);
+    qk_phase<true>(sm.k, kaddr, qf, s, st);
+    softmax_step(0);
+    step_end();
+    for (int j = 1; j < n_tiles; ++j) {
+      slot_chunk(j);
+      stage_for(j);
+      rescale();
+      pv_phase<true>(sm.v + ((j - 1) % kVStages) * kVStage, vaddr, acc, pt, st);
+      qk_phase<false>(sm.k + (j % kStages) * kKStage, kaddr, qf, s, st);
+      softmax_step(j);
+      step_end();
     }
     rescale();
-    phase_b<true, true>(sm.v + vst * kVStage, vaddr, acc, s, rows, sl2, pt, sh, grew, alpha);
-    step_end();
+    pv_phase<false>(sm.v + (last % kVStages) * kVStage, vaddr, acc, pt, st);
   }
-
-  // Tail: second-half exps and PV of the last tile.
-  phase_a<false, true>(sm.k, kaddr, qf, s, sm.slots, 0, w, lane, smax, sb, slot_bytes, sm.k, sm.v,
-                 sh, rows, sl2, pt);
-  rescale();
-  phase_b<true, false>(sm.v + (last % kVStages) * kVStage, vaddr, acc, s, rows, sl2, pt, sh,
-                       grew, alpha);
   // The last steps staged stand-in tiles nobody reads; they must land before
   // the workgroup's LDS can be handed to another workgroup.
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-  acc_settle();
 
+  const float lt = row.l + __shfl_xor(row.l, 32, kWave);
+  const int rho = row0 + kRowsPerWave * w + n;
+  if (rho >= rows_total) return;
+  const int t = rho / G, h = rho - t * G;
+  const float inv = 1.f / lt;
+  __bf16* o = a.out + (int64_t)(q_start + t) * a.out_stride + (int64_t)(hk * G + h) * kD;
+  const __bf16* gt = a.gate ? a.gate + (int64_t)(q_start + t) * a.gate_stride +
+                                  (int64_t)(hk * G + h) * a.gate_hstride
+                            : nullptr;
 #pragma unroll
-  for (int rb = 0; rb < 2; ++rb) {
-    const float lt = rows.l[rb] + __shfl_xor(rows.l[rb], 32, kWave);
-    const int rho = row0 + kRowsPerWave * w + 32 * rb + n;
-    if (rho >= rows_total) continue;
-    const int t = rho / G, h = rho - t * G;
-    const float inv = 1.f / lt;
-    __bf16* o = a.out + (int64_t)(q_start + t) * a.out_stride + (int64_t)(hk * G + h) * kD;
-    const __bf16* gt = a.gate ? a.gate + (int64_t)(q_start + t) * a.gate_stride +
-                                    (int64_t)(hk * G + h) * a.gate_hstride
-                              : nullptr;
+  for (int mt = 0; mt < 8; ++mt) {
 #pragma unroll
-    for (int mt = 0; mt < 8; ++mt) {
-#pragma unroll
-      for (int rq = 0; rq < 4; ++rq) {
-        const int off = 32 * mt + 8 * rq + 4 * g;
-        u32x2 v = {pack_bf16(acc[rb][mt][4 * rq + 0] * inv, acc[rb][mt][4 * rq + 1] * inv),
-                   pack_bf16(acc[rb][mt][4 * rq + 2] * inv, acc[rb][mt][4 * rq + 3] * inv)};
-        if (gt) {
-          const u32x2 gv = ld_g8(gt + off);
-          v = u32x2{gate_pair(v[0], gv[0]), gate_pair(v[1], gv[1])};
-        }
-        *reinterpret_cast<u32x2*>(o + off) = v;
+    for (int rq = 0; rq < 4; ++rq) {
+      const int off = 32 * mt + 8 * rq + 4 * g;
+      u32x2 v = {pack_bf16(acc[mt][4 * rq + 0] * inv, acc[mt][4 * rq + 1] * inv),
+                 pack_bf16(acc[mt][4 * rq + 2] * inv, acc[mt][4 * rq + 3] * inv)};
+      if (gt) {
+        const u32x2 gv = ld_g8(gt + off);
+        v = u32x2{gate_pair(v[0], gv[0]), gate_pair(v[1], gv[1])};
       }
+      *reinterpret_cast<u32x2*>(o + off) = v;
     }
   }
 }
