@@ -77,13 +77,25 @@ __device__ __forceinline__ uint32_t abs_max8(u32x4 v) {
   return m;
 }
 
+// Grid-stride loops over 16-byte chunks, kUnroll chunks per trip with their
+// loads issued together, so a thread keeps kUnroll loads in flight.
+constexpr int kUnroll = 4;
+
 __global__ void __launch_bounds__(kThreads) act_amax_kernel(QuantArgs a) {
   __shared__ uint32_t red[kThreads / kWave];
   const uint32_t n = a.rows * a.c8;
+  const uint32_t stride = gridDim.x * kThreads;
   uint32_t m = 0;
-  for (uint32_t q = blockIdx.x * kThreads + threadIdx.x; q < n; q += gridDim.x * kThreads) {
-    const uint32_t r = q / a.c8, c = q - r * a.c8;
-    m = max(m, abs_max8(ld_nt16(a.x + r * a.xs + 8 * c)));
+  for (uint32_t q0 = blockIdx.x * kThreads + threadIdx.x; q0 < n; q0 += kUnroll * stride) {
+    u32x4 v[kUnroll];
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      const uint32_t q = q0 + u * stride;
+      const uint32_t r = q / a.c8, c = q - r * a.c8;
+      v[u] = q < n ? ld_nt16(a.x + r * a.xs + 8 * c) : u32x4{0u, 0u, 0u, 0u};
+    }
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) m = max(m, abs_max8(v[u]));
   }
   m = block_max(m, red);
   if (threadIdx.x == 0) a.partial[blockIdx.x] = m;
@@ -106,19 +118,32 @@ __global__ void __launch_bounds__(kThreads) act_quant_kernel(QuantArgs a) {
   if (blockIdx.x == 0 && threadIdx.x == 0) *a.scale_out = scale;
 
   const uint32_t n = a.rows * a.c8;
-  for (uint32_t q = blockIdx.x * kThreads + threadIdx.x; q < n; q += gridDim.x * kThreads) {
-    const uint32_t r = q / a.c8, c = q - r * a.c8;
-    const u32x4 v = ld_nt16(a.x + r * a.xs + 8 * c);
-    u32x2 f;
+  const uint32_t stride = gridDim.x * kThreads;
+  for (uint32_t q0 = blockIdx.x * kThreads + threadIdx.x; q0 < n; q0 += kUnroll * stride) {
+    u32x4 v[kUnroll];
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const uint32_t lo = __builtin_amdgcn_cvt_pk_fp8_f32(sat448(bf16_lo(v[2 * j]) / scale),
-                                                          sat448(bf16_hi(v[2 * j]) / scale),
-                                                          0u, false);
-      f[j] = __builtin_amdgcn_cvt_pk_fp8_f32(sat448(bf16_lo(v[2 * j + 1]) / scale),
-                                             sat448(bf16_hi(v[2 * j + 1]) / scale), lo, true);
+    for (int u = 0; u < kUnroll; ++u) {
+      const uint32_t q = q0 + u * stride;
+      const uint32_t r = q / a.c8, c = q - r * a.c8;
+      v[u] = q < n ? ld_nt16(a.x + r * a.xs + 8 * c) : u32x4{0u, 0u, 0u, 0u};
     }
-    *reinterpret_cast<u32x2*>(a.xq + r * a.qs + 8 * c) = f;
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      const uint32_t q = q0 + u * stride;
+      if (q >= n) break;
+      const uint32_t r = q / a.c8, c = q - r * a.c8;
+      u32x2 f;
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const uint32_t lo = __builtin_amdgcn_cvt_pk_fp8_f32(sat448(bf16_lo(v[u][2 * j]) / scale),
+                                                            sat448(bf16_hi(v[u][2 * j]) / scale),
+                                                            0u, false);
+        f[j] = __builtin_amdgcn_cvt_pk_fp8_f32(sat448(bf16_lo(v[u][2 * j + 1]) / scale),
+                                               sat448(bf16_hi(v[u][2 * j + 1]) / scale), lo,
+                                               true);
+      }
+      *reinterpret_cast<u32x2*>(a.xq + r * a.qs + 8 * c) = f;
+    }
   }
 }
 
@@ -471,8 +496,10 @@ int32_t tf_fp8_act_quant(const void* x, int32_t x_dtype, int64_t rows, int64_t c
   a.partial = static_cast<uint32_t*>(workspace);
   a.scale_out = x_scale;
   const int64_t chunks = rows * (cols / 8);
-  // ~8 chunks (128 B of x) per thread, at most kQuantMaxBlocks workgroups
-  const int64_t want = (chunks + 8 * kThreads - 1) / (8 * kThreads);
+  // ~2 chunks (32 B of x) per thread, at most kQuantMaxBlocks workgroups:
+  // small inputs spread over many CUs (one round of loads each), large ones
+  // loop with kUnroll loads in flight per thread
+  const int64_t want = (chunks + 2 * kThreads - 1) / (2 * kThreads);
   a.nblocks = (uint32_t)std::max<int64_t>(1, std::min<int64_t>(want, kQuantMaxBlocks));
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   hipLaunchKernelGGL(act_amax_kernel, dim3(a.nblocks), dim3(kThreads), 0, s, a);
