@@ -87,7 +87,21 @@ def time_kernel(torch, calls, steps, launch):
         launch(calls[i % len(calls)])
         pairs.append((a, _event(torch, stream)))
     torch.cuda.synchronize()
-    return sum(a.elapsed_time(b) for a, b in pairs) / steps
+    times = sorted(a.elapsed_time(b) for a, b in pairs)
+    _LAST_SPREAD.update(p10=_pct(times, 0.1), p50=_pct(times, 0.5), p90=_pct(times, 0.9))
+    return sum(times) / steps
+
+
+_LAST_SPREAD = {}
+
+
+def _pct(sorted_times, f):
+    return sorted_times[min(len(sorted_times) - 1, int(f * len(sorted_times)))]
+
+
+def last_spread():
+    """p10 / median / p90 (ms) of the launches timed by the last time_kernel call."""
+    return dict(_LAST_SPREAD)
 
 
 def bench_decode(torch, workloads, SlotAttentionCall, args):
@@ -99,6 +113,7 @@ def bench_decode(torch, workloads, SlotAttentionCall, args):
     nbytes = sum(w.decode_bytes() for w in wls) / len(wls)
     ms = time_steps(torch, calls, args.steps, args.warmup, lambda c: [c.run])
     k_ms = time_kernel(torch, calls, args.steps, lambda c: c.run_decode_partial())
+    k_spread = last_spread()
     m_ms = time_kernel(torch, calls, args.steps, lambda c: c.run_decode_merge())
     value = nbytes / (ms * 1e-3)
     ach = nbytes / (k_ms * 1e-3)
@@ -107,7 +122,8 @@ def bench_decode(torch, workloads, SlotAttentionCall, args):
         "roofline": {"bound": "hbm", "achieved": ach / 1e9, "peak": HBM_PEAK / 1e9,
                      "unit": "GB/s", "frac": ach / HBM_PEAK, "traffic": None,
                      "kernel": "decode_kernel<bf16> (tf_attn_decode_partial)",
-                     "kernel_ms": k_ms, "merge_kernel_ms": m_ms},
+                     "kernel_ms": k_ms, "kernel_ms_p10_p50_p90": k_spread,
+                     "merge_kernel_ms": m_ms},
         "workloads": wls,
     }
     log(f"decode_b64: {ms*1e3:.1f} us/step, {value/1e9:.0f} GB/s ({value/HBM_PEAK*100:.1f}% "
@@ -125,6 +141,7 @@ def bench_extend(torch, workloads, SlotAttentionCall, args):
     steps = max(3, args.steps // 2)
     ms = time_steps(torch, [call], steps, max(1, args.warmup), lambda c: [c.run])
     k_ms = time_kernel(torch, [call], steps, lambda c: c.run_extend())
+    k_spread = last_spread()
     flops = wl.extend_flops()
     tf = flops / (k_ms * 1e-3)
     log(f"extend_prefix: {ms*1e3:.1f} us/step, {tf/1e12:.1f} TFLOP/s "
@@ -134,6 +151,7 @@ def bench_extend(torch, workloads, SlotAttentionCall, args):
                         "head_dim 256, bf16",
             "value": flops / (ms * 1e-3) / 1e12, "unit": "TFLOP/s", "ms_per_step": ms,
             "steps": steps, "flops_per_step": flops, "kernel_ms": k_ms,
+            "kernel_ms_p10_p50_p90": k_spread,
             "roofline": {"bound": "mfma", "achieved": tf / 1e12, "peak": MFMA_BF16_PEAK / 1e12,
                          "unit": "TFLOP/s", "frac": tf / MFMA_BF16_PEAK,
                          "kernel": "extend_bf16_kernel"}}

@@ -45,13 +45,15 @@ def compile_flags() -> list:
     ]
 
 
-# Per-file flags on top of compile_flags().  extend_bf16.hip: its builtin
-# MFMAs (S^T = K Q^T) must produce VGPR results, because the O^T accumulators
-# of its inline-assembly MFMAs occupy every AGPR.
-# fp8_linear.hip: the GEMM folds each MFMA product into fp32 accumulators
-# with a VALU FMA, which reads VGPRs only.
+# Per-file flags on top of compile_flags(): MFMA accumulators in VGPRs.
+# extend_bf16.hip: two waves per SIMD, O^T, Q^T and S^T all in the 256 VGPRs
+# of a wave.  fp8_linear.hip: the GEMM folds each MFMA product into fp32
+# accumulators with a VALU FMA, which reads VGPRs only.  gdn.hip: the chunked
+# recurrence feeds its accumulators (state, P, Delta) back to VALU work and
+# MFMA operands.
 EXTRA_FLAGS = {"extend_bf16.hip": ["-mllvm", "--amdgpu-mfma-vgpr-form=1"],
-               "fp8_linear.hip": ["-mllvm", "--amdgpu-mfma-vgpr-form=1"]}
+               "fp8_linear.hip": ["-mllvm", "--amdgpu-mfma-vgpr-form=1"],
+               "gdn.hip": ["-mllvm", "--amdgpu-mfma-vgpr-form=1"]}
 
 
 def _filter_stderr(text: str) -> str:

@@ -58,8 +58,8 @@ struct GdnArgs {
   int64_t n_slots;
   int32_t batch, hv, vpk, key_dim, conv_dim;
   int32_t hk;
-  float* wqk;            // extend: fp32 [rows, Hk, 256] normalised q then k, rows permuted
-  float* wg;             // extend: fp32 [rows, Hv, 2] alpha, beta
+  float* wqk;            // extend: fp32 [rows, Hk, 256] normalised q then k
+  float* wg;             // extend: fp32 [rows, Hv, 2] g = log alpha, beta
   uint16_t* wcore;       // extend: bf16 [rows, Hv * Dv] recurrence output
   const int32_t* tok;    // extend: request b owns token rows tok[b] .. tok[b + 1] - 1
   int32_t rows;          // token rows of qkv / a / b / z / out (offsets are clamped to it)
@@ -258,8 +258,8 @@ __global__ void __launch_bounds__(kThreads) gdn_conv_state_kernel(GdnArgs a) {
 
 // Per (token, key head): q / k of the head normalised (F.normalize, eps
 // 1e-12; q also scaled by dk^-0.5) as fp32, and per value head of the group
-// alpha = exp(decay) and beta.  None of it depends on the state, so it runs for
-// all tokens in parallel ahead of the recurrence.
+// the log-decay g = log alpha and beta.  None of it depends on the state,
+// so it runs for all tokens in parallel ahead of the recurrence.
 __global__ void __launch_bounds__(kThreads) gdn_qk_ext_kernel(GdnArgs a) {
   __shared__ float s_sum[2][4];
   const int tok = blockIdx.x, t = threadIdx.x;
@@ -275,17 +275,14 @@ __global__ void __launch_bounds__(kThreads) gdn_qk_ext_kernel(GdnArgs a) {
     __syncthreads();
     const float n = sqrtf(t < kDk ? s_sum[p][0] + s_sum[p][1] : s_sum[p][2] + s_sum[p][3]);
     const float xn = x / fmaxf(n, 1e-12f);
-    // Row j of q (or k) is stored at (j % 8) 16 + j / 8, so the recurrence
-    // lane that owns rows rg, rg + 8, ... reads them as 16 consecutive floats.
     float* qk = a.wqk + ((int64_t)tok * a.hk + hk) * (2 * kDk);
-    qk[(t & kDk) + (j % kRowGroups) * 16 + j / kRowGroups] =
-        t < kDk ? xn * 0.08838834764831845f : xn;     // q (x 128 ** -0.5), then k
+    qk[t] = t < kDk ? xn * 0.08838834764831845f : xn;     // q (x 128 ** -0.5), then k
   }
   for (int h = t; h < a.hv; h += kThreads) {
     const float xa = bf(a.a[tok * a.ab_rs + h]) + a.dt_bias[h];
     const float sp = xa > 20.f ? xa : log1pf(expf(xa));        // F.softplus
     float* gt = a.wg + ((int64_t)tok * a.hv + h) * 2;
-    gt[0] = expf(-expf(a.a_log[h]) * sp);
+    gt[0] = -expf(a.a_log[h]) * sp;                            // g = log alpha
     gt[1] = 1.f / (1.f + expf(-bf(a.b[tok * a.ab_rs + h])));
   }
 }
@@ -306,137 +303,315 @@ __device__ __forceinline__ void dma16(const void* sbase, uint32_t voff, uint32_t
                :: "v"(voff), "s"(sbase), "s"(lds) : "m0");
 }
 
-// The recurrence of one (request, value head) over the request's tokens, the
-// state in registers throughout.  Every per-token quantity is column-local
-// (S^T k, the delta-rule update, S^T q), so each wave owns 32 state columns
-// and runs independently: lane (rg, cq) = (lane / 8, lane % 8) holds rows
-// rg + 8 i (i < 16) of columns 32 w + 4 cq .. + 3, and the two row sums per
-// token are shuffle reductions over the wave's 8 row groups.  Token inputs
-// (normalised q / k, v, gates) reach LDS by DMA 16 tokens at a time, one
-// block ahead, two buffers; a barrier per block, none per token.
-constexpr int kBlkTok = 16;
-struct ExtBuf {
-  float qk[kBlkTok][2 * kDk];          // 16 KB, rows permuted as written by gdn_qk_ext_kernel
-  uint16_t v[kBlkTok][kDv];            // 4 KB
-  float gates[kThreads / kWave][64];   // 1 KB: per wave, token j's alpha, beta at 2 j
+// ---------------------------------------------------------------- chunked recurrence
+// The delta rule over a chunk of C = 32 consecutive tokens of one request and
+// value head, with S0 the state before the chunk, g_t = log alpha_t and
+// gamma_t = g_0 + ... + g_t (t, s index the chunk's tokens):
+//   A[t][s]  = beta_t e^(gamma_t - gamma_s) k_t.k_s   for s < t, else 0
+//   T        = (I + A)^-1                           (unit lower triangular)
+//   X        = diag(beta) (V - diag(e^gamma) K S0)
+//   Delta    = T X
+//   O        = diag(e^gamma) Q S0 + Bm Delta,   Bm[t][s] = e^(gamma_t - gamma_s) q_t.k_s (s <= t)
+//   S        = e^(gamma_C) S0 + (diag(e^(gamma_C - gamma)) K)^T Delta
+// This is the reference's chunk-wise WY form (linear_attention.py:194-242,
+// there with 64-token chunks) and, like it, equals the token recurrence
+// (:278-298) exactly in exact arithmetic.  A chunk's tail past the request's
+// last token is padded with neutral tokens (g = 0, beta = 0), which leave S
+// and every real row unchanged.
+//
+// One 256-thread workgroup per (request, value head) carries S0 in registers
+// through all of the request's chunks: wave w owns state columns 32 w .. + 31
+// and holds them as four 32 x 32 MFMA accumulator tiles (lane (g, n) = (lane
+// / 32, lane % 32): rows 32 ti + 8 (r / 4) + 4 g + r % 4 of column 32 w + n),
+// so the state update is an MFMA into S and the products with S read it as an
+// MFMA operand in place.  Every product runs on v_mfma_f32_32x32x16_bf16 with
+// both fp32 operands split into bf16 high and low parts (hi*hi + hi*lo + lo*hi,
+// about 2^-17 relative error, fp32 accumulation).  Per chunk: gamma by a
+// wave scan; A and Bm from K K^T and Q K^T (one wave each); T by forward
+// substitution (one lane per column); then per wave P = K S0 and R = Q S0 (24
+// MFMAs each), Delta = T X, O and the state update.  Token inputs reach LDS by
+// DMA one chunk ahead; K and Q rows are stored with their 16-byte chunks
+// XOR-swizzled by (t & 15) so that the row-per-lane operand reads are
+// conflict-free.
+constexpr int kChunk = 32;
+constexpr int kTS = 36;   // row stride (floats) of the 32 x 32 chunk matrices
+
+struct ChunkIn {
+  float k[kChunk][kDk];      // 16 KB: normalised k rows, 16-B chunk c of row t at c ^ (t & 15)
+  float q[kChunk][kDk];      // 16 KB: normalised, scaled q rows, same layout
+  uint16_t v[kChunk][kDv];   // 8 KB
+  float gb[kChunk][2];       // g = log alpha, beta
+};
+struct ChunkSmem {
+  ChunkIn in[2];
+  float am[kChunk][kTS];     // A
+  float bm[kChunk][kTS];     // Bm
+  float tm[kChunk][kTS];     // T = (I + A)^-1
+  float gam[kChunk];         // gamma
+  float c[kChunk];           // e^gamma
+  float d[kChunk];           // e^(gamma_C - gamma)
+  float beta[kChunk];        // beta (0 past the last token)
 };
 
-// Sum over lanes l, l ^ 8, l ^ 16, ..., l ^ 56 (the wave's 8 row groups), all
-// in VALU exchanges: DPP row_ror:8 (l ^ 8 within a 16-lane row), then
-// v_permlane16_swap (l ^ 16) and v_permlane32_swap (l ^ 32), each of which
-// returns the lane's own value and its partner's.
-__device__ __forceinline__ float sum8(float x) {
-  x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x128, 0xf, 0xf, false));
-  const auto p16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false,
-                                                    false);
-  x = __uint_as_float(p16[0]) + __uint_as_float(p16[1]);
-  const auto p32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false,
-                                                    false);
-  return __uint_as_float(p32[0]) + __uint_as_float(p32[1]);
+// 16-byte chunk `c` (4 floats) of the swizzled row `t` of a K / Q buffer.
+__device__ __forceinline__ f32x4 row_chunk(const float (*rows)[kDk], int t, int c) {
+  return *reinterpret_cast<const f32x4*>(&rows[t][4 * (c ^ (t & 15))]);
 }
-__device__ __forceinline__ f32x4 sum_row_groups(f32x4 v) {
-  return f32x4{sum8(v[0]), sum8(v[1]), sum8(v[2]), sum8(v[3])};
+__device__ __forceinline__ float row_elem(const float (*rows)[kDk], int t, int i) {
+  return rows[t][4 * ((i >> 2) ^ (t & 15)) + (i & 3)];
 }
 
-__global__ void __launch_bounds__(kThreads) gdn_recur_ext_kernel(GdnArgs a) {
-  __shared__ __attribute__((aligned(16))) ExtBuf sb[2];
+// Eight fp32 values -> bf16 high parts and the bf16 rounding of the
+// remainders, two per dword, element order kept.
+__device__ __forceinline__ void split8(const f32x4& x0, const f32x4& x1, u32x4& hi, u32x4& lo) {
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    hi[i] = pack_bf16(x0[2 * i], x0[2 * i + 1]);
+    lo[i] = pack_bf16(x0[2 * i] - bf16_lo(hi[i]), x0[2 * i + 1] - bf16_hi(hi[i]));
+    hi[2 + i] = pack_bf16(x1[2 * i], x1[2 * i + 1]);
+    lo[2 + i] = pack_bf16(x1[2 * i] - bf16_lo(hi[2 + i]), x1[2 * i + 1] - bf16_hi(hi[2 + i]));
+  }
+}
+__device__ __forceinline__ void split16(const f32x16& x, int r0, u32x4& hi, u32x4& lo) {
+  split8(f32x4{x[r0], x[r0 + 1], x[r0 + 2], x[r0 + 3]},
+         f32x4{x[r0 + 4], x[r0 + 5], x[r0 + 6], x[r0 + 7]}, hi, lo);
+}
+// c + a b with a = ah + al, b = bh + bl (the al bl term is below fp32 rounding).
+__device__ __forceinline__ f32x16 mma3(f32x16 c, const u32x4& ah, const u32x4& al,
+                                       const u32x4& bh, const u32x4& bl) {
+  c = mfma_32x32x16(al, bh, c);
+  c = mfma_32x32x16(ah, bl, c);
+  return mfma_32x32x16(ah, bh, c);
+}
+// Token of accumulator register r of lane half g (rows of a 32 x 32 C tile).
+__device__ __forceinline__ int c_row(int r, int g) { return 8 * (r >> 2) + 4 * g + (r & 3); }
+
+__global__ void __launch_bounds__(kThreads) gdn_chunk_ext_kernel(GdnArgs a) {
+  __shared__ __attribute__((aligned(16))) ChunkSmem sm;
   const int bi = blockIdx.x / a.hv, h = blockIdx.x % a.hv;
   const int hk = h / a.vpk;
   const int lane = threadIdx.x & (kWave - 1), w = wave_id();
+  const int g = lane >> 5, n = lane & 31;
   const int64_t r = a.req[bi];
   if (r < 0 || r >= a.n_slots) return;
   const int t0 = min(max(a.tok[bi], 0), a.rows), t1 = min(max(a.tok[bi + 1], t0), a.rows);
   if (t1 <= t0) return;
   const int last = t1 - 1;
-  const int nblk = (t1 - t0 + kBlkTok - 1) / kBlkTok;
+  const int nchunks = (t1 - t0 + kChunk - 1) / kChunk;
+  const int j = kColBlk * w + n;   // this lane's state column
 
-  const int rg = lane >> 3, cq = lane & 7;
-  const int d0 = kColBlk * w + 4 * cq;         // first of this lane's 4 columns
+  // The 64 KB state goes through LDS (the chunk buffers, not yet in use) so
+  // that the global accesses are coalesced 16-byte ones and each lane reads
+  // its 64 values at immediate offsets from one LDS address.
   float* S = a.ssm + r * a.ssm_ss + (int64_t)h * kDk * kDv;
-  f32x4 s[16];
+  float* stage = &sm.in[0].k[0][0];
+  static_assert(sizeof(sm.in) >= kDk * kDv * 4, "state staging");
 #pragma unroll
-  for (int i = 0; i < 16; ++i)
-    s[i] = *reinterpret_cast<const f32x4*>(S + (rg + kRowGroups * i) * kDv + d0);
+  for (int i = 0; i < kDk * kDv / 4 / kThreads; ++i) {
+    const int q = i * kThreads + threadIdx.x;
+    reinterpret_cast<f32x4*>(stage)[q] = reinterpret_cast<const f32x4*>(S)[q];
+  }
+  __syncthreads();
+  const float* my = stage + 4 * g * kDv + j;
+  f32x16 st[4];
+#pragma unroll
+  for (int ti = 0; ti < 4; ++ti)
+#pragma unroll
+    for (int rr = 0; rr < 16; ++rr) st[ti][rr] = my[(32 * ti + 8 * (rr >> 2) + (rr & 3)) * kDv];
+  __syncthreads();
 
-  // Block bl (tokens t0 + 16 bl ..; past the last token: the last token) into
-  // buffer bf.  Per thread: 4 + 1 + 1 loads.
+  // Chunk ci's inputs into buffer bf; tokens past the last one re-read the
+  // last token (their gates are replaced by neutral ones where they are used).
+  // Wave w moves K and Q rows 8w .. 8w + 7 (4 + 4 instructions, two rows
+  // each) and V rows 8w .. 8w + 7 (2 instructions); wave 0 also the gates.
   const uint8_t* qk_base = reinterpret_cast<const uint8_t*>(a.wqk) + (int64_t)hk * 2 * kDk * 4;
-  const uint8_t* v_base = reinterpret_cast<const uint8_t*>(a.ws) + ((int64_t)2 * a.key_dim + h * kDv) * 2;
+  const uint8_t* v_base =
+      reinterpret_cast<const uint8_t*>(a.ws) + ((int64_t)2 * a.key_dim + h * kDv) * 2;
   const uint8_t* g_base = reinterpret_cast<const uint8_t*>(a.wg) + (int64_t)h * 8;
-  auto issue = [&](int bl, int bf) {
-    const int tb = t0 + kBlkTok * bl;
+  auto issue = [&](int ci, int bf) {
+    const int tb = t0 + kChunk * ci;
+    ChunkIn& I = sm.in[bf];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int j = 4 * i + w;
-      const int tok = min(tb + j, last);
-      dma16(qk_base + (int64_t)tok * a.hk * 2 * kDk * 4, 16 * lane, lds_addr(&sb[bf].qk[j][0]));
+    for (int p = 0; p < 4; ++p) {
+      const int t = 8 * w + 2 * p + g;
+      const uint32_t row = (uint32_t)min(tb + t, last) * (uint32_t)a.hk * (2u * kDk * 4u);
+      const uint32_t cpos = (uint32_t)(n ^ (t & 15)) * 16u;
+      dma16(qk_base, row + kDk * 4u + cpos, lds_addr(&I.k[8 * w + 2 * p][0]));
+      dma16(qk_base, row + cpos, lds_addr(&I.q[8 * w + 2 * p][0]));
     }
-    {
-      const int tok = min(tb + 4 * w + lane / 16, last);
-      dma16(v_base, (uint32_t)tok * (uint32_t)a.conv_dim * 2u + 16u * (lane & 15),
-            lds_addr(&sb[bf].v[4 * w][0]));
+#pragma unroll
+    for (int p = 0; p < 2; ++p) {
+      const int t = 8 * w + 4 * p + (lane >> 4);
+      dma16(v_base, (uint32_t)min(tb + t, last) * (uint32_t)a.conv_dim * 2u + 16u * (lane & 15),
+            lds_addr(&I.v[8 * w + 4 * p][0]));
     }
-    {
-      const int d = lane & 31;
-      const int tok = min(tb + d / 2, last);
-      dma4(g_base, (uint32_t)tok * (uint32_t)a.hv * 8u + 4u * (d & 1),
-           lds_addr(&sb[bf].gates[w][0]));
+    if (w == 0) {
+      dma4(g_base, (uint32_t)min(tb + (lane >> 1), last) * (uint32_t)a.hv * 8u + 4u * (lane & 1),
+           lds_addr(&I.gb[0][0]));
     }
   };
   issue(0, 0);
-  issue(min(1, nblk - 1), 1);
-  asm volatile("s_waitcnt vmcnt(6)" ::: "memory");
-  __syncthreads();
 
-  for (int bl = 0; bl < nblk; ++bl) {
-    const ExtBuf& B = sb[bl & 1];
-    const int tb = t0 + kBlkTok * bl;
-    const int ntok = min(kBlkTok, t1 - tb);
-    for (int j = 0; j < ntok; ++j) {
-      const float* qk = &B.qk[j][rg * 16];
-      const float2 gt = *reinterpret_cast<const float2*>(&B.gates[w][2 * j]);
-      f32x4 vp[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};   // two chains
+  for (int ci = 0; ci < nchunks; ++ci) {
+    const ChunkIn& I = sm.in[ci & 1];
+    const int tb = t0 + kChunk * ci;
+    const int ntok = min(kChunk, t1 - tb);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();   // chunk ci has landed; every wave is done with chunk ci - 1
+    if (ci + 1 < nchunks) issue(ci + 1, (ci + 1) & 1);
+
+    // (1) gamma (inclusive scan of g over the chunk), e^gamma, e^(gamma_C - gamma)
+    if (w == 3) {
+      const float gt = n < ntok ? I.gb[n][0] : 0.f;
+      float x = gt;
 #pragma unroll
-      for (int i4 = 0; i4 < 4; ++i4) {
-        const f32x4 k4 = *reinterpret_cast<const f32x4*>(qk + kDk + 4 * i4);
-#pragma unroll
-        for (int c = 0; c < 4; ++c) {
-          s[4 * i4 + c] *= gt.x;
-          vp[c & 1] += s[4 * i4 + c] * k4[c];
-        }
+      for (int off = 1; off < 32; off <<= 1) {
+        const float y = __shfl_up(x, off, 32);
+        if (n >= off) x += y;
       }
-      const f32x4 v_pred = sum_row_groups(vp[0] + vp[1]);
-      const u32x2 vb = *reinterpret_cast<const u32x2*>(&B.v[j][d0]);
-      const f32x4 vv = {bf16_lo(vb[0]), bf16_hi(vb[0]), bf16_lo(vb[1]), bf16_hi(vb[1])};
-      const f32x4 delta = gt.y * (vv - v_pred);
-      f32x4 op[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
-#pragma unroll
-      for (int i4 = 0; i4 < 4; ++i4) {
-        const f32x4 k4 = *reinterpret_cast<const f32x4*>(qk + kDk + 4 * i4);
-        const f32x4 q4 = *reinterpret_cast<const f32x4*>(qk + 4 * i4);
-#pragma unroll
-        for (int c = 0; c < 4; ++c) {
-          s[4 * i4 + c] += k4[c] * delta;
-          op[c & 1] += s[4 * i4 + c] * q4[c];
-        }
-      }
-      const f32x4 o = sum_row_groups(op[0] + op[1]);
-      if (rg == 0) {
-        u32x2 pk;
-        pk[0] = pack_bf16(o[0], o[1]);   // .to(orig_dtype)
-        pk[1] = pack_bf16(o[2], o[3]);
-        *reinterpret_cast<u32x2*>(a.wcore + (int64_t)(tb + j) * (a.hv * kDv) + h * kDv + d0) = pk;
+      const float gc = __shfl(x, 31, 32);
+      if (g == 0) {
+        sm.gam[n] = x;
+        sm.c[n] = __expf(x);
+        sm.d[n] = __expf(gc - x);
+        sm.beta[n] = n < ntok ? I.gb[n][1] : 0.f;
       }
     }
-    __syncthreads();                              // every wave is done with this buffer
-    issue(min(bl + 2, nblk - 1), bl & 1);          // refill it (a re-read past the end)
-    asm volatile("s_waitcnt vmcnt(6)" ::: "memory");   // block bl + 1 has landed
     __syncthreads();
-  }
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+
+    // (2) A = beta e^(gamma_t - gamma_s) K K^T (wave 0), Bm = e^(..) Q K^T (wave 1)
+    if (w < 2) {
+      const float (*X)[kDk] = w == 0 ? I.k : I.q;
+      f32x16 acc = {};
 #pragma unroll
-  for (int i = 0; i < 16; ++i)
-    *reinterpret_cast<f32x4*>(S + (rg + kRowGroups * i) * kDv + d0) = s[i];
+      for (int ks = 0; ks < 8; ++ks) {   // dims 16 ks .. + 15; lane half g: 16 ks + 8 g .. + 7
+        const int c0 = 4 * ks + 2 * g;
+        u32x4 xh, xl, kh, kl;
+        split8(row_chunk(X, n, c0), row_chunk(X, n, c0 + 1), xh, xl);
+        split8(row_chunk(I.k, n, c0), row_chunk(I.k, n, c0 + 1), kh, kl);
+        acc = mma3(acc, xh, xl, kh, kl);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      const float gs = sm.gam[n];
+      float (*M)[kTS] = w == 0 ? sm.am : sm.bm;
+#pragma unroll
+      for (int rr = 0; rr < 16; ++rr) {
+        const int t = c_row(rr, g);
+        const bool keep = w == 0 ? n < t : n <= t;
+        const float f = (w == 0 ? sm.beta[t] : 1.f) * __expf(fminf(sm.gam[t] - gs, 0.f));
+        M[t][n] = keep ? f * acc[rr] : 0.f;
+      }
+    }
+    __syncthreads();
+
+    // (3) T = (I + A)^-1 by forward substitution, lane n < 32 of wave 2 owns
+    // column n; a scheduling barrier per row keeps the compiler from hoisting
+    // every row's reads of A.
+    if (w == 2 && g == 0) {
+      float tc[kChunk];
+#pragma unroll
+      for (int t = 0; t < kChunk; ++t) {
+        float acc = t == n ? 1.f : 0.f;
+#pragma unroll
+        for (int s4 = 0; s4 < t; s4 += 4) {
+          const f32x4 arow = *reinterpret_cast<const f32x4*>(&sm.am[t][s4]);
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            if (s4 + e < t) acc = fmaf(-arow[e], tc[s4 + e], acc);
+        }
+        tc[t] = acc;
+        __builtin_amdgcn_sched_barrier(0);
+      }
+#pragma unroll
+      for (int t = 0; t < kChunk; ++t) sm.tm[t][n] = tc[t];
+    }
+    __syncthreads();
+
+    // (4) P = K S0 and R = Q S0 over the state rows (this wave's 32 columns)
+    f32x16 P = {}, R = {};
+#pragma unroll
+    for (int ti = 0; ti < 4; ++ti) {
+#pragma unroll
+      for (int hh = 0; hh < 2; ++hh) {
+        // k index 8 g + jj <-> state row 32 ti + 16 hh + 8 (jj / 4) + 4 g + jj % 4
+        u32x4 sh, sl, kh, kl, qh, ql;
+        split16(st[ti], 8 * hh, sh, sl);
+        const int c0 = 8 * ti + 4 * hh + g;
+        split8(row_chunk(I.k, n, c0), row_chunk(I.k, n, c0 + 2), kh, kl);
+        split8(row_chunk(I.q, n, c0), row_chunk(I.q, n, c0 + 2), qh, ql);
+        P = mma3(P, kh, kl, sh, sl);
+        R = mma3(R, qh, ql, sh, sl);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+    // X = beta (v - e^gamma P), then Delta = T X (k index 8 g + jj <-> token
+    // 16 hh + 8 (jj / 4) + 4 g + jj % 4)
+    f32x16 X;
+#pragma unroll
+    for (int rr = 0; rr < 16; ++rr) {
+      const int t = c_row(rr, g);
+      X[rr] = sm.beta[t] * (bf(I.v[t][j]) - sm.c[t] * P[rr]);
+    }
+    f32x16 D = {};
+#pragma unroll
+    for (int hh = 0; hh < 2; ++hh) {
+      u32x4 xh, xl, th, tl;
+      split16(X, 8 * hh, xh, xl);
+      split8(*reinterpret_cast<const f32x4*>(&sm.tm[n][16 * hh + 4 * g]),
+             *reinterpret_cast<const f32x4*>(&sm.tm[n][16 * hh + 8 + 4 * g]), th, tl);
+      D = mma3(D, th, tl, xh, xl);
+    }
+    u32x4 dh[2], dl[2];
+    split16(D, 0, dh[0], dl[0]);
+    split16(D, 8, dh[1], dl[1]);
+    // O = e^gamma R + Bm Delta -> the recurrence output rows of this chunk
+    f32x16 O = {};
+#pragma unroll
+    for (int hh = 0; hh < 2; ++hh) {
+      u32x4 bh, bl;
+      split8(*reinterpret_cast<const f32x4*>(&sm.bm[n][16 * hh + 4 * g]),
+             *reinterpret_cast<const f32x4*>(&sm.bm[n][16 * hh + 8 + 4 * g]), bh, bl);
+      O = mma3(O, bh, bl, dh[hh], dl[hh]);
+    }
+#pragma unroll
+    for (int rr = 0; rr < 16; ++rr) {
+      const int t = c_row(rr, g);
+      if (t < ntok)
+        a.wcore[(int64_t)(tb + t) * (a.hv * kDv) + h * kDv + j] =
+            to_bf(fmaf(sm.c[t], R[rr], O[rr]));   // .to(orig_dtype)
+    }
+    // S = e^(gamma_C) S0 + (diag(e^(gamma_C - gamma)) K)^T Delta
+    const float cC = sm.c[kChunk - 1];
+#pragma unroll
+    for (int ti = 0; ti < 4; ++ti) {
+      st[ti] *= cC;
+#pragma unroll
+      for (int hh = 0; hh < 2; ++hh) {
+        float av[8];
+#pragma unroll
+        for (int jj = 0; jj < 8; ++jj) {
+          const int s = 16 * hh + 8 * (jj >> 2) + 4 * g + (jj & 3);
+          av[jj] = sm.d[s] * row_elem(I.k, s, 32 * ti + n);
+        }
+        u32x4 ah, al;
+        split8(f32x4{av[0], av[1], av[2], av[3]}, f32x4{av[4], av[5], av[6], av[7]}, ah, al);
+        st[ti] = mma3(st[ti], ah, al, dh[hh], dl[hh]);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+  }
+  __syncthreads();   // every wave is done with the chunk buffers
+  float* mine = stage + 4 * g * kDv + j;
+#pragma unroll
+  for (int ti = 0; ti < 4; ++ti)
+#pragma unroll
+    for (int rr = 0; rr < 16; ++rr) mine[(32 * ti + 8 * (rr >> 2) + (rr & 3)) * kDv] = st[ti][rr];
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < kDk * kDv / 4 / kThreads; ++i) {
+    const int q = i * kThreads + threadIdx.x;
+    reinterpret_cast<f32x4*>(S)[q] = reinterpret_cast<const f32x4*>(stage)[q];
+  }
 }
 
 // Gated RMSNorm (rms_norm_gated.py:26-40) of every value head of one token
@@ -650,7 +825,9 @@ int32_t tf_gdn_extend(const void* qkv, int64_t qkv_row_stride, const void* a, co
     return fail(TF_ERR_INVALID, "gdn_extend: workspace of %lld bytes (needs %lld, 16-byte aligned)",
                 (long long)workspace_bytes,
                 (long long)(n_tokens * gdn_ext_row_bytes(num_k_heads, num_v_heads)));
-  if (n_tokens > 65535LL * 65535LL) return fail(TF_ERR_UNSUPPORTED, "gdn_extend: too many tokens");
+  if (n_tokens > 65535LL * 65535LL || n_tokens * num_k_heads * 2 * kDk * 4 > UINT32_MAX ||
+      n_tokens * g.conv_dim * 2 > UINT32_MAX || n_tokens * num_v_heads * 8 > UINT32_MAX)
+    return fail(TF_ERR_UNSUPPORTED, "gdn_extend: too many tokens (32-bit staging offsets)");
   g.tok = token_offsets;
   uint8_t* w = static_cast<uint8_t*>(workspace);
   const int64_t conv_bytes = n_tokens * g.conv_dim * 2;
@@ -668,7 +845,7 @@ int32_t tf_gdn_extend(const void* qkv, int64_t qkv_row_stride, const void* a, co
   }
   hipLaunchKernelGGL(gdn_conv_state_kernel, dim3(cblocks, batch_size), dim3(kThreads), 0, s, g);
   hipLaunchKernelGGL(gdn_qk_ext_kernel, dim3((uint32_t)n_tokens), dim3(kThreads), 0, s, g);
-  hipLaunchKernelGGL(gdn_recur_ext_kernel, dim3((int64_t)batch_size * num_v_heads),
+  hipLaunchKernelGGL(gdn_chunk_ext_kernel, dim3((int64_t)batch_size * num_v_heads),
                      dim3(kThreads), 0, s, g);
   hipLaunchKernelGGL(gdn_norm_ext_kernel, dim3((uint32_t)n_tokens), dim3(kThreads), 0, s, g);
   return launch_status("tf_gdn_extend launch");
