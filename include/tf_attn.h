@@ -371,18 +371,19 @@ int32_t tf_gdn_decode(const void* qkv, int64_t qkv_row_stride, const void* a, co
  * _gated_delta_rule_step, then the gated norm).  Request b owns the token rows
  * token_offsets[b] .. token_offsets[b + 1] - 1 of qkv, a, b, z and out
  * (device int32 [batch_size + 1], non-decreasing, clamped into [0, n_tokens]);
- * max_extend_len: the largest extend length (host int; longer requests are
- * only partly convolved);
- * its conv runs over [conv_state, its tokens] and its state is carried through
- * its tokens in order.  The chunked WY update of the reference (:194-242) and
- * the token-by-token recurrence computed here are the same recurrence (equal
- * up to fp32 rounding).  Five launches: the conv for every (token, channel)
- * in parallel, the conv-state shift, normalised q / k and the gates for every
- * token in parallel, the recurrence (one workgroup per request and value head,
- * its state in registers from first token to last) and the gated norm for
- * every token in parallel.  Other arguments as for tf_gdn_decode, with rows =
- * tokens; workspace: tf_gdn_extend_workspace_bytes(n_tokens, Hk, Hv) bytes,
- * 16-byte aligned.
+ * max_extend_len: the largest extend length (host int, validated only);
+ * each request's conv runs over [conv_state, its tokens] and its state is
+ * carried through its tokens in order.  The state update is the reference's
+ * chunk-wise WY form (:194-242) with 32-token chunks (the same recurrence as
+ * token by token, equal up to fp32 rounding).  Five launches: the conv for
+ * every (token, channel) in parallel, the conv-state shift, normalised q / k
+ * and the gates for every token in parallel, the chunked recurrence (one
+ * workgroup per request and value head, its state in registers from first
+ * chunk to last) and the gated norm for every (token, value head) in
+ * parallel.  qkv must be 8-byte aligned with qkv_row_stride a multiple of 4;
+ * z, out and core_out 4-byte aligned with even row strides.  Other arguments
+ * as for tf_gdn_decode, with rows = tokens; workspace:
+ * tf_gdn_extend_workspace_bytes(n_tokens, Hk, Hv) bytes, 16-byte aligned.
  */
 int64_t tf_gdn_extend_workspace_bytes(int64_t n_tokens, int32_t num_k_heads,
                                       int32_t num_v_heads);

@@ -204,36 +204,75 @@ __global__ void __launch_bounds__(kThreads) gdn_recur_kernel(GdnArgs a) {
 
 constexpr int kConvTokens = 16;   // tokens per thread in the extend conv
 
-// Conv + SiLU of kConvTokens consecutive tokens of one request for one channel
-// per thread (grid: channel blocks x requests x token blocks).  The window
-// before the request's first token comes from the conv state, which this
-// kernel only reads; gdn_conv_state_kernel shifts it afterwards.
-__global__ void __launch_bounds__(kThreads) gdn_conv_ext_kernel(GdnArgs a) {
-  const int c = blockIdx.x * kThreads + threadIdx.x, bi = blockIdx.y;
-  if (c >= a.conv_dim) return;
-  const int64_t r = a.req[bi];
-  if (r < 0 || r >= a.n_slots) return;
-  const int t0 = min(max(a.tok[bi], 0), a.rows), t1 = min(max(a.tok[bi + 1], t0), a.rows);
-  const int tb = t0 + blockIdx.z * kConvTokens;
-  if (tb >= t1) return;
-  const uint16_t* st = a.conv_state + r * a.conv_ss + 3 * (int64_t)c;
-  uint16_t x[kConvTokens + 3];
-#pragma unroll
-  for (int i = 0; i < 3; ++i) {
-    const int tt = tb - 3 + i;
-    x[i] = tt >= t0 ? a.qkv[tt * a.qkv_rs + c] : st[tt - t0 + 3];
+// The request owning token row `tt` (the last b whose clamped offset is <=
+// tt), for a wave-uniform tt: each round splits the candidate range in 64
+// parts, one offset load per lane, and keeps the last part that starts at or
+// before tt (offsets are non-decreasing), so B <= 4096 takes two rounds.
+__device__ __forceinline__ int owner(const GdnArgs& a, int tt) {
+  const int lane = threadIdx.x & (kWave - 1);
+  int lo = 0, n = a.batch;
+  while (n > 1) {
+    const int step = (n + kWave - 1) / kWave;
+    const int idx = lo + lane * step;
+    const bool le = idx < lo + n && min(max(a.tok[idx], 0), a.rows) <= tt;
+    const uint64_t m = __ballot(le);
+    const int k = m ? 63 - __builtin_clzll(m) : 0;
+    const int nlo = lo + k * step;
+    n = min(step, lo + n - nlo);
+    lo = nlo;
   }
+  return lo;
+}
+
+constexpr int kConvCh = 4;   // channels per thread in the extend conv
+
+// Conv + SiLU of kConvTokens consecutive token rows for kConvCh channels per
+// thread (grid: channel blocks x token-row blocks of the flattened batch).
+// Each token's window takes the inputs before its request's first token from
+// the request's conv state, which this kernel only reads;
+// gdn_conv_state_kernel shifts it afterwards.  Rows of requests whose slot is
+// outside the pool are skipped.
+__global__ void __launch_bounds__(kThreads) gdn_conv_ext_kernel(GdnArgs a) {
+  const int c = kConvCh * (blockIdx.x * kThreads + threadIdx.x);
+  const int tb = blockIdx.y * kConvTokens;
+  if (tb >= a.rows) return;
+  int bi = owner(a, tb);   // wave-uniform: before any lane leaves
+  if (c >= a.conv_dim) return;
+  u32x2 x[kConvTokens + 3];   // rows tb - 3 .. tb + 15 (0 outside [0, rows))
 #pragma unroll
-  for (int i = 0; i < kConvTokens; ++i)
-    x[3 + i] = tb + i < t1 ? a.qkv[(tb + i) * a.qkv_rs + c] : (uint16_t)0;
-  const f32x4 w = *reinterpret_cast<const f32x4*>(a.conv_w + 4 * (int64_t)c);
+  for (int i = 0; i < kConvTokens + 3; ++i) {
+    const int tt = tb - 3 + i;
+    x[i] = tt >= 0 && tt < a.rows ? *reinterpret_cast<const u32x2*>(a.qkv + tt * a.qkv_rs + c)
+                                  : u32x2{0u, 0u};
+  }
+  f32x4 w[kConvCh];
+#pragma unroll
+  for (int e = 0; e < kConvCh; ++e)
+    w[e] = *reinterpret_cast<const f32x4*>(a.conv_w + 4 * (int64_t)(c + e));
 #pragma unroll
   for (int i = 0; i < kConvTokens; ++i) {
-    if (tb + i >= t1) break;
-    const float acc = w[0] * bf(x[i]) + w[1] * bf(x[i + 1]) + w[2] * bf(x[i + 2]) +
-                      w[3] * bf(x[i + 3]);
-    const float y = round_bf(acc);
-    a.ws[(int64_t)(tb + i) * a.conv_dim + c] = to_bf(y / (1.f + expf(-y)));
+    const int tt = tb + i;
+    if (tt >= a.rows) break;
+    while (bi + 1 < a.batch && min(max(a.tok[bi + 1], 0), a.rows) <= tt) ++bi;
+    const int t0 = min(max(a.tok[bi], 0), a.rows);
+    const int64_t r = a.req[bi];
+    if (r < 0 || r >= a.n_slots) continue;
+    const uint16_t* st = a.conv_state + r * a.conv_ss + 3 * (int64_t)c;
+    float y[kConvCh];
+#pragma unroll
+    for (int e = 0; e < kConvCh; ++e) {
+      float in[4];
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const int p = tt - 3 + k;   // input position; before t0 it is in the conv state
+        const uint32_t pr = x[i + k][e >> 1];
+        in[k] = p >= t0 ? ((e & 1) ? bf16_hi(pr) : bf16_lo(pr)) : bf(st[3 * e + p - t0 + 3]);
+      }
+      y[e] = round_bf(w[e][0] * in[0] + w[e][1] * in[1] + w[e][2] * in[2] + w[e][3] * in[3]);
+      y[e] = y[e] / (1.f + expf(-y[e]));
+    }
+    *reinterpret_cast<u32x2*>(a.ws + (int64_t)tt * a.conv_dim + c) =
+        u32x2{pack_bf16(y[0], y[1]), pack_bf16(y[2], y[3])};
   }
 }
 
@@ -261,24 +300,31 @@ __global__ void __launch_bounds__(kThreads) gdn_conv_state_kernel(GdnArgs a) {
 // the log-decay g = log alpha and beta.  None of it depends on the state,
 // so it runs for all tokens in parallel ahead of the recurrence.
 __global__ void __launch_bounds__(kThreads) gdn_qk_ext_kernel(GdnArgs a) {
-  __shared__ float s_sum[2][4];
-  const int tok = blockIdx.x, t = threadIdx.x;
-  const uint16_t* y = a.ws + (int64_t)tok * a.conv_dim;
-  const int j = t & (kDk - 1);
-  for (int hk = 0; hk < a.hk; ++hk) {
-    const int p = hk & 1;   // alternating sum buffers: one barrier per head
-    const float x = bf(t < kDk ? y[hk * kDk + t] : y[a.key_dim + hk * kDk + (t - kDk)]);
-    float v2 = x * x;
+  // One wave per (token, key head): lane l normalises dims 2 l, 2 l + 1 of q
+  // and of k, each norm a wave reduction (grid: token rows x blocks of 4 key
+  // heads); the first block of each token also forms the value heads' gates.
+  const int tok = blockIdx.x;
+  const int hk = blockIdx.y * (kThreads / kWave) + wave_id();
+  const int lane = threadIdx.x & (kWave - 1);
+  if (hk < a.hk) {
+    const uint16_t* y = a.ws + (int64_t)tok * a.conv_dim;
+    const uint32_t qv = *reinterpret_cast<const uint32_t*>(y + hk * kDk + 2 * lane);
+    const uint32_t kv = *reinterpret_cast<const uint32_t*>(y + a.key_dim + hk * kDk + 2 * lane);
+    const float q0 = bf16_lo(qv), q1 = bf16_hi(qv), k0 = bf16_lo(kv), k1 = bf16_hi(kv);
+    float sq = q0 * q0 + q1 * q1, sk = k0 * k0 + k1 * k1;
 #pragma unroll
-    for (int d = 32; d >= 1; d >>= 1) v2 += __shfl_xor(v2, d, kWave);
-    if ((t & (kWave - 1)) == 0) s_sum[p][t / kWave] = v2;
-    __syncthreads();
-    const float n = sqrtf(t < kDk ? s_sum[p][0] + s_sum[p][1] : s_sum[p][2] + s_sum[p][3]);
-    const float xn = x / fmaxf(n, 1e-12f);
+    for (int d = 32; d >= 1; d >>= 1) {
+      sq += __shfl_xor(sq, d, kWave);
+      sk += __shfl_xor(sk, d, kWave);
+    }
+    const float nq = fmaxf(sqrtf(sq), 1e-12f), nk = fmaxf(sqrtf(sk), 1e-12f);
     float* qk = a.wqk + ((int64_t)tok * a.hk + hk) * (2 * kDk);
-    qk[t] = t < kDk ? xn * 0.08838834764831845f : xn;     // q (x 128 ** -0.5), then k
+    *reinterpret_cast<float2*>(qk + 2 * lane) =     // q (x 128 ** -0.5), then k
+        float2{q0 / nq * 0.08838834764831845f, q1 / nq * 0.08838834764831845f};
+    *reinterpret_cast<float2*>(qk + kDk + 2 * lane) = float2{k0 / nk, k1 / nk};
   }
-  for (int h = t; h < a.hv; h += kThreads) {
+  if (blockIdx.y != 0) return;
+  for (int h = threadIdx.x; h < a.hv; h += kThreads) {
     const float xa = bf(a.a[tok * a.ab_rs + h]) + a.dt_bias[h];
     const float sp = xa > 20.f ? xa : log1pf(expf(xa));        // F.softplus
     float* gt = a.wg + ((int64_t)tok * a.hv + h) * 2;
@@ -614,40 +660,32 @@ __global__ void __launch_bounds__(kThreads) gdn_chunk_ext_kernel(GdnArgs a) {
   }
 }
 
-// Gated RMSNorm (rms_norm_gated.py:26-40) of every value head of one token
-// from the bf16 recurrence output, two heads per pass (one per 128 threads);
-// also copies the recurrence output to core_out when asked.
+// Gated RMSNorm (rms_norm_gated.py:26-40) of one (token, value head) per wave
+// from the bf16 recurrence output: lane l holds dims 2 l, 2 l + 1 and the sum
+// of squares is a wave reduction (grid: token rows x blocks of 4 value heads).
+// Also copies the recurrence output to core_out when asked.  Rows of requests
+// whose slot is outside the pool are left untouched, as in the recurrence.
 __global__ void __launch_bounds__(kThreads) gdn_norm_ext_kernel(GdnArgs a) {
-  __shared__ float s_sum[2][4];
-  const int tok = blockIdx.x, t = threadIdx.x;
-  // The request owning this row (last b with offset <= tok); rows of requests
-  // whose slot is outside the pool are left untouched, as in the recurrence.
-  int lo = 0, hi = a.batch - 1;
-  while (lo < hi) {
-    const int mid = (lo + hi + 1) >> 1;
-    if (min(max(a.tok[mid], 0), a.rows) <= tok) lo = mid; else hi = mid - 1;
-  }
-  const int64_t r = a.req[lo];
-  if (r < 0 || r >= a.n_slots) return;
-  const int half = t / kDv, d = t % kDv;
-  for (int h0 = 0; h0 < a.hv; h0 += 2) {
-    const int h = h0 + half, p = (h0 >> 1) & 1;
-    const bool act = h < a.hv;
-    const uint16_t ob = act ? a.wcore[(int64_t)tok * (a.hv * kDv) + h * kDv + d] : (uint16_t)0;
-    if (act && a.core) a.core[tok * a.core_rs + h * kDv + d] = ob;
-    const float o = bf(ob);
-    float v2 = o * o;
+  const int tok = blockIdx.x;
+  const int h = blockIdx.y * (kThreads / kWave) + wave_id();
+  const int64_t r = a.req[owner(a, tok)];
+  if (h >= a.hv || r < 0 || r >= a.n_slots) return;
+  const int lane = threadIdx.x & (kWave - 1);
+  const int d = 2 * lane;
+  const uint32_t ob =
+      *reinterpret_cast<const uint32_t*>(a.wcore + (int64_t)tok * (a.hv * kDv) + h * kDv + d);
+  if (a.core) *reinterpret_cast<uint32_t*>(a.core + tok * a.core_rs + h * kDv + d) = ob;
+  const float o0 = bf16_lo(ob), o1 = bf16_hi(ob);
+  float v2 = o0 * o0 + o1 * o1;
 #pragma unroll
-    for (int s2 = 32; s2 >= 1; s2 >>= 1) v2 += __shfl_xor(v2, s2, kWave);
-    if ((t & (kWave - 1)) == 0) s_sum[p][t / kWave] = v2;
-    __syncthreads();
-    const float var = (s_sum[p][2 * half] + s_sum[p][2 * half + 1]) / (float)kDv;
-    if (act) {
-      const float zz = bf(a.z[tok * a.z_rs + h * kDv + d]);
-      a.out[tok * a.out_rs + h * kDv + d] =
-          to_bf(a.norm_w[h * kDv + d] * (o * rsqrtf(var + a.eps)) * (zz / (1.f + expf(-zz))));
-    }
-  }
+  for (int s2 = 32; s2 >= 1; s2 >>= 1) v2 += __shfl_xor(v2, s2, kWave);
+  const float inv = rsqrtf(v2 / (float)kDv + a.eps);
+  const uint32_t zz = *reinterpret_cast<const uint32_t*>(a.z + tok * a.z_rs + h * kDv + d);
+  const float z0 = bf16_lo(zz), z1 = bf16_hi(zz);
+  const float* nw = a.norm_w + h * kDv + d;
+  *reinterpret_cast<uint32_t*>(a.out + tok * a.out_rs + h * kDv + d) =
+      pack_bf16(nw[0] * (o0 * inv) * (z0 / (1.f + expf(-z0))),
+                nw[1] * (o1 * inv) * (z1 / (1.f + expf(-z1))));
 }
 
 }  // namespace
@@ -825,9 +863,16 @@ int32_t tf_gdn_extend(const void* qkv, int64_t qkv_row_stride, const void* a, co
     return fail(TF_ERR_INVALID, "gdn_extend: workspace of %lld bytes (needs %lld, 16-byte aligned)",
                 (long long)workspace_bytes,
                 (long long)(n_tokens * gdn_ext_row_bytes(num_k_heads, num_v_heads)));
-  if (n_tokens > 65535LL * 65535LL || n_tokens * num_k_heads * 2 * kDk * 4 > UINT32_MAX ||
+  if (n_tokens > 65535LL * kConvTokens || n_tokens * num_k_heads * 2 * kDk * 4 > UINT32_MAX ||
       n_tokens * g.conv_dim * 2 > UINT32_MAX || n_tokens * num_v_heads * 8 > UINT32_MAX)
     return fail(TF_ERR_UNSUPPORTED, "gdn_extend: too many tokens (32-bit staging offsets)");
+  if ((reinterpret_cast<uintptr_t>(qkv) & 7u) || qkv_row_stride % 4 ||
+      (reinterpret_cast<uintptr_t>(z) & 3u) || z_row_stride % 2 ||
+      (reinterpret_cast<uintptr_t>(out) & 3u) || out_row_stride % 2 ||
+      (core_out && ((reinterpret_cast<uintptr_t>(core_out) & 3u) || core_row_stride % 2)))
+    return fail(TF_ERR_INVALID,
+                "gdn_extend: qkv must be 8-byte aligned with a row stride that is a multiple "
+                "of 4; z / out / core_out 4-byte aligned with even row strides");
   g.tok = token_offsets;
   uint8_t* w = static_cast<uint8_t*>(workspace);
   const int64_t conv_bytes = n_tokens * g.conv_dim * 2;
@@ -838,16 +883,21 @@ int32_t tf_gdn_extend(const void* qkv, int64_t qkv_row_stride, const void* a, co
   g.wcore = reinterpret_cast<uint16_t*>(reinterpret_cast<uint8_t*>(g.wg) + gate_bytes);
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   const uint32_t cblocks = (g.conv_dim + kThreads - 1) / kThreads;
-  const uint32_t tblocks = (uint32_t)((max_extend_len + kConvTokens - 1) / kConvTokens);
-  if (tblocks > 0) {
-    hipLaunchKernelGGL(gdn_conv_ext_kernel, dim3(cblocks, batch_size, tblocks), dim3(kThreads),
-                       0, s, g);
-  }
+  const uint32_t tblocks = (uint32_t)((n_tokens + kConvTokens - 1) / kConvTokens);
+  hipLaunchKernelGGL(gdn_conv_ext_kernel,
+                     dim3((g.conv_dim / kConvCh + kThreads - 1) / kThreads, tblocks),
+                     dim3(kThreads), 0, s, g);
   hipLaunchKernelGGL(gdn_conv_state_kernel, dim3(cblocks, batch_size), dim3(kThreads), 0, s, g);
-  hipLaunchKernelGGL(gdn_qk_ext_kernel, dim3((uint32_t)n_tokens), dim3(kThreads), 0, s, g);
+  hipLaunchKernelGGL(gdn_qk_ext_kernel,
+                     dim3((uint32_t)n_tokens,
+                          (num_k_heads + kThreads / kWave - 1) / (kThreads / kWave)),
+                     dim3(kThreads), 0, s, g);
   hipLaunchKernelGGL(gdn_chunk_ext_kernel, dim3((int64_t)batch_size * num_v_heads),
                      dim3(kThreads), 0, s, g);
-  hipLaunchKernelGGL(gdn_norm_ext_kernel, dim3((uint32_t)n_tokens), dim3(kThreads), 0, s, g);
+  hipLaunchKernelGGL(gdn_norm_ext_kernel,
+                     dim3((uint32_t)n_tokens,
+                          (num_v_heads + kThreads / kWave - 1) / (kThreads / kWave)),
+                     dim3(kThreads), 0, s, g);
   return launch_status("tf_gdn_extend launch");
 }
 
