@@ -375,18 +375,20 @@ int32_t tf_gdn_decode(const void* qkv, int64_t qkv_row_stride, const void* a, co
  * each request's conv runs over [conv_state, its tokens] and its state is
  * carried through its tokens in order.  The state update is the reference's
  * chunk-wise WY form (:194-242) with 32-token chunks (the same recurrence as
- * token by token, equal up to fp32 rounding).  Five launches: the conv for
- * every (token, channel) in parallel, the conv-state shift, normalised q / k
- * and the gates for every token in parallel, the chunked recurrence (one
- * workgroup per request and value head, its state in registers from first
- * chunk to last) and the gated norm for every (token, value head) in
- * parallel.  qkv must be 8-byte aligned with qkv_row_stride a multiple of 4;
+ * token by token, equal up to fp32 rounding).  Seven launches: the request
+ * of every token row, the conv for every (token, channel) in parallel, the
+ * conv-state shift, normalised q / k and the gates for every token in
+ * parallel, the state-independent part of every chunk in parallel, the
+ * chunked recurrence (one workgroup per request and value head, its state in
+ * registers from first chunk to last) and the gated norm for every (token,
+ * value head) in parallel.  qkv must be 8-byte aligned with qkv_row_stride a multiple of 4;
  * z, out and core_out 4-byte aligned with even row strides.  Other arguments
  * as for tf_gdn_decode, with rows = tokens; workspace:
- * tf_gdn_extend_workspace_bytes(n_tokens, Hk, Hv) bytes, 16-byte aligned.
+ * tf_gdn_extend_workspace_bytes(n_tokens, batch_size, Hk, Hv) bytes, 16-byte
+ * aligned.
  */
-int64_t tf_gdn_extend_workspace_bytes(int64_t n_tokens, int32_t num_k_heads,
-                                      int32_t num_v_heads);
+int64_t tf_gdn_extend_workspace_bytes(int64_t n_tokens, int32_t batch_size,
+                                      int32_t num_k_heads, int32_t num_v_heads);
 
 int32_t tf_gdn_extend(const void* qkv, int64_t qkv_row_stride, const void* a, const void* b,
                       int64_t ab_row_stride, const void* z, int64_t z_row_stride,

@@ -12,7 +12,7 @@ from pathlib import Path
 from typing import Optional
 
 LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libtf_attn.so"
-ABI_VERSION = 9
+ABI_VERSION = 10
 
 TF_DTYPE_BF16 = 0
 TF_DTYPE_FP8_E4M3 = 1
@@ -123,7 +123,7 @@ SIGNATURES = {
         _p, _i64, _p, _i64,            # out, out_row_stride, core_out, core_row_stride
         _p, _i64, _p,                  # workspace, workspace_bytes, stream
     ]),
-    "tf_gdn_extend_workspace_bytes": (_i64, [_i64, _i32, _i32]),
+    "tf_gdn_extend_workspace_bytes": (_i64, [_i64, _i32, _i32, _i32]),
     "tf_gather_kv": (_i32, [
         _p, _i32, _i64, _i64,          # pool, kv_dtype, pool_slots, row_elems
         _p, _i64, _i64, _i64,          # req_to_token, rtt_rows, rtt_row_stride, rtt_cols

@@ -58,8 +58,10 @@ struct GdnArgs {
   int64_t n_slots;
   int32_t batch, hv, vpk, key_dim, conv_dim;
   int32_t hk;
-  float* wqk;            // extend: fp32 [rows, Hk, 256] normalised q then k
+  uint16_t* wqk;         // extend: bf16 [rows, Hk, 4, 128] normalised q (hi, lo parts) then k
   float* wg;             // extend: fp32 [rows, Hv, 2] g = log alpha, beta
+  int32_t* owner;        // extend: int32 [rows] request of each token row (-1: none / skipped)
+  float* wrec;           // extend: fp32 [chunk slots, Hv, 2304] chunk records
   uint16_t* wcore;       // extend: bf16 [rows, Hv * Dv] recurrence output
   const int32_t* tok;    // extend: request b owns token rows tok[b] .. tok[b + 1] - 1
   int32_t rows;          // token rows of qkv / a / b / z / out (offsets are clamped to it)
@@ -204,24 +206,19 @@ __global__ void __launch_bounds__(kThreads) gdn_recur_kernel(GdnArgs a) {
 
 constexpr int kConvTokens = 16;   // tokens per thread in the extend conv
 
-// The request owning token row `tt` (the last b whose clamped offset is <=
-// tt), for a wave-uniform tt: each round splits the candidate range in 64
-// parts, one offset load per lane, and keeps the last part that starts at or
-// before tt (offsets are non-decreasing), so B <= 4096 takes two rounds.
-__device__ __forceinline__ int owner(const GdnArgs& a, int tt) {
-  const int lane = threadIdx.x & (kWave - 1);
-  int lo = 0, n = a.batch;
-  while (n > 1) {
-    const int step = (n + kWave - 1) / kWave;
-    const int idx = lo + lane * step;
-    const bool le = idx < lo + n && min(max(a.tok[idx], 0), a.rows) <= tt;
-    const uint64_t m = __ballot(le);
-    const int k = m ? 63 - __builtin_clzll(m) : 0;
-    const int nlo = lo + k * step;
-    n = min(step, lo + n - nlo);
-    lo = nlo;
+// owner[tt] = the request whose rows hold tt, or -1 when none does or the
+// request's slot is outside the pool (those rows are skipped everywhere).
+__global__ void __launch_bounds__(kThreads) gdn_owner_kernel(GdnArgs a) {
+  const int tt = blockIdx.x * kThreads + threadIdx.x;
+  if (tt >= a.rows) return;
+  int lo = 0, hi = a.batch - 1;
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) >> 1;
+    if (min(max(a.tok[mid], 0), a.rows) <= tt) lo = mid; else hi = mid - 1;
   }
-  return lo;
+  const int t0 = min(max(a.tok[lo], 0), a.rows), t1 = min(max(a.tok[lo + 1], 0), a.rows);
+  const int64_t r = a.req[lo];
+  a.owner[tt] = tt >= t0 && tt < t1 && r >= 0 && r < a.n_slots ? lo : -1;
 }
 
 constexpr int kConvCh = 4;   // channels per thread in the extend conv
@@ -235,9 +232,7 @@ constexpr int kConvCh = 4;   // channels per thread in the extend conv
 __global__ void __launch_bounds__(kThreads) gdn_conv_ext_kernel(GdnArgs a) {
   const int c = kConvCh * (blockIdx.x * kThreads + threadIdx.x);
   const int tb = blockIdx.y * kConvTokens;
-  if (tb >= a.rows) return;
-  int bi = owner(a, tb);   // wave-uniform: before any lane leaves
-  if (c >= a.conv_dim) return;
+  if (tb >= a.rows || c >= a.conv_dim) return;
   u32x2 x[kConvTokens + 3];   // rows tb - 3 .. tb + 15 (0 outside [0, rows))
 #pragma unroll
   for (int i = 0; i < kConvTokens + 3; ++i) {
@@ -253,10 +248,10 @@ __global__ void __launch_bounds__(kThreads) gdn_conv_ext_kernel(GdnArgs a) {
   for (int i = 0; i < kConvTokens; ++i) {
     const int tt = tb + i;
     if (tt >= a.rows) break;
-    while (bi + 1 < a.batch && min(max(a.tok[bi + 1], 0), a.rows) <= tt) ++bi;
+    const int bi = a.owner[tt];
+    if (bi < 0) continue;
     const int t0 = min(max(a.tok[bi], 0), a.rows);
     const int64_t r = a.req[bi];
-    if (r < 0 || r >= a.n_slots) continue;
     const uint16_t* st = a.conv_state + r * a.conv_ss + 3 * (int64_t)c;
     float y[kConvCh];
 #pragma unroll
@@ -318,10 +313,17 @@ __global__ void __launch_bounds__(kThreads) gdn_qk_ext_kernel(GdnArgs a) {
       sk += __shfl_xor(sk, d, kWave);
     }
     const float nq = fmaxf(sqrtf(sq), 1e-12f), nk = fmaxf(sqrtf(sk), 1e-12f);
-    float* qk = a.wqk + ((int64_t)tok * a.hk + hk) * (2 * kDk);
-    *reinterpret_cast<float2*>(qk + 2 * lane) =     // q (x 128 ** -0.5), then k
-        float2{q0 / nq * 0.08838834764831845f, q1 / nq * 0.08838834764831845f};
-    *reinterpret_cast<float2*>(qk + kDk + 2 * lane) = float2{k0 / nk, k1 / nk};
+    // q (x 128 ** -0.5), then k, each as bf16 high parts and the bf16
+    // rounding of the remainders (the two MFMA operand halves)
+    uint16_t* qk = a.wqk + ((int64_t)tok * a.hk + hk) * (4 * kDk);
+    const float qa = q0 / nq * 0.08838834764831845f, qb = q1 / nq * 0.08838834764831845f;
+    const float ka = k0 / nk, kb = k1 / nk;
+    const uint32_t qh = pack_bf16(qa, qb), kh = pack_bf16(ka, kb);
+    uint32_t* q32 = reinterpret_cast<uint32_t*>(qk);
+    q32[lane] = qh;
+    q32[kDk / 2 + lane] = pack_bf16(qa - bf16_lo(qh), qb - bf16_hi(qh));
+    q32[kDk + lane] = kh;
+    q32[3 * kDk / 2 + lane] = pack_bf16(ka - bf16_lo(kh), kb - bf16_hi(kh));
   }
   if (blockIdx.y != 0) return;
   for (int h = threadIdx.x; h < a.hv; h += kThreads) {
@@ -358,54 +360,39 @@ __device__ __forceinline__ void dma16(const void* sbase, uint32_t voff, uint32_t
 //   X        = diag(beta) (V - diag(e^gamma) K S0)
 //   Delta    = T X
 //   O        = diag(e^gamma) Q S0 + Bm Delta,   Bm[t][s] = e^(gamma_t - gamma_s) q_t.k_s (s <= t)
-//   S        = e^(gamma_C) S0 + (diag(e^(gamma_C - gamma)) K)^T Delta
+//   S        = e^(gamma_C) S0 + K^T diag(e^(gamma_C - gamma)) Delta
 // This is the reference's chunk-wise WY form (linear_attention.py:194-242,
 // there with 64-token chunks) and, like it, equals the token recurrence
-// (:278-298) exactly in exact arithmetic.  A chunk's tail past the request's
-// last token is padded with neutral tokens (g = 0, beta = 0), which leave S
-// and every real row unchanged.
+// (:278-298) in exact arithmetic.  A chunk's tail past the request's last
+// token is padded with neutral tokens (g = 0, beta = 0), which leave S and
+// every real row unchanged.
 //
-// One 256-thread workgroup per (request, value head) carries S0 in registers
-// through all of the request's chunks: wave w owns state columns 32 w .. + 31
-// and holds them as four 32 x 32 MFMA accumulator tiles (lane (g, n) = (lane
-// / 32, lane % 32): rows 32 ti + 8 (r / 4) + 4 g + r % 4 of column 32 w + n),
-// so the state update is an MFMA into S and the products with S read it as an
+// Two launches.  gdn_chunk_prep_kernel computes everything that does not
+// depend on S - T, Bm, e^gamma, e^(gamma_C - gamma), beta - for every chunk
+// of every request in parallel into a 9 KB record per (chunk, value head).
+// gdn_chunk_ext_kernel then carries S through a request's chunks, one
+// 256-thread workgroup per (request, value head): wave w owns state columns
+// 32 w .. + 31 as four 32 x 32 MFMA accumulator tiles (lane (g, n) = (lane /
+// 32, lane % 32): rows 32 ti + 8 (r / 4) + 4 g + r % 4 of column 32 w + n), so
+// the state update is an MFMA into S and the products with S read it as an
 // MFMA operand in place.  Every product runs on v_mfma_f32_32x32x16_bf16 with
-// both fp32 operands split into bf16 high and low parts (hi*hi + hi*lo + lo*hi,
-// about 2^-17 relative error, fp32 accumulation).  Per chunk: gamma by a
-// wave scan; A and Bm from K K^T and Q K^T (one wave each); T by forward
-// substitution (one lane per column); then per wave P = K S0 and R = Q S0 (24
-// MFMAs each), Delta = T X, O and the state update.  Token inputs reach LDS by
-// DMA one chunk ahead; K and Q rows are stored with their 16-byte chunks
-// XOR-swizzled by (t & 15) so that the row-per-lane operand reads are
-// conflict-free.
+// both fp32 operands split into bf16 high and low parts (hi*hi + hi*lo +
+// lo*hi, about 2^-17 relative error, fp32 accumulation); q and k arrive
+// already split (gdn_qk_ext_kernel).  Chunk records are numbered
+// floor(t0_b / 32) + b + ci for chunk ci of request b (first token row t0_b),
+// which is unique and below n_tokens / 32 + B.
 constexpr int kChunk = 32;
-constexpr int kTS = 36;   // row stride (floats) of the 32 x 32 chunk matrices
+constexpr int kRec = 2304;     // floats per chunk record: T, Bm, e^gamma, e^(gC - gamma), beta
+constexpr int kRecT = 0, kRecB = 1024, kRecC = 2048, kRecD = 2080, kRecBeta = 2112;
 
-struct ChunkIn {
-  float k[kChunk][kDk];      // 16 KB: normalised k rows, 16-B chunk c of row t at c ^ (t & 15)
-  float q[kChunk][kDk];      // 16 KB: normalised, scaled q rows, same layout
-  uint16_t v[kChunk][kDv];   // 8 KB
-  float gb[kChunk][2];       // g = log alpha, beta
-};
-struct ChunkSmem {
-  ChunkIn in[2];
-  float am[kChunk][kTS];     // A
-  float bm[kChunk][kTS];     // Bm
-  float tm[kChunk][kTS];     // T = (I + A)^-1
-  float gam[kChunk];         // gamma
-  float c[kChunk];           // e^gamma
-  float d[kChunk];           // e^(gamma_C - gamma)
-  float beta[kChunk];        // beta (0 past the last token)
-};
-
-// 16-byte chunk `c` (4 floats) of the swizzled row `t` of a K / Q buffer.
-__device__ __forceinline__ f32x4 row_chunk(const float (*rows)[kDk], int t, int c) {
-  return *reinterpret_cast<const f32x4*>(&rows[t][4 * (c ^ (t & 15))]);
+__device__ __forceinline__ int clamp_row(const GdnArgs& a, int b) {
+  return min(max(a.tok[b], 0), a.rows);
 }
-__device__ __forceinline__ float row_elem(const float (*rows)[kDk], int t, int i) {
-  return rows[t][4 * ((i >> 2) ^ (t & 15)) + (i & 3)];
+__device__ __forceinline__ int chunk_key(const GdnArgs& a, int b) {
+  return clamp_row(a, b) / kChunk + b;
 }
+// Token of accumulator register r of lane half g (rows of a 32 x 32 C tile).
+__device__ __forceinline__ int c_row(int r, int g) { return 8 * (r >> 2) + 4 * g + (r & 3); }
 
 // Eight fp32 values -> bf16 high parts and the bf16 rounding of the
 // remainders, two per dword, element order kept.
@@ -429,61 +416,184 @@ __device__ __forceinline__ f32x16 mma3(f32x16 c, const u32x4& ah, const u32x4& a
   c = mfma_32x32x16(ah, bl, c);
   return mfma_32x32x16(ah, bh, c);
 }
-// Token of accumulator register r of lane half g (rows of a 32 x 32 C tile).
-__device__ __forceinline__ int c_row(int r, int g) { return 8 * (r >> 2) + 4 * g + (r & 3); }
+
+// ---- prep: one workgroup per (chunk record slot, key head)
+struct PrepSmem {
+  u32x4 qk[kChunk][65];            // per token: q hi, q lo, k hi, k lo (16 chunks each) + pad
+  float kk[kChunk][kChunk + 1];    // k_t . k_s
+  float qq[kChunk][kChunk + 1];    // q_t . k_s
+  float am[4][kChunk][kChunk + 1]; // A of the value head each wave solves
+};
+
+__global__ void __launch_bounds__(kThreads) gdn_chunk_prep_kernel(GdnArgs a) {
+  __shared__ __attribute__((aligned(16))) PrepSmem sm;
+  const int slot = blockIdx.x, hk = blockIdx.y;
+  const int lane = threadIdx.x & (kWave - 1), w = wave_id();
+  const int g = lane >> 5, n = lane & 31;
+  int lo = 0, hi = a.batch - 1;   // the request: last b with chunk_key(b) <= slot
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) >> 1;
+    if (chunk_key(a, mid) <= slot) lo = mid; else hi = mid - 1;
+  }
+  const int b = lo;
+  const int t0 = clamp_row(a, b), t1 = max(clamp_row(a, b + 1), t0);
+  const int64_t r = a.req[b];
+  const int ci = slot - chunk_key(a, b);
+  if (r < 0 || r >= a.n_slots || ci < 0 || ci >= (t1 - t0 + kChunk - 1) / kChunk) return;
+  const int tb = t0 + kChunk * ci, ntok = min(kChunk, t1 - tb), last = t1 - 1;
+
+  for (int q = threadIdx.x; q < kChunk * 64; q += kThreads) {
+    const int t = q >> 6, c = q & 63;
+    sm.qk[t][c] = *reinterpret_cast<const u32x4*>(
+        reinterpret_cast<const uint8_t*>(a.wqk) + ((int64_t)min(tb + t, last) * a.hk + hk) * 1024 +
+        16 * c);
+  }
+  __syncthreads();
+  if (w < 2) {   // K K^T (wave 0), Q K^T (wave 1): rows t = lane n, dims 16 ks + 8 g .. + 7
+    f32x16 acc = {};
+#pragma unroll
+    for (int ks = 0; ks < 8; ++ks) {
+      const int ch = 2 * ks + g;
+      const int xo = w == 0 ? 32 : 0;
+      acc = mma3(acc, sm.qk[n][xo + ch], sm.qk[n][xo + 16 + ch], sm.qk[n][32 + ch],
+                 sm.qk[n][48 + ch]);
+    }
+    float (*M)[kChunk + 1] = w == 0 ? sm.kk : sm.qq;
+#pragma unroll
+    for (int rr = 0; rr < 16; ++rr) M[c_row(rr, g)][n] = acc[rr];
+  }
+  __syncthreads();
+
+  for (int v = w; v < a.vpk; v += kThreads / kWave) {
+    const int h = hk * a.vpk + v;
+    float* rec = a.wrec + ((int64_t)slot * a.hv + h) * kRec;
+    const float2 gbv = *reinterpret_cast<const float2*>(a.wg + ((int64_t)min(tb + n, last) * a.hv + h) * 2);
+    const float gn = n < ntok ? gbv.x : 0.f, bn = n < ntok ? gbv.y : 0.f;
+    float x = gn;   // gamma_n: inclusive scan over the chunk
+#pragma unroll
+    for (int off = 1; off < kChunk; off <<= 1) {
+      const float y = __shfl_up(x, off, 32);
+      if (n >= off) x += y;
+    }
+    const float gc = __shfl(x, kChunk - 1, 32);
+    float (*A)[kChunk + 1] = sm.am[w];
+    if (g == 0) {
+      rec[kRecC + n] = __expf(x);
+      rec[kRecD + n] = __expf(gc - x);
+      rec[kRecBeta + n] = bn;
+    }
+    // lane n = column s: A[t][s] into LDS, Bm[t][s] into the record
+#pragma unroll
+    for (int t = 0; t < kChunk; ++t) {
+      const float gt = __shfl(x, t, 32), bt = __shfl(bn, t, 32);
+      const float e = __expf(fminf(gt - x, 0.f));
+      if (g == 0) {
+        A[t][n] = n < t ? bt * e * sm.kk[t][n] : 0.f;
+        rec[kRecB + t * kChunk + n] = n <= t ? e * sm.qq[t][n] : 0.f;
+      }
+    }
+    // this wave's writes of A before its reads (one wave: no barrier needed)
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    if (g == 0) {   // T = (I + A)^-1 by forward substitution, lane n owns column n
+      float tc[kChunk];
+#pragma unroll
+      for (int t = 0; t < kChunk; ++t) {
+        float acc = t == n ? 1.f : 0.f;
+#pragma unroll
+        for (int s = 0; s < t; ++s) acc = fmaf(-A[t][s], tc[s], acc);
+        tc[t] = acc;
+        __builtin_amdgcn_sched_barrier(0);
+      }
+#pragma unroll
+      for (int t = 0; t < kChunk; ++t) rec[kRecT + t * kChunk + n] = tc[t];
+    }
+  }
+}
+
+// ---- the recurrence: one workgroup per (request, value head)
+struct ChunkIn {
+  uint32_t q[kChunk][128];   // 512 B per token: 16-B chunks 0-15 hi, 16-31 lo; chunk c of
+  uint32_t k[kChunk][128];   //   either half stored at c ^ (t & 15) of that half
+  uint16_t v[kChunk][kDv];   // 8 KB
+  float rec[kRec];           // 9 KB: the chunk's record
+};
+
+// Dims d0 .. d0 + 3 and d0 + 8 .. d0 + 11 (d0 a multiple of 4, d0 % 8 < 4) of
+// swizzled row t, high and low parts, as two MFMA operands.
+__device__ __forceinline__ void row8(const uint32_t (*rows)[128], int t, int d0, u32x4& hi,
+                                     u32x4& lo) {
+  const uint32_t* row = rows[t];
+  const int c = d0 >> 3, e = (d0 & 7) >> 1;   // 16-B chunk, dword within it
+  const int p0 = 4 * ((c) ^ (t & 15)) + e, p1 = 4 * ((c + 1) ^ (t & 15)) + e;
+  const u32x2 h0 = *reinterpret_cast<const u32x2*>(row + p0);
+  const u32x2 h1 = *reinterpret_cast<const u32x2*>(row + p1);
+  const u32x2 l0 = *reinterpret_cast<const u32x2*>(row + 64 + p0);
+  const u32x2 l1 = *reinterpret_cast<const u32x2*>(row + 64 + p1);
+  hi = u32x4{h0[0], h0[1], h1[0], h1[1]};
+  lo = u32x4{l0[0], l0[1], l1[0], l1[1]};
+}
+// The bf16 high (part 0) or low (part 1) value of dim i of swizzled row t.
+__device__ __forceinline__ uint32_t row_half(const uint32_t (*rows)[128], int t, int i, int part) {
+  const uint16_t* row = reinterpret_cast<const uint16_t*>(rows[t]);
+  return row[128 * part + 8 * ((i >> 3) ^ (t & 15)) + (i & 7)];
+}
 
 __global__ void __launch_bounds__(kThreads) gdn_chunk_ext_kernel(GdnArgs a) {
-  __shared__ __attribute__((aligned(16))) ChunkSmem sm;
+  __shared__ __attribute__((aligned(16))) ChunkIn sm[2];
   const int bi = blockIdx.x / a.hv, h = blockIdx.x % a.hv;
   const int hk = h / a.vpk;
   const int lane = threadIdx.x & (kWave - 1), w = wave_id();
   const int g = lane >> 5, n = lane & 31;
   const int64_t r = a.req[bi];
   if (r < 0 || r >= a.n_slots) return;
-  const int t0 = min(max(a.tok[bi], 0), a.rows), t1 = min(max(a.tok[bi + 1], t0), a.rows);
+  const int t0 = clamp_row(a, bi), t1 = max(clamp_row(a, bi + 1), t0);
   if (t1 <= t0) return;
   const int last = t1 - 1;
   const int nchunks = (t1 - t0 + kChunk - 1) / kChunk;
-  const int j = kColBlk * w + n;   // this lane's state column
+  const int key0 = chunk_key(a, bi);
+  const int j = 32 * w + n;   // this lane's state column
 
   // The 64 KB state goes through LDS (the chunk buffers, not yet in use) so
   // that the global accesses are coalesced 16-byte ones and each lane reads
   // its 64 values at immediate offsets from one LDS address.
   float* S = a.ssm + r * a.ssm_ss + (int64_t)h * kDk * kDv;
-  float* stage = &sm.in[0].k[0][0];
-  static_assert(sizeof(sm.in) >= kDk * kDv * 4, "state staging");
+  float* stage = reinterpret_cast<float*>(&sm[0]);
+  static_assert(sizeof(sm) >= kDk * kDv * 4, "state staging");
 #pragma unroll
   for (int i = 0; i < kDk * kDv / 4 / kThreads; ++i) {
     const int q = i * kThreads + threadIdx.x;
     reinterpret_cast<f32x4*>(stage)[q] = reinterpret_cast<const f32x4*>(S)[q];
   }
   __syncthreads();
-  const float* my = stage + 4 * g * kDv + j;
   f32x16 st[4];
+  {
+    const float* my = stage + 4 * g * kDv + j;
 #pragma unroll
-  for (int ti = 0; ti < 4; ++ti)
+    for (int ti = 0; ti < 4; ++ti)
 #pragma unroll
-    for (int rr = 0; rr < 16; ++rr) st[ti][rr] = my[(32 * ti + 8 * (rr >> 2) + (rr & 3)) * kDv];
+      for (int rr = 0; rr < 16; ++rr)
+        st[ti][rr] = my[(32 * ti + 8 * (rr >> 2) + (rr & 3)) * kDv];
+  }
   __syncthreads();
 
-  // Chunk ci's inputs into buffer bf; tokens past the last one re-read the
-  // last token (their gates are replaced by neutral ones where they are used).
-  // Wave w moves K and Q rows 8w .. 8w + 7 (4 + 4 instructions, two rows
-  // each) and V rows 8w .. 8w + 7 (2 instructions); wave 0 also the gates.
-  const uint8_t* qk_base = reinterpret_cast<const uint8_t*>(a.wqk) + (int64_t)hk * 2 * kDk * 4;
+  // Chunk ci into buffer bf (tokens past the last one re-read the last token;
+  // the record gives them beta = 0 and g = 0).  Wave w moves q and k rows
+  // 8 w .. 8 w + 7 (4 + 4 instructions, two rows each), V rows 8 w .. + 7 (2)
+  // and 3 KB of the record (waves 0-2).
+  const uint8_t* qk_base = reinterpret_cast<const uint8_t*>(a.wqk) + (int64_t)hk * 1024;
   const uint8_t* v_base =
       reinterpret_cast<const uint8_t*>(a.ws) + ((int64_t)2 * a.key_dim + h * kDv) * 2;
-  const uint8_t* g_base = reinterpret_cast<const uint8_t*>(a.wg) + (int64_t)h * 8;
+  const uint8_t* rec_base = reinterpret_cast<const uint8_t*>(a.wrec) + (int64_t)h * kRec * 4;
   auto issue = [&](int ci, int bf) {
     const int tb = t0 + kChunk * ci;
-    ChunkIn& I = sm.in[bf];
+    ChunkIn& I = sm[bf];
 #pragma unroll
     for (int p = 0; p < 4; ++p) {
       const int t = 8 * w + 2 * p + g;
-      const uint32_t row = (uint32_t)min(tb + t, last) * (uint32_t)a.hk * (2u * kDk * 4u);
-      const uint32_t cpos = (uint32_t)(n ^ (t & 15)) * 16u;
-      dma16(qk_base, row + kDk * 4u + cpos, lds_addr(&I.k[8 * w + 2 * p][0]));
+      const uint32_t row = (uint32_t)min(tb + t, last) * (uint32_t)a.hk * 1024u;
+      const uint32_t cpos = (uint32_t)((n & 16) | ((n & 15) ^ (t & 15))) * 16u;
       dma16(qk_base, row + cpos, lds_addr(&I.q[8 * w + 2 * p][0]));
+      dma16(qk_base, row + 512u + cpos, lds_addr(&I.k[8 * w + 2 * p][0]));
     }
 #pragma unroll
     for (int p = 0; p < 2; ++p) {
@@ -491,132 +601,69 @@ __global__ void __launch_bounds__(kThreads) gdn_chunk_ext_kernel(GdnArgs a) {
       dma16(v_base, (uint32_t)min(tb + t, last) * (uint32_t)a.conv_dim * 2u + 16u * (lane & 15),
             lds_addr(&I.v[8 * w + 4 * p][0]));
     }
-    if (w == 0) {
-      dma4(g_base, (uint32_t)min(tb + (lane >> 1), last) * (uint32_t)a.hv * 8u + 4u * (lane & 1),
-           lds_addr(&I.gb[0][0]));
+    if (w < 3) {
+      const uint32_t rec = (uint32_t)(key0 + ci) * (uint32_t)a.hv * (uint32_t)(kRec * 4);
+#pragma unroll
+      for (int p = 0; p < 3; ++p)
+        dma16(rec_base, rec + 1024u * (3 * w + p) + 16u * lane,
+              lds_addr(&I.rec[256 * (3 * w + p)]));
     }
   };
   issue(0, 0);
 
   for (int ci = 0; ci < nchunks; ++ci) {
-    const ChunkIn& I = sm.in[ci & 1];
+    const ChunkIn& I = sm[ci & 1];
     const int tb = t0 + kChunk * ci;
     const int ntok = min(kChunk, t1 - tb);
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();   // chunk ci has landed; every wave is done with chunk ci - 1
     if (ci + 1 < nchunks) issue(ci + 1, (ci + 1) & 1);
 
-    // (1) gamma (inclusive scan of g over the chunk), e^gamma, e^(gamma_C - gamma)
-    if (w == 3) {
-      const float gt = n < ntok ? I.gb[n][0] : 0.f;
-      float x = gt;
-#pragma unroll
-      for (int off = 1; off < 32; off <<= 1) {
-        const float y = __shfl_up(x, off, 32);
-        if (n >= off) x += y;
-      }
-      const float gc = __shfl(x, 31, 32);
-      if (g == 0) {
-        sm.gam[n] = x;
-        sm.c[n] = __expf(x);
-        sm.d[n] = __expf(gc - x);
-        sm.beta[n] = n < ntok ? I.gb[n][1] : 0.f;
-      }
-    }
-    __syncthreads();
-
-    // (2) A = beta e^(gamma_t - gamma_s) K K^T (wave 0), Bm = e^(..) Q K^T (wave 1)
-    if (w < 2) {
-      const float (*X)[kDk] = w == 0 ? I.k : I.q;
-      f32x16 acc = {};
-#pragma unroll
-      for (int ks = 0; ks < 8; ++ks) {   // dims 16 ks .. + 15; lane half g: 16 ks + 8 g .. + 7
-        const int c0 = 4 * ks + 2 * g;
-        u32x4 xh, xl, kh, kl;
-        split8(row_chunk(X, n, c0), row_chunk(X, n, c0 + 1), xh, xl);
-        split8(row_chunk(I.k, n, c0), row_chunk(I.k, n, c0 + 1), kh, kl);
-        acc = mma3(acc, xh, xl, kh, kl);
-        __builtin_amdgcn_sched_barrier(0);
-      }
-      const float gs = sm.gam[n];
-      float (*M)[kTS] = w == 0 ? sm.am : sm.bm;
-#pragma unroll
-      for (int rr = 0; rr < 16; ++rr) {
-        const int t = c_row(rr, g);
-        const bool keep = w == 0 ? n < t : n <= t;
-        const float f = (w == 0 ? sm.beta[t] : 1.f) * __expf(fminf(sm.gam[t] - gs, 0.f));
-        M[t][n] = keep ? f * acc[rr] : 0.f;
-      }
-    }
-    __syncthreads();
-
-    // (3) T = (I + A)^-1 by forward substitution, lane n < 32 of wave 2 owns
-    // column n; a scheduling barrier per row keeps the compiler from hoisting
-    // every row's reads of A.
-    if (w == 2 && g == 0) {
-      float tc[kChunk];
-#pragma unroll
-      for (int t = 0; t < kChunk; ++t) {
-        float acc = t == n ? 1.f : 0.f;
-#pragma unroll
-        for (int s4 = 0; s4 < t; s4 += 4) {
-          const f32x4 arow = *reinterpret_cast<const f32x4*>(&sm.am[t][s4]);
-#pragma unroll
-          for (int e = 0; e < 4; ++e)
-            if (s4 + e < t) acc = fmaf(-arow[e], tc[s4 + e], acc);
-        }
-        tc[t] = acc;
-        __builtin_amdgcn_sched_barrier(0);
-      }
-#pragma unroll
-      for (int t = 0; t < kChunk; ++t) sm.tm[t][n] = tc[t];
-    }
-    __syncthreads();
-
-    // (4) P = K S0 and R = Q S0 over the state rows (this wave's 32 columns)
+    // P = K S0 and R = Q S0 over the state rows (k index 8 g + jj <-> state
+    // row 32 ti + 16 hh + 8 (jj / 4) + 4 g + jj % 4)
     f32x16 P = {}, R = {};
 #pragma unroll
     for (int ti = 0; ti < 4; ++ti) {
 #pragma unroll
       for (int hh = 0; hh < 2; ++hh) {
-        // k index 8 g + jj <-> state row 32 ti + 16 hh + 8 (jj / 4) + 4 g + jj % 4
         u32x4 sh, sl, kh, kl, qh, ql;
         split16(st[ti], 8 * hh, sh, sl);
-        const int c0 = 8 * ti + 4 * hh + g;
-        split8(row_chunk(I.k, n, c0), row_chunk(I.k, n, c0 + 2), kh, kl);
-        split8(row_chunk(I.q, n, c0), row_chunk(I.q, n, c0 + 2), qh, ql);
+        const int d0 = 32 * ti + 16 * hh + 4 * g;
+        row8(I.k, n, d0, kh, kl);
+        row8(I.q, n, d0, qh, ql);
         P = mma3(P, kh, kl, sh, sl);
         R = mma3(R, qh, ql, sh, sl);
-        __builtin_amdgcn_sched_barrier(0);
       }
     }
-    // X = beta (v - e^gamma P), then Delta = T X (k index 8 g + jj <-> token
+    // X = beta (v - e^gamma P); Delta = T X (k index 8 g + jj <-> token
     // 16 hh + 8 (jj / 4) + 4 g + jj % 4)
     f32x16 X;
 #pragma unroll
     for (int rr = 0; rr < 16; ++rr) {
       const int t = c_row(rr, g);
-      X[rr] = sm.beta[t] * (bf(I.v[t][j]) - sm.c[t] * P[rr]);
+      X[rr] = I.rec[kRecBeta + t] * (bf(I.v[t][j]) - I.rec[kRecC + t] * P[rr]);
     }
     f32x16 D = {};
 #pragma unroll
     for (int hh = 0; hh < 2; ++hh) {
       u32x4 xh, xl, th, tl;
       split16(X, 8 * hh, xh, xl);
-      split8(*reinterpret_cast<const f32x4*>(&sm.tm[n][16 * hh + 4 * g]),
-             *reinterpret_cast<const f32x4*>(&sm.tm[n][16 * hh + 8 + 4 * g]), th, tl);
+      const float* trow = &I.rec[kRecT + n * kChunk + 16 * hh + 4 * g];
+      split8(*reinterpret_cast<const f32x4*>(trow), *reinterpret_cast<const f32x4*>(trow + 8), th,
+             tl);
       D = mma3(D, th, tl, xh, xl);
     }
+    // O = e^gamma R + Bm Delta -> the recurrence output rows of this chunk
     u32x4 dh[2], dl[2];
     split16(D, 0, dh[0], dl[0]);
     split16(D, 8, dh[1], dl[1]);
-    // O = e^gamma R + Bm Delta -> the recurrence output rows of this chunk
     f32x16 O = {};
 #pragma unroll
     for (int hh = 0; hh < 2; ++hh) {
       u32x4 bh, bl;
-      split8(*reinterpret_cast<const f32x4*>(&sm.bm[n][16 * hh + 4 * g]),
-             *reinterpret_cast<const f32x4*>(&sm.bm[n][16 * hh + 8 + 4 * g]), bh, bl);
+      const float* brow = &I.rec[kRecB + n * kChunk + 16 * hh + 4 * g];
+      split8(*reinterpret_cast<const f32x4*>(brow), *reinterpret_cast<const f32x4*>(brow + 8), bh,
+             bl);
       O = mma3(O, bh, bl, dh[hh], dl[hh]);
     }
 #pragma unroll
@@ -624,34 +671,41 @@ __global__ void __launch_bounds__(kThreads) gdn_chunk_ext_kernel(GdnArgs a) {
       const int t = c_row(rr, g);
       if (t < ntok)
         a.wcore[(int64_t)(tb + t) * (a.hv * kDv) + h * kDv + j] =
-            to_bf(fmaf(sm.c[t], R[rr], O[rr]));   // .to(orig_dtype)
+            to_bf(fmaf(I.rec[kRecC + t], R[rr], O[rr]));   // .to(orig_dtype)
     }
-    // S = e^(gamma_C) S0 + (diag(e^(gamma_C - gamma)) K)^T Delta
-    const float cC = sm.c[kChunk - 1];
+    // S = e^(gamma_C) S0 + K^T (diag(e^(gamma_C - gamma)) Delta)
+#pragma unroll
+    for (int rr = 0; rr < 16; ++rr) D[rr] *= I.rec[kRecD + c_row(rr, g)];
+    split16(D, 0, dh[0], dl[0]);
+    split16(D, 8, dh[1], dl[1]);
+    const float cC = I.rec[kRecC + kChunk - 1];
 #pragma unroll
     for (int ti = 0; ti < 4; ++ti) {
       st[ti] *= cC;
 #pragma unroll
       for (int hh = 0; hh < 2; ++hh) {
-        float av[8];
-#pragma unroll
-        for (int jj = 0; jj < 8; ++jj) {
-          const int s = 16 * hh + 8 * (jj >> 2) + 4 * g + (jj & 3);
-          av[jj] = sm.d[s] * row_elem(I.k, s, 32 * ti + n);
-        }
+        // A operand: K^T rows i = 32 ti + n, tokens s(jj) as for Delta
         u32x4 ah, al;
-        split8(f32x4{av[0], av[1], av[2], av[3]}, f32x4{av[4], av[5], av[6], av[7]}, ah, al);
+#pragma unroll
+        for (int m = 0; m < 4; ++m) {
+          const int s0 = 16 * hh + 8 * (m >> 1) + 4 * g + 2 * (m & 1);
+          const int i = 32 * ti + n;
+          ah[m] = row_half(I.k, s0, i, 0) | (row_half(I.k, s0 + 1, i, 0) << 16);
+          al[m] = row_half(I.k, s0, i, 1) | (row_half(I.k, s0 + 1, i, 1) << 16);
+        }
         st[ti] = mma3(st[ti], ah, al, dh[hh], dl[hh]);
-        __builtin_amdgcn_sched_barrier(0);
       }
     }
   }
   __syncthreads();   // every wave is done with the chunk buffers
-  float* mine = stage + 4 * g * kDv + j;
+  {
+    float* mine = stage + 4 * g * kDv + j;
 #pragma unroll
-  for (int ti = 0; ti < 4; ++ti)
+    for (int ti = 0; ti < 4; ++ti)
 #pragma unroll
-    for (int rr = 0; rr < 16; ++rr) mine[(32 * ti + 8 * (rr >> 2) + (rr & 3)) * kDv] = st[ti][rr];
+      for (int rr = 0; rr < 16; ++rr)
+        mine[(32 * ti + 8 * (rr >> 2) + (rr & 3)) * kDv] = st[ti][rr];
+  }
   __syncthreads();
 #pragma unroll
   for (int i = 0; i < kDk * kDv / 4 / kThreads; ++i) {
@@ -668,8 +722,7 @@ __global__ void __launch_bounds__(kThreads) gdn_chunk_ext_kernel(GdnArgs a) {
 __global__ void __launch_bounds__(kThreads) gdn_norm_ext_kernel(GdnArgs a) {
   const int tok = blockIdx.x;
   const int h = blockIdx.y * (kThreads / kWave) + wave_id();
-  const int64_t r = a.req[owner(a, tok)];
-  if (h >= a.hv || r < 0 || r >= a.n_slots) return;
+  if (h >= a.hv || a.owner[tok] < 0) return;
   const int lane = threadIdx.x & (kWave - 1);
   const int d = 2 * lane;
   const uint32_t ob =
@@ -704,10 +757,18 @@ int64_t tf_gdn_decode_workspace_bytes(int32_t batch_size, int32_t num_k_heads,
 
 namespace tfa {
 // Extend workspace bytes per token row: conv outputs (bf16), normalised q / k
-// (fp32), gates (fp32) and the recurrence output (bf16).
+// (bf16 high and low parts), gates (fp32), the recurrence output (bf16) and
+// the row's request (int32).
 int64_t gdn_ext_row_bytes(int32_t hk, int32_t hv) {
   const int64_t conv_dim = 2LL * hk * kDk + (int64_t)hv * kDv;
-  return conv_dim * 2 + (int64_t)hk * 2 * kDk * 4 + (int64_t)hv * 2 * 4 + (int64_t)hv * kDv * 2;
+  return conv_dim * 2 + (int64_t)hk * 4 * kDk * 2 + (int64_t)hv * 2 * 4 + (int64_t)hv * kDv * 2 + 4;
+}
+// Chunk-record slots: chunk ci of request b is slot floor(t0_b / 32) + b + ci.
+int64_t gdn_chunk_slots(int64_t n_tokens, int32_t batch) { return n_tokens / kChunk + batch + 1; }
+// Per-token rows (16-byte aligned), then the chunk records.
+int64_t gdn_ext_ws_bytes(int64_t n_tokens, int32_t batch, int32_t hk, int32_t hv) {
+  return ((n_tokens * gdn_ext_row_bytes(hk, hv) + 64) & ~15LL) +
+         gdn_chunk_slots(n_tokens, batch) * hv * kRec * 4;
 }
 }  // namespace tfa
 
@@ -780,6 +841,8 @@ int32_t gdn_setup(const char* fn, const void* qkv, int64_t qkv_row_stride, const
   g->hk = num_k_heads;
   g->wqk = nullptr;
   g->wg = nullptr;
+  g->owner = nullptr;
+  g->wrec = nullptr;
   g->wcore = nullptr;
   g->ws = static_cast<uint16_t*>(workspace);
   g->out = static_cast<uint16_t*>(out);
@@ -821,12 +884,12 @@ int32_t tf_gdn_decode(const void* qkv, int64_t qkv_row_stride, const void* a, co
   return launch_status("tf_gdn_decode launch");
 }
 
-int64_t tf_gdn_extend_workspace_bytes(int64_t n_tokens, int32_t num_k_heads,
-                                      int32_t num_v_heads) {
+int64_t tf_gdn_extend_workspace_bytes(int64_t n_tokens, int32_t batch_size,
+                                      int32_t num_k_heads, int32_t num_v_heads) {
   tfa::clear_error();
-  if (n_tokens < 0 || num_k_heads <= 0 || num_v_heads <= 0)
+  if (n_tokens < 0 || batch_size < 0 || num_k_heads <= 0 || num_v_heads <= 0)
     return tfa::fail(TF_ERR_INVALID, "gdn_extend_workspace_bytes: bad arguments");
-  return n_tokens * tfa::gdn_ext_row_bytes(num_k_heads, num_v_heads);
+  return tfa::gdn_ext_ws_bytes(n_tokens, batch_size, num_k_heads, num_v_heads);
 }
 
 int32_t tf_gdn_extend(const void* qkv, int64_t qkv_row_stride, const void* a, const void* b,
@@ -858,13 +921,14 @@ int32_t tf_gdn_extend(const void* qkv, int64_t qkv_row_stride, const void* a, co
       head_k_dim, head_v_dim, conv_kernel, out, out_row_stride, core_out, core_row_stride,
       workspace, workspace_bytes, &g);
   if (rc != TF_OK) return rc;
-  if (workspace_bytes < n_tokens * gdn_ext_row_bytes(num_k_heads, num_v_heads) ||
-      (reinterpret_cast<uintptr_t>(workspace) & 15u))
+  const int64_t need = gdn_ext_ws_bytes(n_tokens, batch_size, num_k_heads, num_v_heads);
+  if (workspace_bytes < need || (reinterpret_cast<uintptr_t>(workspace) & 15u))
     return fail(TF_ERR_INVALID, "gdn_extend: workspace of %lld bytes (needs %lld, 16-byte aligned)",
-                (long long)workspace_bytes,
-                (long long)(n_tokens * gdn_ext_row_bytes(num_k_heads, num_v_heads)));
-  if (n_tokens > 65535LL * kConvTokens || n_tokens * num_k_heads * 2 * kDk * 4 > UINT32_MAX ||
-      n_tokens * g.conv_dim * 2 > UINT32_MAX || n_tokens * num_v_heads * 8 > UINT32_MAX)
+                (long long)workspace_bytes, (long long)need);
+  const int64_t n_slots_rec = gdn_chunk_slots(n_tokens, batch_size);
+  if (n_tokens > 65535LL * kConvTokens || n_tokens * num_k_heads * 4 * kDk * 2 > UINT32_MAX ||
+      n_tokens * g.conv_dim * 2 > UINT32_MAX || n_tokens * num_v_heads * 8 > UINT32_MAX ||
+      n_slots_rec * num_v_heads * kRec * 4 > UINT32_MAX)
     return fail(TF_ERR_UNSUPPORTED, "gdn_extend: too many tokens (32-bit staging offsets)");
   if ((reinterpret_cast<uintptr_t>(qkv) & 7u) || qkv_row_stride % 4 ||
       (reinterpret_cast<uintptr_t>(z) & 3u) || z_row_stride % 2 ||
@@ -876,14 +940,20 @@ int32_t tf_gdn_extend(const void* qkv, int64_t qkv_row_stride, const void* a, co
   g.tok = token_offsets;
   uint8_t* w = static_cast<uint8_t*>(workspace);
   const int64_t conv_bytes = n_tokens * g.conv_dim * 2;
-  const int64_t qk_bytes = n_tokens * num_k_heads * 2 * kDk * 4;
+  const int64_t qk_bytes = n_tokens * num_k_heads * 4 * kDk * 2;
   const int64_t gate_bytes = n_tokens * num_v_heads * 2 * 4;
-  g.wqk = reinterpret_cast<float*>(w + ((conv_bytes + 15) & ~15LL));
+  const int64_t core_bytes = n_tokens * num_v_heads * kDv * 2;
+  g.wqk = reinterpret_cast<uint16_t*>(w + ((conv_bytes + 15) & ~15LL));
   g.wg = reinterpret_cast<float*>(reinterpret_cast<uint8_t*>(g.wqk) + qk_bytes);
   g.wcore = reinterpret_cast<uint16_t*>(reinterpret_cast<uint8_t*>(g.wg) + gate_bytes);
+  g.owner = reinterpret_cast<int32_t*>(reinterpret_cast<uint8_t*>(g.wcore) + core_bytes);
+  g.wrec = reinterpret_cast<float*>(w + ((n_tokens * gdn_ext_row_bytes(num_k_heads, num_v_heads) +
+                                          64) & ~15LL));
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   const uint32_t cblocks = (g.conv_dim + kThreads - 1) / kThreads;
   const uint32_t tblocks = (uint32_t)((n_tokens + kConvTokens - 1) / kConvTokens);
+  hipLaunchKernelGGL(gdn_owner_kernel, dim3((uint32_t)((n_tokens + kThreads - 1) / kThreads)),
+                     dim3(kThreads), 0, s, g);
   hipLaunchKernelGGL(gdn_conv_ext_kernel,
                      dim3((g.conv_dim / kConvCh + kThreads - 1) / kThreads, tblocks),
                      dim3(kThreads), 0, s, g);
@@ -891,6 +961,8 @@ int32_t tf_gdn_extend(const void* qkv, int64_t qkv_row_stride, const void* a, co
   hipLaunchKernelGGL(gdn_qk_ext_kernel,
                      dim3((uint32_t)n_tokens,
                           (num_k_heads + kThreads / kWave - 1) / (kThreads / kWave)),
+                     dim3(kThreads), 0, s, g);
+  hipLaunchKernelGGL(gdn_chunk_prep_kernel, dim3((uint32_t)n_slots_rec, num_k_heads),
                      dim3(kThreads), 0, s, g);
   hipLaunchKernelGGL(gdn_chunk_ext_kernel, dim3((int64_t)batch_size * num_v_heads),
                      dim3(kThreads), 0, s, g);

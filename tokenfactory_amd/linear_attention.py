@@ -121,7 +121,8 @@ def gdn_extend_step(qkv: torch.Tensor, b: torch.Tensor, a: torch.Tensor, z: torc
     value_dim = num_v_heads * HEAD_DIM
     out = torch.empty((n_tok, value_dim), dtype=torch.bfloat16, device=qkv.device)
     core = torch.empty_like(out) if return_core else None
-    ws_bytes = _native.load().tf_gdn_extend_workspace_bytes(n_tok, num_k_heads, num_v_heads)
+    ws_bytes = _native.load().tf_gdn_extend_workspace_bytes(n_tok, len(lens), num_k_heads,
+                                                           num_v_heads)
     if ws_bytes < 0:
         raise ValueError("gdn_extend_step: bad head counts")
     ws = torch.empty((max(ws_bytes, 1),), dtype=torch.uint8, device=qkv.device)
