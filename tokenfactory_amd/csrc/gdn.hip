@@ -117,7 +117,15 @@ __global__ void __launch_bounds__(kThreads) gdn_recur_kernel(GdnArgs a) {
   const int t = threadIdx.x;
   const int64_t r = a.req[bi];
   if (r < 0 || r >= a.n_slots) return;   // a slot outside the pool: no work, no output
-  const uint16_t* y = a.ws + (int64_t)bi * a.conv_dim;
+  // Decode: request bi is row bi.  Extend (token offsets given): this kernel
+  // takes the requests that extend by exactly one token, at their row.
+  int row = bi;
+  if (a.tok) {
+    const int t0 = min(max(a.tok[bi], 0), a.rows);
+    if (min(max(a.tok[bi + 1], 0), a.rows) != t0 + 1) return;
+    row = t0;
+  }
+  const uint16_t* y = a.ws + (int64_t)row * a.conv_dim;
 
   // The state loads go out first; q / k normalisation runs under their latency.
   const int d0 = 4 * (t & 31), g = t >> 5;
@@ -144,10 +152,10 @@ __global__ void __launch_bounds__(kThreads) gdn_recur_kernel(GdnArgs a) {
     __syncthreads();
   }
 
-  const float x = bf(a.a[bi * a.ab_rs + h]) + a.dt_bias[h];
+  const float x = bf(a.a[row * a.ab_rs + h]) + a.dt_bias[h];
   const float sp = x > 20.f ? x : log1pf(expf(x));           // F.softplus
   const float alpha = expf(-expf(a.a_log[h]) * sp);
-  const float beta = 1.f / (1.f + expf(-bf(a.b[bi * a.ab_rs + h])));
+  const float beta = 1.f / (1.f + expf(-bf(a.b[row * a.ab_rs + h])));
 
   f32x4 vp = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -183,14 +191,14 @@ __global__ void __launch_bounds__(kThreads) gdn_recur_kernel(GdnArgs a) {
 #pragma unroll
     for (int q = 0; q < kRowGroups; ++q) o += s_red[q][t];
     o = round_bf(o);                               // .to(orig_dtype)
-    if (a.core) a.core[bi * a.core_rs + h * kDv + t] = to_bf(o);
+    if (a.core) a.core[row * a.core_rs + h * kDv + t] = to_bf(o);
   }
   const float var = sum128(t < kDv ? o * o : 0.f, s_sum) / (float)kDv;
   if (t < kDv) {
     const float xn = o * rsqrtf(var + a.eps);
-    const float zz = bf(a.z[bi * a.z_rs + h * kDv + t]);
+    const float zz = bf(a.z[row * a.z_rs + h * kDv + t]);
     const float out = a.norm_w[h * kDv + t] * xn * (zz / (1.f + expf(-zz)));
-    a.out[bi * a.out_rs + h * kDv + t] = to_bf(out);
+    a.out[row * a.out_rs + h * kDv + t] = to_bf(out);
   }
 }
 
@@ -439,7 +447,8 @@ __global__ void __launch_bounds__(kThreads) gdn_chunk_prep_kernel(GdnArgs a) {
   const int t0 = clamp_row(a, b), t1 = max(clamp_row(a, b + 1), t0);
   const int64_t r = a.req[b];
   const int ci = slot - chunk_key(a, b);
-  if (r < 0 || r >= a.n_slots || ci < 0 || ci >= (t1 - t0 + kChunk - 1) / kChunk) return;
+  if (r < 0 || r >= a.n_slots || t1 - t0 < 2 || ci < 0 || ci >= (t1 - t0 + kChunk - 1) / kChunk)
+    return;
   const int tb = t0 + kChunk * ci, ntok = min(kChunk, t1 - tb), last = t1 - 1;
 
   for (int q = threadIdx.x; q < kChunk * 64; q += kThreads) {
@@ -547,7 +556,7 @@ __global__ void __launch_bounds__(kThreads) gdn_chunk_ext_kernel(GdnArgs a) {
   const int64_t r = a.req[bi];
   if (r < 0 || r >= a.n_slots) return;
   const int t0 = clamp_row(a, bi), t1 = max(clamp_row(a, bi + 1), t0);
-  if (t1 <= t0) return;
+  if (t1 - t0 < 2) return;   // one-token requests: gdn_recur_kernel
   const int last = t1 - 1;
   const int nchunks = (t1 - t0 + kChunk - 1) / kChunk;
   const int key0 = chunk_key(a, bi);
@@ -722,7 +731,10 @@ __global__ void __launch_bounds__(kThreads) gdn_chunk_ext_kernel(GdnArgs a) {
 __global__ void __launch_bounds__(kThreads) gdn_norm_ext_kernel(GdnArgs a) {
   const int tok = blockIdx.x;
   const int h = blockIdx.y * (kThreads / kWave) + wave_id();
-  if (h >= a.hv || a.owner[tok] < 0) return;
+  const int bo = a.owner[tok];
+  if (h >= a.hv || bo < 0) return;
+  if (min(max(a.tok[bo + 1], 0), a.rows) - min(max(a.tok[bo], 0), a.rows) == 1)
+    return;   // a one-token request: gdn_recur_kernel wrote its row
   const int lane = threadIdx.x & (kWave - 1);
   const int d = 2 * lane;
   const uint32_t ob =
@@ -964,6 +976,8 @@ int32_t tf_gdn_extend(const void* qkv, int64_t qkv_row_stride, const void* a, co
                      dim3(kThreads), 0, s, g);
   hipLaunchKernelGGL(gdn_chunk_prep_kernel, dim3((uint32_t)n_slots_rec, num_k_heads),
                      dim3(kThreads), 0, s, g);
+  hipLaunchKernelGGL(gdn_recur_kernel, dim3((int64_t)batch_size * num_v_heads), dim3(kThreads), 0,
+                     s, g);
   hipLaunchKernelGGL(gdn_chunk_ext_kernel, dim3((int64_t)batch_size * num_v_heads),
                      dim3(kThreads), 0, s, g);
   hipLaunchKernelGGL(gdn_norm_ext_kernel,
