@@ -272,7 +272,7 @@ __global__ void __launch_bounds__(kThreads) gdn_conv_ext_kernel(GdnArgs a) {
         in[k] = p >= t0 ? ((e & 1) ? bf16_hi(pr) : bf16_lo(pr)) : bf(st[3 * e + p - t0 + 3]);
       }
       y[e] = round_bf(w[e][0] * in[0] + w[e][1] * in[1] + w[e][2] * in[2] + w[e][3] * in[3]);
-      y[e] = y[e] / (1.f + expf(-y[e]));
+      y[e] = y[e] / (1.f + expf(-y[e]));   // F.silu, rounded to bf16 below
     }
     *reinterpret_cast<u32x2*>(a.ws + (int64_t)tt * a.conv_dim + c) =
         u32x2{pack_bf16(y[0], y[1]), pack_bf16(y[2], y[3])};
@@ -430,7 +430,7 @@ struct PrepSmem {
   u32x4 qk[kChunk][65];            // per token: q hi, q lo, k hi, k lo (16 chunks each) + pad
   float kk[kChunk][kChunk + 1];    // k_t . k_s
   float qq[kChunk][kChunk + 1];    // q_t . k_s
-  float am[4][kChunk][kChunk + 1]; // A of the value head each wave solves
+  float am[4][kChunk][36];         // A of the value head each wave solves (16-B rows)
 };
 
 __global__ void __launch_bounds__(kThreads) gdn_chunk_prep_kernel(GdnArgs a) {
@@ -485,7 +485,7 @@ __global__ void __launch_bounds__(kThreads) gdn_chunk_prep_kernel(GdnArgs a) {
       if (n >= off) x += y;
     }
     const float gc = __shfl(x, kChunk - 1, 32);
-    float (*A)[kChunk + 1] = sm.am[w];
+    float (*A)[36] = sm.am[w];
     if (g == 0) {
       rec[kRecC + n] = __expf(x);
       rec[kRecD + n] = __expf(gc - x);
@@ -509,7 +509,12 @@ __global__ void __launch_bounds__(kThreads) gdn_chunk_prep_kernel(GdnArgs a) {
       for (int t = 0; t < kChunk; ++t) {
         float acc = t == n ? 1.f : 0.f;
 #pragma unroll
-        for (int s = 0; s < t; ++s) acc = fmaf(-A[t][s], tc[s], acc);
+        for (int s4 = 0; s4 < t; s4 += 4) {
+          const f32x4 ar = *reinterpret_cast<const f32x4*>(&A[t][s4]);
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            if (s4 + e < t) acc = fmaf(-ar[e], tc[s4 + e], acc);
+        }
         tc[t] = acc;
         __builtin_amdgcn_sched_barrier(0);
       }
@@ -547,8 +552,13 @@ __device__ __forceinline__ uint32_t row_half(const uint32_t (*rows)[128], int t,
   return row[128 * part + 8 * ((i >> 3) ^ (t & 15)) + (i & 7)];
 }
 
+constexpr int kKtStride = 40;   // bf16 per row of the transposed k copy (80 B: 8-B reads, few conflicts)
+
 __global__ void __launch_bounds__(kThreads) gdn_chunk_ext_kernel(GdnArgs a) {
   __shared__ __attribute__((aligned(16))) ChunkIn sm[2];
+  // k of the current chunk transposed, [part][dim][token], rebuilt per chunk:
+  // the state update reads 4 tokens of one dim per 8-byte load.
+  __shared__ __attribute__((aligned(16))) uint16_t kt[2][kDk][kKtStride];
   const int bi = blockIdx.x / a.hv, h = blockIdx.x % a.hv;
   const int hk = h / a.vpk;
   const int lane = threadIdx.x & (kWave - 1), w = wave_id();
@@ -627,6 +637,14 @@ __global__ void __launch_bounds__(kThreads) gdn_chunk_ext_kernel(GdnArgs a) {
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();   // chunk ci has landed; every wave is done with chunk ci - 1
     if (ci + 1 < nchunks) issue(ci + 1, (ci + 1) & 1);
+    {   // thread (part, dim) = (tid / 128, tid % 128) transposes its 32 tokens
+      const int i = threadIdx.x & (kDk - 1), part = threadIdx.x >> 7;
+#pragma unroll
+      for (int s2 = 0; s2 < kChunk; s2 += 2)
+        *reinterpret_cast<uint32_t*>(&kt[part][i][s2]) =
+            row_half(I.k, s2, i, part) | (row_half(I.k, s2 + 1, i, part) << 16);
+    }
+    __syncthreads();
 
     // P = K S0 and R = Q S0 over the state rows (k index 8 g + jj <-> state
     // row 32 ti + 16 hh + 8 (jj / 4) + 4 g + jj % 4)
@@ -693,15 +711,13 @@ __global__ void __launch_bounds__(kThreads) gdn_chunk_ext_kernel(GdnArgs a) {
       st[ti] *= cC;
 #pragma unroll
       for (int hh = 0; hh < 2; ++hh) {
-        // A operand: K^T rows i = 32 ti + n, tokens s(jj) as for Delta
-        u32x4 ah, al;
-#pragma unroll
-        for (int m = 0; m < 4; ++m) {
-          const int s0 = 16 * hh + 8 * (m >> 1) + 4 * g + 2 * (m & 1);
-          const int i = 32 * ti + n;
-          ah[m] = row_half(I.k, s0, i, 0) | (row_half(I.k, s0 + 1, i, 0) << 16);
-          al[m] = row_half(I.k, s0, i, 1) | (row_half(I.k, s0 + 1, i, 1) << 16);
-        }
+        // A operand: K^T row i = 32 ti + n at tokens s(jj) as for Delta
+        const int i = 32 * ti + n, s0 = 16 * hh + 4 * g;
+        const u32x2 h0 = *reinterpret_cast<const u32x2*>(&kt[0][i][s0]);
+        const u32x2 h1 = *reinterpret_cast<const u32x2*>(&kt[0][i][s0 + 8]);
+        const u32x2 l0 = *reinterpret_cast<const u32x2*>(&kt[1][i][s0]);
+        const u32x2 l1 = *reinterpret_cast<const u32x2*>(&kt[1][i][s0 + 8]);
+        const u32x4 ah = {h0[0], h0[1], h1[0], h1[1]}, al = {l0[0], l0[1], l1[0], l1[1]};
         st[ti] = mma3(st[ti], ah, al, dh[hh], dl[hh]);
       }
     }
