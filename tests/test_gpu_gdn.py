@@ -94,7 +94,9 @@ def test_decode_steps_match_oracle(gpu, bsz, hk, hv):
 
 
 @pytest.mark.parametrize("lens,hk,hv", [([5], 16, 48), ([1, 70, 3, 130], 16, 48),
-                                         ([200, 1, 1, 64, 2], 4, 12)])
+                                         ([200, 1, 1, 64, 2], 4, 12),
+                                         # 32-token chunk edges: exact, one over, one short
+                                         ([32, 64, 33, 31, 1, 2], 4, 12)])
 def test_extend_matches_oracle(gpu, lens, hk, hv):
     """Mixed extend lengths against the oracle's per-request loop (chunked WY
     update for ext > 1): two consecutive calls, the second with other lengths.
