@@ -272,7 +272,7 @@ __global__ void __launch_bounds__(kThreads) gdn_conv_ext_kernel(GdnArgs a) {
         in[k] = p >= t0 ? ((e & 1) ? bf16_hi(pr) : bf16_lo(pr)) : bf(st[3 * e + p - t0 + 3]);
       }
       y[e] = round_bf(w[e][0] * in[0] + w[e][1] * in[1] + w[e][2] * in[2] + w[e][3] * in[3]);
-      y[e] = y[e] / (1.f + expf(-y[e]));   // F.silu, rounded to bf16 below
+      y[e] = y[e] / (1.f + expf(-y[e]));   // F.silu (accurate exp: q / k / v feed everything)
     }
     *reinterpret_cast<u32x2*>(a.ws + (int64_t)tt * a.conv_dim + c) =
         u32x2{pack_bf16(y[0], y[1]), pack_bf16(y[2], y[3])};
@@ -427,7 +427,6 @@ __device__ __forceinline__ f32x16 mma3(f32x16 c, const u32x4& ah, const u32x4& a
 
 // ---- prep: one workgroup per (chunk record slot, key head)
 struct PrepSmem {
-  u32x4 qk[kChunk][65];            // per token: q hi, q lo, k hi, k lo (16 chunks each) + pad
   float kk[kChunk][kChunk + 1];    // k_t . k_s
   float qq[kChunk][kChunk + 1];    // q_t . k_s
   float am[4][kChunk][36];         // A of the value head each wave solves (16-B rows)
@@ -451,22 +450,24 @@ __global__ void __launch_bounds__(kThreads) gdn_chunk_prep_kernel(GdnArgs a) {
     return;
   const int tb = t0 + kChunk * ci, ntok = min(kChunk, t1 - tb), last = t1 - 1;
 
-  for (int q = threadIdx.x; q < kChunk * 64; q += kThreads) {
-    const int t = q >> 6, c = q & 63;
-    sm.qk[t][c] = *reinterpret_cast<const u32x4*>(
-        reinterpret_cast<const uint8_t*>(a.wqk) + ((int64_t)min(tb + t, last) * a.hk + hk) * 1024 +
-        16 * c);
-  }
-  __syncthreads();
   if (w < 2) {   // K K^T (wave 0), Q K^T (wave 1): rows t = lane n, dims 16 ks + 8 g .. + 7
-    f32x16 acc = {};
+    // operands straight from the split q / k rows (L2-resident): per token
+    // 64 16-byte chunks, q hi, q lo, k hi, k lo
+    const u32x4* row = reinterpret_cast<const u32x4*>(
+        reinterpret_cast<const uint8_t*>(a.wqk) + ((int64_t)min(tb + n, last) * a.hk + hk) * 1024);
+    const int xo = w == 0 ? 32 : 0;
+    u32x4 xh[8], xl[8], kh[8], kl[8];
 #pragma unroll
     for (int ks = 0; ks < 8; ++ks) {
       const int ch = 2 * ks + g;
-      const int xo = w == 0 ? 32 : 0;
-      acc = mma3(acc, sm.qk[n][xo + ch], sm.qk[n][xo + 16 + ch], sm.qk[n][32 + ch],
-                 sm.qk[n][48 + ch]);
+      xh[ks] = row[xo + ch];
+      xl[ks] = row[xo + 16 + ch];
+      kh[ks] = row[32 + ch];
+      kl[ks] = row[48 + ch];
     }
+    f32x16 acc = {};
+#pragma unroll
+    for (int ks = 0; ks < 8; ++ks) acc = mma3(acc, xh[ks], xl[ks], kh[ks], kl[ks]);
     float (*M)[kChunk + 1] = w == 0 ? sm.kk : sm.qq;
 #pragma unroll
     for (int rr = 0; rr < 16; ++rr) M[c_row(rr, g)][n] = acc[rr];
