@@ -51,6 +51,70 @@ def _workspace(device: torch.device, stream: torch.cuda.Stream, nbytes: int) -> 
         return ws
 
 
+class _Uploader:
+    """Host -> device copies of per-step plan lists through a ring of pinned
+    staging buffers (allocated once, grown on demand), so that a step neither
+    allocates pinned memory nor copies from pageable memory, either of which
+    can block the host until the GPU has caught up.  A slot is reused only
+    after its previous copy has executed (its event)."""
+
+    SLOTS = 32
+
+    def __init__(self):
+        self.bufs = [None] * self.SLOTS
+        self.events = [None] * self.SLOTS
+        self.next = 0
+
+    def upload(self, arr: np.ndarray, device: torch.device,
+               stream: torch.cuda.Stream) -> torch.Tensor:
+        i = self.next
+        self.next = (i + 1) % self.SLOTS
+        ev = self.events[i]
+        if ev is not None:
+            ev.synchronize()
+        buf = self.bufs[i]
+        if buf is None or buf.numel() < arr.size:
+            buf = torch.empty(max(arr.size, 1 << 16), dtype=torch.int32, pin_memory=True)
+            self.bufs[i] = buf
+        buf[: arr.size].numpy()[:] = arr
+        with torch.cuda.stream(stream):
+            dev = torch.empty(arr.size, dtype=torch.int32, device=device)
+            dev.copy_(buf[: arr.size], non_blocking=True)
+        if ev is None:
+            ev = torch.cuda.Event()
+            self.events[i] = ev
+        ev.record(stream)
+        return dev
+
+
+_uploaders: Dict[int, _Uploader] = {}
+
+
+def _upload(arr: np.ndarray, device: torch.device, stream: torch.cuda.Stream) -> torch.Tensor:
+    idx = device.index if device.index is not None else torch.cuda.current_device()
+    with _ws_lock:
+        up = _uploaders.get(idx)
+        if up is None:
+            up = _Uploader()
+            _uploaders[idx] = up
+        return up.upload(arr, device, stream)
+
+
+_side_streams: Dict[int, torch.cuda.Stream] = {}
+
+
+def _side_stream(device: torch.device) -> torch.cuda.Stream:
+    """A second stream per device (default priority) for the decode launches of
+    a mixed step, which then run beside the extend kernel."""
+    idx = device.index if device.index is not None else torch.cuda.current_device()
+    with _ws_lock:
+        st = _side_streams.get(idx)
+        if st is None:
+            st = torch.cuda.Stream(device=idx)
+            _side_streams[idx] = st
+        return st
+
+
 def _ptr(t) -> Optional[int]:
     return None if t is None else t.data_ptr()
 
@@ -113,11 +177,18 @@ class SlotAttentionCall:
     ``run()`` enqueues every kernel of the step. For timing, ``run_extend()``,
     ``run_decode_partial()`` and ``run_decode_merge()`` enqueue the individual
     launches; run in that order they are exactly ``run()``.
+
+    ``overlap_decode`` (default: ``device_plan``): on a mixed step, run the
+    decode launches on a second stream beside the extend kernel (the results
+    are identical). Meant for a call that is built once and run many times:
+    with a new call per step the ROCm runtime stalls the host periodically on
+    the cross-stream waits, so per-step calls keep one stream.
     """
 
     def __init__(self, q, layer_k_buffer, layer_v_buffer, batch, *, scaling=None,
                  k_scale=None, v_scale=None, decode_workgroups: int = 0, out=None,
-                 stream=None, gate=None, device_plan: bool = False):
+                 stream=None, gate=None, device_plan: bool = False,
+                 overlap_decode: Optional[bool] = None):
         _check_inputs(q, layer_k_buffer, layer_v_buffer, batch)
         n_tok, n_q, head_dim = q.shape
         n_slots, n_kv, _ = layer_k_buffer.shape
@@ -175,6 +246,7 @@ class SlotAttentionCall:
                            rtt.data_ptr(), rtt.shape[0], rtt.stride(0), rtt.shape[1],
                            batch.req_pool_indices.data_ptr(), batch.seq_lens.data_ptr(),
                            seq_override)
+        self.overlap_decode = device_plan if overlap_decode is None else bool(overlap_decode)
         self.n_work = 0
         self.n_dec = 0
         self._meta = None
@@ -210,8 +282,7 @@ class SlotAttentionCall:
             meta[: self.n_work * 8] = work.reshape(-1)
             meta[self.n_work * 8: self.n_work * 8 + self.n_dec] = items
             meta[self.n_work * 8 + self.n_dec: self.n_work * 8 + 2 * self.n_dec] = rows
-            with torch.cuda.stream(self.stream):
-                self._meta = torch.from_numpy(meta).pin_memory().to(q.device, non_blocking=True)
+            self._meta = _upload(meta, q.device, self.stream)
             base = self._meta.data_ptr() + 4 * self.n_work * 8
             if self.n_dec:
                 self._items = _DevPtr(base)
@@ -249,16 +320,17 @@ class SlotAttentionCall:
         n = self.n_work * 8 + 2 * self.n_dec
         return tuple(int(x) for x in self._meta[n:n + 3].cpu())
 
-    def _decode(self, entry: str) -> None:
+    def _decode(self, entry: str, stream: Optional[torch.cuda.Stream] = None) -> None:
         if not self.n_dec:
             return
         ws = self.ws
+        stream = stream if stream is not None else self.stream
         _native.call(entry, self.q.data_ptr(), self.q.stride(0), *self._pool_args,
                      _ptr(self._items), _ptr(self._rows), self.n_dec,
                      self.n_q, self.n_kv, self.head_dim, self.scaling,
                      self.out.data_ptr(), self.out.stride(0),
                      _ptr(ws), 0 if ws is None else ws.numel(), self.max_len,
-                     self.decode_workgroups, *self._gate_args, self.stream.cuda_stream)
+                     self.decode_workgroups, *self._gate_args, stream.cuda_stream)
 
     def run_extend(self) -> None:
         if self.n_work:
@@ -276,8 +348,20 @@ class SlotAttentionCall:
 
     def run(self) -> torch.Tensor:
         self.run_plan()
-        self.run_extend()
-        self._decode("tf_attn_decode")
+        if self.n_work and self.n_dec and self.overlap_decode:
+            # Mixed step: the HBM-bound decode launches go to a second stream and
+            # run beside the MFMA-bound extend kernel (they write disjoint rows
+            # of out); the caller's stream waits for both.
+            # (wait_stream: per-call Event objects destroyed while their
+            # waits are pending stall the host by a whole step on ROCm.)
+            main, side = self.stream, _side_stream(self.q.device)
+            side.wait_stream(main)
+            self._decode("tf_attn_decode", side)
+            self.run_extend()
+            main.wait_stream(side)
+        else:
+            self.run_extend()
+            self._decode("tf_attn_decode")
         return self.out
 
 
