@@ -649,7 +649,9 @@ __global__ void __launch_bounds__(kThreads) gdn_chunk_ext_kernel(GdnArgs a) {
 
     // P = K S0 and R = Q S0 over the state rows (k index 8 g + jj <-> state
     // row 32 ti + 16 hh + 8 (jj / 4) + 4 g + jj % 4)
-    f32x16 P = {}, R = {};
+    // (two accumulators each for P and R, one per half of the state rows:
+    // four independent MFMA chains)
+    f32x16 Pp[2] = {{}, {}}, Rp[2] = {{}, {}};
 #pragma unroll
     for (int ti = 0; ti < 4; ++ti) {
 #pragma unroll
@@ -659,10 +661,11 @@ __global__ void __launch_bounds__(kThreads) gdn_chunk_ext_kernel(GdnArgs a) {
         const int d0 = 32 * ti + 16 * hh + 4 * g;
         row8(I.k, n, d0, kh, kl);
         row8(I.q, n, d0, qh, ql);
-        P = mma3(P, kh, kl, sh, sl);
-        R = mma3(R, qh, ql, sh, sl);
+        Pp[ti >> 1] = mma3(Pp[ti >> 1], kh, kl, sh, sl);
+        Rp[ti >> 1] = mma3(Rp[ti >> 1], qh, ql, sh, sl);
       }
     }
+    const f32x16 P = Pp[0] + Pp[1], R = Rp[0] + Rp[1];
     // X = beta (v - e^gamma P); Delta = T X (k index 8 g + jj <-> token
     // 16 hh + 8 (jj / 4) + 4 g + jj % 4)
     f32x16 X;
@@ -671,7 +674,7 @@ __global__ void __launch_bounds__(kThreads) gdn_chunk_ext_kernel(GdnArgs a) {
       const int t = c_row(rr, g);
       X[rr] = I.rec[kRecBeta + t] * (bf(I.v[t][j]) - I.rec[kRecC + t] * P[rr]);
     }
-    f32x16 D = {};
+    f32x16 Dp[2];
 #pragma unroll
     for (int hh = 0; hh < 2; ++hh) {
       u32x4 xh, xl, th, tl;
@@ -679,21 +682,23 @@ __global__ void __launch_bounds__(kThreads) gdn_chunk_ext_kernel(GdnArgs a) {
       const float* trow = &I.rec[kRecT + n * kChunk + 16 * hh + 4 * g];
       split8(*reinterpret_cast<const f32x4*>(trow), *reinterpret_cast<const f32x4*>(trow + 8), th,
              tl);
-      D = mma3(D, th, tl, xh, xl);
+      Dp[hh] = mma3(f32x16{}, th, tl, xh, xl);
     }
+    f32x16 D = Dp[0] + Dp[1];
     // O = e^gamma R + Bm Delta -> the recurrence output rows of this chunk
     u32x4 dh[2], dl[2];
     split16(D, 0, dh[0], dl[0]);
     split16(D, 8, dh[1], dl[1]);
-    f32x16 O = {};
+    f32x16 Op[2];
 #pragma unroll
     for (int hh = 0; hh < 2; ++hh) {
       u32x4 bh, bl;
       const float* brow = &I.rec[kRecB + n * kChunk + 16 * hh + 4 * g];
       split8(*reinterpret_cast<const f32x4*>(brow), *reinterpret_cast<const f32x4*>(brow + 8), bh,
              bl);
-      O = mma3(O, bh, bl, dh[hh], dl[hh]);
+      Op[hh] = mma3(f32x16{}, bh, bl, dh[hh], dl[hh]);
     }
+    const f32x16 O = Op[0] + Op[1];
 #pragma unroll
     for (int rr = 0; rr < 16; ++rr) {
       const int t = c_row(rr, g);
