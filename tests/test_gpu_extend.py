@@ -63,6 +63,26 @@ def test_mixed_chunked_prefill_and_decode(gpu):
     check(wl, "mixed")
 
 
+def test_mixed_step_with_decode_on_a_second_stream(gpu):
+    """A reused call with overlap_decode=True (decode launches on a second
+    stream beside the extend kernel) gives the one-stream result bit for bit,
+    run after run, and matches the oracle."""
+    from tokenfactory_amd.attention import SlotAttentionCall
+    wl = workloads.mixed(device=gpu, n_extend=3, extend_new=150, prefix_hi=700, n_decode=9,
+                         dec_lo=1, dec_hi=2500, pool_slots=1 << 15)
+    serial = SlotAttentionCall(wl.q, wl.k_pool, wl.v_pool, wl.batch, scaling=wl.scale,
+                               overlap_decode=False).run().clone()
+    call = SlotAttentionCall(wl.q, wl.k_pool, wl.v_pool, wl.batch, scaling=wl.scale,
+                             overlap_decode=True)
+    assert call.n_work and call.n_dec
+    for _ in range(3):
+        call.out.zero_()
+        out = call.run()
+        torch.cuda.synchronize()
+        assert torch.equal(out, serial)
+    assert_attn_close(out, restatement(wl), what="mixed, decode overlapped")
+
+
 def test_prefix_extend_rows_equal_full_prefill(gpu):
     P, N = 300, 90
     full = small_case([P + N], [P + N], hq=24, hkv=4, d=256, seed=3, device=gpu,
