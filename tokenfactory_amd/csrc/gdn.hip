@@ -35,7 +35,6 @@ constexpr int kDk = 128;
 constexpr int kDv = 128;
 constexpr int kThreads = 256;
 constexpr int kRowGroups = kThreads / 32;   // 8 row groups of 16 rows
-constexpr int kColBlk = kDv / (kThreads / kWave);   // extend: state columns per wave (32)
 
 struct GdnArgs {
   const uint16_t* qkv;   // bf16 [B, conv_dim]
@@ -343,16 +342,12 @@ __global__ void __launch_bounds__(kThreads) gdn_qk_ext_kernel(GdnArgs a) {
   }
 }
 
-// global_load_lds_dword{,x4} with a scalar base and a 32-bit lane offset: lane
-// l's 4 / 16 bytes land at LDS address M0 + 4 l / 16 l.  The compiler does not
+// global_load_lds_dwordx4 with a scalar base and a 32-bit lane offset: lane
+// l's 16 bytes land at LDS address M0 + 16 l.  The compiler does not
 // count these loads: readers wait with an explicit s_waitcnt vmcnt and a
 // barrier.
 __device__ __forceinline__ uint32_t lds_addr(const void* p) {
   return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
-}
-__device__ __forceinline__ void dma4(const void* sbase, uint32_t voff, uint32_t lds) {
-  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dword %0, %1"
-               :: "v"(voff), "s"(sbase), "s"(lds) : "m0");
 }
 __device__ __forceinline__ void dma16(const void* sbase, uint32_t voff, uint32_t lds) {
   asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1"
