@@ -381,8 +381,8 @@ int32_t tf_gdn_decode(const void* qkv, int64_t qkv_row_stride, const void* a, co
  * parallel, the state-independent part of every chunk in parallel, the
  * chunked recurrence (one workgroup per request and value head, its state in
  * registers from first chunk to last) and the gated norm for every (token,
- * value head) in parallel.  qkv must be 8-byte aligned with qkv_row_stride a multiple of 4;
- * z, out and core_out 4-byte aligned with even row strides.  Other arguments
+ * value head) in parallel.  qkv, z, out and core_out must be 8-byte aligned
+ * with row strides that are multiples of 4; norm_weight 16-byte aligned.  Other arguments
  * as for tf_gdn_decode, with rows = tokens; workspace:
  * tf_gdn_extend_workspace_bytes(n_tokens, batch_size, Hk, Hv) bytes, 16-byte
  * aligned.

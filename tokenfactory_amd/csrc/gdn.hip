@@ -740,34 +740,43 @@ __global__ void __launch_bounds__(kThreads) gdn_chunk_ext_kernel(GdnArgs a) {
   }
 }
 
-// Gated RMSNorm (rms_norm_gated.py:26-40) of one (token, value head) per wave
-// from the bf16 recurrence output: lane l holds dims 2 l, 2 l + 1 and the sum
-// of squares is a wave reduction (grid: token rows x blocks of 4 value heads).
-// Also copies the recurrence output to core_out when asked.  Rows of requests
-// whose slot is outside the pool are left untouched, as in the recurrence.
+// Gated RMSNorm (rms_norm_gated.py:26-40) of two (token, value head) rows per
+// wave from the bf16 recurrence output: each half-wave takes one head, lane l
+// of it dims 4 l .. 4 l + 3, and the sum of squares is a 32-lane reduction
+// (grid: token rows x blocks of 8 value heads).  Also copies the recurrence
+// output to core_out when asked.  Rows of requests whose slot is outside the
+// pool are left untouched, as in the recurrence; rows of one-token requests
+// were written by gdn_recur_kernel.
+constexpr int kNormHeads = 2 * kThreads / kWave;   // value heads per workgroup
+
 __global__ void __launch_bounds__(kThreads) gdn_norm_ext_kernel(GdnArgs a) {
   const int tok = blockIdx.x;
-  const int h = blockIdx.y * (kThreads / kWave) + wave_id();
+  const int lane = threadIdx.x & (kWave - 1);
+  const int h = blockIdx.y * kNormHeads + 2 * wave_id() + (lane >> 5);
   const int bo = a.owner[tok];
-  if (h >= a.hv || bo < 0) return;
+  if (bo < 0) return;
   if (min(max(a.tok[bo + 1], 0), a.rows) - min(max(a.tok[bo], 0), a.rows) == 1)
     return;   // a one-token request: gdn_recur_kernel wrote its row
-  const int lane = threadIdx.x & (kWave - 1);
-  const int d = 2 * lane;
-  const uint32_t ob =
-      *reinterpret_cast<const uint32_t*>(a.wcore + (int64_t)tok * (a.hv * kDv) + h * kDv + d);
-  if (a.core) *reinterpret_cast<uint32_t*>(a.core + tok * a.core_rs + h * kDv + d) = ob;
-  const float o0 = bf16_lo(ob), o1 = bf16_hi(ob);
-  float v2 = o0 * o0 + o1 * o1;
+  const bool act = h < a.hv;
+  const int d = 4 * (lane & 31);
+  const int hc = act ? h : 0;
+  const u32x2 ob =
+      *reinterpret_cast<const u32x2*>(a.wcore + (int64_t)tok * (a.hv * kDv) + hc * kDv + d);
+  const float o[4] = {bf16_lo(ob[0]), bf16_hi(ob[0]), bf16_lo(ob[1]), bf16_hi(ob[1])};
+  float v2 = act ? o[0] * o[0] + o[1] * o[1] + o[2] * o[2] + o[3] * o[3] : 0.f;
 #pragma unroll
-  for (int s2 = 32; s2 >= 1; s2 >>= 1) v2 += __shfl_xor(v2, s2, kWave);
+  for (int s2 = 16; s2 >= 1; s2 >>= 1) v2 += __shfl_xor(v2, s2, kWave);
+  if (!act) return;
+  if (a.core) *reinterpret_cast<u32x2*>(a.core + tok * a.core_rs + h * kDv + d) = ob;
   const float inv = rsqrtf(v2 / (float)kDv + a.eps);
-  const uint32_t zz = *reinterpret_cast<const uint32_t*>(a.z + tok * a.z_rs + h * kDv + d);
-  const float z0 = bf16_lo(zz), z1 = bf16_hi(zz);
-  const float* nw = a.norm_w + h * kDv + d;
-  *reinterpret_cast<uint32_t*>(a.out + tok * a.out_rs + h * kDv + d) =
-      pack_bf16(nw[0] * (o0 * inv) * (z0 / (1.f + expf(-z0))),
-                nw[1] * (o1 * inv) * (z1 / (1.f + expf(-z1))));
+  const u32x2 zz = *reinterpret_cast<const u32x2*>(a.z + tok * a.z_rs + h * kDv + d);
+  const float z[4] = {bf16_lo(zz[0]), bf16_hi(zz[0]), bf16_lo(zz[1]), bf16_hi(zz[1])};
+  const f32x4 nw = *reinterpret_cast<const f32x4*>(a.norm_w + h * kDv + d);
+  float y[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) y[e] = nw[e] * (o[e] * inv) * (z[e] / (1.f + expf(-z[e])));
+  *reinterpret_cast<u32x2*>(a.out + tok * a.out_rs + h * kDv + d) =
+      u32x2{pack_bf16(y[0], y[1]), pack_bf16(y[2], y[3])};
 }
 
 }  // namespace
@@ -960,12 +969,13 @@ int32_t tf_gdn_extend(const void* qkv, int64_t qkv_row_stride, const void* a, co
       n_slots_rec * num_v_heads * kRec * 4 > UINT32_MAX)
     return fail(TF_ERR_UNSUPPORTED, "gdn_extend: too many tokens (32-bit staging offsets)");
   if ((reinterpret_cast<uintptr_t>(qkv) & 7u) || qkv_row_stride % 4 ||
-      (reinterpret_cast<uintptr_t>(z) & 3u) || z_row_stride % 2 ||
-      (reinterpret_cast<uintptr_t>(out) & 3u) || out_row_stride % 2 ||
-      (core_out && ((reinterpret_cast<uintptr_t>(core_out) & 3u) || core_row_stride % 2)))
+      (reinterpret_cast<uintptr_t>(z) & 7u) || z_row_stride % 4 ||
+      (reinterpret_cast<uintptr_t>(out) & 7u) || out_row_stride % 4 ||
+      (core_out && ((reinterpret_cast<uintptr_t>(core_out) & 7u) || core_row_stride % 4)) ||
+      !aligned16(norm_weight))
     return fail(TF_ERR_INVALID,
-                "gdn_extend: qkv must be 8-byte aligned with a row stride that is a multiple "
-                "of 4; z / out / core_out 4-byte aligned with even row strides");
+                "gdn_extend: qkv, z, out and core_out must be 8-byte aligned with row strides "
+                "that are multiples of 4; norm_weight 16-byte aligned");
   g.tok = token_offsets;
   uint8_t* w = static_cast<uint8_t*>(workspace);
   const int64_t conv_bytes = n_tokens * g.conv_dim * 2;
@@ -998,8 +1008,7 @@ int32_t tf_gdn_extend(const void* qkv, int64_t qkv_row_stride, const void* a, co
   hipLaunchKernelGGL(gdn_chunk_ext_kernel, dim3((int64_t)batch_size * num_v_heads),
                      dim3(kThreads), 0, s, g);
   hipLaunchKernelGGL(gdn_norm_ext_kernel,
-                     dim3((uint32_t)n_tokens,
-                          (num_v_heads + kThreads / kWave - 1) / (kThreads / kWave)),
+                     dim3((uint32_t)n_tokens, (num_v_heads + kNormHeads - 1) / kNormHeads),
                      dim3(kThreads), 0, s, g);
   return launch_status("tf_gdn_extend launch");
 }
