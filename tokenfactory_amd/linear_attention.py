@@ -13,7 +13,8 @@ layer's conv and SSM states in place.
 ``forward(hidden_states, cache_pool, forward_batch)``: all-decode batches run
 ``gdn_decode_step``; batches with longer extends run ``gdn_extend_step``
 (``tf_gdn_extend``), the reference's per-request conv + chunked-update loop
-computed token by token with each head's state held in registers.
+(the same chunk-wise WY update on MFMAs, 32-token chunks, each head's state
+held in registers from the first chunk to the last).
 """
 from __future__ import annotations
 
