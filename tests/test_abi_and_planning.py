@@ -50,6 +50,24 @@ def test_decode_workspace_size_and_unsupported_arguments():
         _native.decode_workspace_bytes(4, 16, 2, 256, 512, -1)
 
 
+def test_gdn_extend_workspace_covers_rows_and_chunk_records():
+    # Per token row: conv outputs (bf16), split q / k (4 x 128 bf16 per key
+    # head), gates (2 fp32 per value head), recurrence output (bf16), the row's
+    # request (int32); then one 9 KB record per (32-token chunk slot, value
+    # head), with n_tokens / 32 + batch + 1 slots.
+    lib = _native.load()
+    hk, hv = 16, 48
+    row = (2 * hk * 128 + hv * 128) * 2 + hk * 4 * 128 * 2 + hv * 8 + hv * 128 * 2 + 4
+    for n_tok, bsz in [(1, 1), (8320, 132), (70, 3)]:
+        got = lib.tf_gdn_extend_workspace_bytes(n_tok, bsz, hk, hv)
+        assert got >= n_tok * row + (n_tok // 32 + bsz + 1) * hv * 2304 * 4
+        assert got <= n_tok * row + 80 + (n_tok // 32 + bsz + 1) * hv * 2304 * 4
+    assert lib.tf_gdn_extend_workspace_bytes(100, 5, hk, hv) < \
+        lib.tf_gdn_extend_workspace_bytes(100, 6, hk, hv)
+    assert lib.tf_gdn_extend_workspace_bytes(10, -1, hk, hv) == _native.TF_ERR_INVALID
+    assert lib.tf_gdn_extend_workspace_bytes(10, 1, 0, hv) == _native.TF_ERR_INVALID
+
+
 def test_entry_points_reject_bad_arguments_before_launching():
     lib = _native.load()
     rc = lib.tf_attn_decode(None, 0, None, None, 16, 0, None, None, None, 1, 16, 16,
