@@ -100,6 +100,24 @@ def _upload(arr: np.ndarray, device: torch.device, stream: torch.cuda.Stream) ->
         return up.upload(arr, device, stream)
 
 
+_fork_events: Dict[Tuple[int, int], Tuple[torch.cuda.Event, torch.cuda.Event]] = {}
+
+
+def _fork_join_events(device: torch.device, main: torch.cuda.Stream):
+    """Two events per (device, caller stream), created once and re-recorded by
+    every mixed step on that stream (a wait enqueued earlier keeps the record
+    it saw).  Events made per step and destroyed while their waits are still
+    queued stall the host by about a step on ROCm."""
+    idx = device.index if device.index is not None else torch.cuda.current_device()
+    key = (idx, main.cuda_stream)
+    with _ws_lock:
+        ev = _fork_events.get(key)
+        if ev is None:
+            ev = (torch.cuda.Event(), torch.cuda.Event())
+            _fork_events[key] = ev
+        return ev
+
+
 _side_streams: Dict[int, torch.cuda.Stream] = {}
 
 
@@ -352,13 +370,14 @@ class SlotAttentionCall:
             # Mixed step: the HBM-bound decode launches go to a second stream and
             # run beside the MFMA-bound extend kernel (they write disjoint rows
             # of out); the caller's stream waits for both.
-            # (wait_stream: per-call Event objects destroyed while their
-            # waits are pending stall the host by a whole step on ROCm.)
             main, side = self.stream, _side_stream(self.q.device)
-            side.wait_stream(main)
+            fork, join = _fork_join_events(self.q.device, main)
+            fork.record(main)
+            side.wait_event(fork)
             self._decode("tf_attn_decode", side)
             self.run_extend()
-            main.wait_stream(side)
+            join.record(side)
+            main.wait_event(join)
         else:
             self.run_extend()
             self._decode("tf_attn_decode")
