@@ -27,12 +27,14 @@ def rand_inputs(t, hk, hv, seed):
     return q, k, v, a, b, a_log, dt_bias, state
 
 
-@pytest.mark.parametrize("t", [5, 64, 70])
-def test_chunked_prefill_equals_recurrence(t):
+@pytest.mark.parametrize("t,chunk", [(5, 64), (64, 64), (70, 64), (70, 32), (33, 32)])
+def test_chunked_prefill_equals_recurrence(t, chunk):
+    # chunk 64: the reference's chunk length; chunk 32: the GPU kernel's
     hk, hv = 2, 6
     q, k, v, a, b, a_log, dt_bias, s0 = rand_inputs(t, hk, hv, t)
     s_chunk = s0.clone()
-    out_chunk = og.gated_delta_rule_chunked(q, k, v, b, a, s_chunk, a_log, dt_bias, hv // hk)
+    out_chunk = og.gated_delta_rule_chunked(q, k, v, b, a, s_chunk, a_log, dt_bias, hv // hk,
+                                            chunk_size=chunk)
     s = s0.clone()
     outs = []
     for i in range(t):
