@@ -427,7 +427,7 @@ struct PrepSmem {
   float am[4][kChunk][36];         // A of the value head each wave solves (16-B rows)
 };
 
-__global__ void __launch_bounds__(kThreads) gdn_chunk_prep_kernel(GdnArgs a) {
+__global__ void __launch_bounds__(kThreads, 4) gdn_chunk_prep_kernel(GdnArgs a) {
   __shared__ __attribute__((aligned(16))) PrepSmem sm;
   const int slot = blockIdx.x, hk = blockIdx.y;
   const int lane = threadIdx.x & (kWave - 1), w = wave_id();
