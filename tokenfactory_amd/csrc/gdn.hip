@@ -211,7 +211,7 @@ __global__ void __launch_bounds__(kThreads) gdn_recur_kernel(GdnArgs a) {
 // recurrence is the reference's chunked WY update (:194-242) computed one
 // token at a time; both are the same linear recurrence.
 
-constexpr int kConvTokens = 16;   // tokens per thread in the extend conv
+constexpr int kConvTokens = 8;    // tokens per thread in the extend conv
 
 // owner[tt] = the request whose rows hold tt, or -1 when none does or the
 // request's slot is outside the pool (those rows are skipped everywhere).
