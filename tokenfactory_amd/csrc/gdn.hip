@@ -302,35 +302,55 @@ __global__ void __launch_bounds__(kThreads) gdn_conv_state_kernel(GdnArgs a) {
 // the log-decay g = log alpha and beta.  None of it depends on the state,
 // so it runs for all tokens in parallel ahead of the recurrence.
 __global__ void __launch_bounds__(kThreads) gdn_qk_ext_kernel(GdnArgs a) {
-  // One wave per (token, key head): lane l normalises dims 2 l, 2 l + 1 of q
-  // and of k, each norm a wave reduction (grid: token rows x blocks of 4 key
-  // heads); the first block of each token also forms the value heads' gates.
+  // One half-wave per (token, key head): lane l of it normalises dims 4 l ..
+  // 4 l + 3 of q and of k, each norm a 32-lane reduction (grid: token rows x
+  // blocks of 8 key heads); the first block of each token also forms the
+  // value heads' gates.
   const int tok = blockIdx.x;
-  const int hk = blockIdx.y * (kThreads / kWave) + wave_id();
   const int lane = threadIdx.x & (kWave - 1);
-  if (hk < a.hk) {
-    const uint16_t* y = a.ws + (int64_t)tok * a.conv_dim;
-    const uint32_t qv = *reinterpret_cast<const uint32_t*>(y + hk * kDk + 2 * lane);
-    const uint32_t kv = *reinterpret_cast<const uint32_t*>(y + a.key_dim + hk * kDk + 2 * lane);
-    const float q0 = bf16_lo(qv), q1 = bf16_hi(qv), k0 = bf16_lo(kv), k1 = bf16_hi(kv);
-    float sq = q0 * q0 + q1 * q1, sk = k0 * k0 + k1 * k1;
+  const int hk = blockIdx.y * (2 * kThreads / kWave) + 2 * wave_id() + (lane >> 5);
+  const bool act = hk < a.hk;
+  const int d = 4 * (lane & 31);
+  {
+    const uint16_t* y = a.ws + (int64_t)tok * a.conv_dim + (act ? hk : 0) * kDk + d;
+    const u32x2 qv = *reinterpret_cast<const u32x2*>(y);
+    const u32x2 kv = *reinterpret_cast<const u32x2*>(y + a.key_dim);
+    const float q[4] = {bf16_lo(qv[0]), bf16_hi(qv[0]), bf16_lo(qv[1]), bf16_hi(qv[1])};
+    const float k[4] = {bf16_lo(kv[0]), bf16_hi(kv[0]), bf16_lo(kv[1]), bf16_hi(kv[1])};
+    float sq = 0.f, sk = 0.f;
 #pragma unroll
-    for (int d = 32; d >= 1; d >>= 1) {
-      sq += __shfl_xor(sq, d, kWave);
-      sk += __shfl_xor(sk, d, kWave);
+    for (int e = 0; e < 4; ++e) {
+      sq += q[e] * q[e];
+      sk += k[e] * k[e];
     }
-    const float nq = fmaxf(sqrtf(sq), 1e-12f), nk = fmaxf(sqrtf(sk), 1e-12f);
-    // q (x 128 ** -0.5), then k, each as bf16 high parts and the bf16
-    // rounding of the remainders (the two MFMA operand halves)
-    uint16_t* qk = a.wqk + ((int64_t)tok * a.hk + hk) * (4 * kDk);
-    const float qa = q0 / nq * 0.08838834764831845f, qb = q1 / nq * 0.08838834764831845f;
-    const float ka = k0 / nk, kb = k1 / nk;
-    const uint32_t qh = pack_bf16(qa, qb), kh = pack_bf16(ka, kb);
-    uint32_t* q32 = reinterpret_cast<uint32_t*>(qk);
-    q32[lane] = qh;
-    q32[kDk / 2 + lane] = pack_bf16(qa - bf16_lo(qh), qb - bf16_hi(qh));
-    q32[kDk + lane] = kh;
-    q32[3 * kDk / 2 + lane] = pack_bf16(ka - bf16_lo(kh), kb - bf16_hi(kh));
+#pragma unroll
+    for (int m = 16; m >= 1; m >>= 1) {
+      sq += __shfl_xor(sq, m, kWave);
+      sk += __shfl_xor(sk, m, kWave);
+    }
+    if (act) {
+      const float nq = fmaxf(sqrtf(sq), 1e-12f), nk = fmaxf(sqrtf(sk), 1e-12f);
+      float qn[4], kn[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        qn[e] = q[e] / nq * 0.08838834764831845f;   // q x 128 ** -0.5
+        kn[e] = k[e] / nk;
+      }
+      // q, then k, each as bf16 high parts and the bf16 rounding of the
+      // remainders (the two MFMA operand halves)
+      uint32_t* q32 = reinterpret_cast<uint32_t*>(a.wqk + ((int64_t)tok * a.hk + hk) * (4 * kDk));
+      const int i = d / 2;   // dword of dims d, d + 1
+      const uint32_t qh0 = pack_bf16(qn[0], qn[1]), qh1 = pack_bf16(qn[2], qn[3]);
+      const uint32_t kh0 = pack_bf16(kn[0], kn[1]), kh1 = pack_bf16(kn[2], kn[3]);
+      *reinterpret_cast<u32x2*>(q32 + i) = u32x2{qh0, qh1};
+      *reinterpret_cast<u32x2*>(q32 + kDk / 2 + i) =
+          u32x2{pack_bf16(qn[0] - bf16_lo(qh0), qn[1] - bf16_hi(qh0)),
+                pack_bf16(qn[2] - bf16_lo(qh1), qn[3] - bf16_hi(qh1))};
+      *reinterpret_cast<u32x2*>(q32 + kDk + i) = u32x2{kh0, kh1};
+      *reinterpret_cast<u32x2*>(q32 + 3 * kDk / 2 + i) =
+          u32x2{pack_bf16(kn[0] - bf16_lo(kh0), kn[1] - bf16_hi(kh0)),
+                pack_bf16(kn[2] - bf16_lo(kh1), kn[3] - bf16_hi(kh1))};
+    }
   }
   if (blockIdx.y != 0) return;
   for (int h = threadIdx.x; h < a.hv; h += kThreads) {
@@ -999,7 +1019,7 @@ int32_t tf_gdn_extend(const void* qkv, int64_t qkv_row_stride, const void* a, co
   hipLaunchKernelGGL(gdn_conv_state_kernel, dim3(cblocks, batch_size), dim3(kThreads), 0, s, g);
   hipLaunchKernelGGL(gdn_qk_ext_kernel,
                      dim3((uint32_t)n_tokens,
-                          (num_k_heads + kThreads / kWave - 1) / (kThreads / kWave)),
+                          (num_k_heads + 2 * kThreads / kWave - 1) / (2 * kThreads / kWave)),
                      dim3(kThreads), 0, s, g);
   hipLaunchKernelGGL(gdn_chunk_prep_kernel, dim3((uint32_t)n_slots_rec, num_k_heads),
                      dim3(kThreads), 0, s, g);
