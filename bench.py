@@ -459,43 +459,93 @@ def bench_copy(torch, args):
     return {"bytes_read": n, "bytes_written": n, "ms": ms}
 
 
+def _time_host(fn, seconds, min_runs):
+    """Median, p10 and p90 (s) of ``fn`` over at least ``min_runs`` runs and
+    ``seconds`` of wall time, after 10 warm-up runs."""
+    for _ in range(10):
+        fn()
+    times = []
+    t_end = time.perf_counter() + seconds
+    while time.perf_counter() < t_end or len(times) < min_runs:
+        t0 = time.perf_counter_ns()
+        fn()
+        times.append((time.perf_counter_ns() - t0) * 1e-9)
+    times.sort()
+    return _pct(times, 0.5), _pct(times, 0.1), _pct(times, 0.9), len(times)
+
+
 def cpu_baseline(torch, dec_res):
-    """The oracle's restatement of the reference decode branch, fp32, host cores."""
+    """The oracle's op-for-op restatement of the reference decode branch
+    (full_attention.py:215-242), fp32, on every host core this process may use.
+
+    Headline: the reference's own CPU decode case (batch 4, contexts
+    128/256/384/512, 16 q / 2 kv heads, head_dim 256, fp32 4096-slot pool).
+    Also reported: 4 requests of the GPU headline step (decode_b64), in the same
+    bf16 algorithmic bytes as the GPU line."""
     from oracle.harness import prepare_host_inputs
     from oracle.slot_attention import slot_based_attention_ref
+    from tokenfactory_amd import workloads
     from tokenfactory_amd.workloads import subset
-    wl = dec_res["workloads"][0]
-    pick = [0, 17, 40, 63]
-    sub = subset(wl, pick)
-    host_args = prepare_host_inputs(sub)
-    cores = min(16, len(os.sched_getaffinity(0)))
+    cores = len(os.sched_getaffinity(0))
     torch.set_num_threads(cores)
-    fn = lambda: slot_based_attention_ref(*host_args)
-    fn()
-    times = []
-    t_end = time.perf_counter() + 15.0
-    while time.perf_counter() < t_end or len(times) < 3:
-        t0 = time.perf_counter()
-        fn()
-        times.append(time.perf_counter() - t0)
-    times.sort()
-    med = times[len(times) // 2]
-    nbytes = sub.decode_bytes()
-    # The restatement reads fp32 K/V; report the same algorithmic (bf16) bytes as the GPU.
-    log(f"cpu baseline: {med*1e3:.1f} ms per 4-request sample on {cores} threads "
-        f"({nbytes/med/1e9:.2f} GB/s)")
     cpu = None
     try:
         with open("/proc/cpuinfo") as fh:
             cpu = next((ln.split(":", 1)[1].strip() for ln in fh if "model name" in ln), None)
     except OSError:
         pass
+
+    small = workloads.decode_cpu_small(device="cpu")
+    args = (small.q, small.k_pool, small.v_pool, small.batch,
+            small.num_q_heads // small.num_kv_heads, small.scale)
+    med, p10, p90, n = _time_host(lambda: slot_based_attention_ref(*args), 12.0, 50)
+    # fp32 everywhere: K/V rows, int64 slot ids, q read and out written.
+    sum_l = sum(small.seq_lens)
+    nbytes = (sum_l * (2 * small.num_kv_heads * small.head_dim * 4 + 8)
+              + 2 * len(small.seq_lens) * small.num_q_heads * small.head_dim * 4)
+    flops = 4 * small.num_q_heads * small.head_dim * sum_l
+    log(f"cpu baseline (reference CPU decode case): {med*1e3:.3f} ms on {cores} threads "
+        f"({nbytes/med/1e9:.2f} GB/s)")
+
+    wl = dec_res["workloads"][0]
+    sub = subset(wl, [0, 17, 40, 63])
+    host_args = prepare_host_inputs(sub)
+    med2, _, _, n2 = _time_host(lambda: slot_based_attention_ref(*host_args), 8.0, 3)
+    b2 = sub.decode_bytes()
+    log(f"cpu baseline (4 decode_b64 requests): {med2*1e3:.1f} ms ({b2/med2/1e9:.2f} GB/s)")
     return {"value": nbytes / med / 1e9, "unit": "GB/s", "cores": cores, "kind": "port",
-            "sample": f"4 of the 64 decode requests (contexts {sub.seq_lens}), fp32 op-for-op "
-                      f"restatement of full_attention.py:215-242 (padded gather, "
-                      f"repeat_interleave, -inf mask, SDPA); median of {len(times)} runs; "
-                      f"same algorithmic bytes as the GPU line",
-            "ms_per_sample": med * 1e3, "cpu_model": cpu}
+            "sample": "the reference's CPU decode case: batch 4, contexts 128/256/384/512, "
+                      "16 q / 2 kv heads, head_dim 256, fp32 KV in a 4096-slot pool, slots a "
+                      "seeded random subset; fp32 op-for-op restatement of "
+                      "full_attention.py:215-242 (padded gather, clamp, repeat_interleave, "
+                      f"-inf mask, SDPA); median of {n} runs after 10 warm-up runs; "
+                      "algorithmic fp32 bytes (K/V rows, int64 slot ids, q, out)",
+            "ms_per_call": med * 1e3, "ms_p10_p90": [p10 * 1e3, p90 * 1e3],
+            "bytes_per_call": nbytes, "gflops": flops / med / 1e9, "cpu_model": cpu,
+            "decode_b64_sample": {
+                "value": b2 / med2 / 1e9, "unit": "GB/s", "ms_per_sample": med2 * 1e3,
+                "runs": n2,
+                "sample": f"4 of the 64 decode_b64 requests (contexts {sub.seq_lens}), "
+                          "same restatement in fp32, bf16 algorithmic bytes as the GPU line"}}
+
+
+def measured_traffic():
+    """HBM bytes per launch of the decode kernel from the committed FETCH_SIZE /
+    WRITE_SIZE measurement, or None when that measurement was taken on other
+    kernel sources than the ones built now (the file records their hash)."""
+    import hashlib
+    f = REPO / "profiles" / "decode_b64_hbm_traffic.json"
+    try:
+        rec = json.loads(f.read_text())
+    except (ValueError, OSError):
+        return None
+    srcs = rec.get("sources", {})
+    for name, digest in srcs.items():
+        path = REPO / "tokenfactory_amd" / "csrc" / name
+        if not path.exists() or hashlib.sha256(path.read_bytes()).hexdigest() != digest:
+            log(f"traffic: {f.name} was measured on another {name}; reporting null")
+            return None
+    return rec.get("bytes_per_launch") if srcs else None
 
 
 def main():
@@ -545,13 +595,7 @@ def main():
         print(json.dumps({"metric": METRIC, "value": None, "secondary": secondary},
                          default=float))
         return
-    traffic_file = REPO / "profiles" / "decode_b64_hbm_traffic.json"
-    if traffic_file.exists():
-        try:
-            dec["roofline"]["traffic"] = json.loads(traffic_file.read_text()).get(
-                "bytes_per_launch")
-        except (ValueError, OSError):
-            pass
+    dec["roofline"]["traffic"] = measured_traffic()
     cpu = None if args.no_cpu else cpu_baseline(torch, dec)
     line = {
         "metric": METRIC,

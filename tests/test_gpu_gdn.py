@@ -100,9 +100,10 @@ def test_decode_steps_match_oracle(gpu, bsz, hk, hv):
 def test_extend_matches_oracle(gpu, lens, hk, hv):
     """Mixed extend lengths against the oracle's per-request loop (chunked WY
     update for ext > 1): two consecutive calls, the second with other lengths.
-    The kernel carries the state token by token; against the chunked form the
-    fp32 state agrees to ~1e-4 relative (allowed: 2e-4 max|S| on all but 1e-3 of
-    the elements)."""
+    The kernel runs the chunked form with 32-token chunks on MFMAs (bf16
+    high/low operand splits, fp32 accumulation); against the oracle's 64-token
+    chunks the fp32 state agrees to ~1e-4 relative (allowed: 2e-4 max|S| on all
+    but 1e-3 of the elements)."""
     print(f"[gdn extend] lens={lens} Hk={hk} Hv={hv}", flush=True)
     n_slots = len(lens) + 3
     conv_dim = 2 * hk * 128 + hv * 128
@@ -165,6 +166,62 @@ def test_out_of_pool_slots_are_skipped(gpu):
     assert torch.equal(cs[keep.to(gpu)], cs0[keep.to(gpu)])
     assert torch.equal(ss[keep.to(gpu)], ss0[keep.to(gpu)])
     assert not torch.equal(ss[2], ss0[2])
+
+
+@pytest.mark.parametrize("lens", [[40, 1, 70], [1, 40, 70]])
+def test_extend_out_of_pool_slots_are_skipped(gpu, lens):
+    """Extend batch with requests on slot -1 and on slot n_slots beside a valid
+    one: the skipped requests touch no conv or SSM slot and their output rows
+    are zeros; the valid request matches the oracle run on it alone."""
+    hk, hv, n_slots = 4, 12, 6
+    conv_dim = 2 * hk * 128 + hv * 128
+    g = torch.Generator().manual_seed(sum(lens))
+    conv_state = torch.randn((n_slots, conv_dim, 3), generator=g).to(torch.bfloat16)
+    ssm_state = torch.randn((n_slots, hv, 128, 128), generator=g) * 0.2
+    params = make_params(hk, hv, 5)
+    cs, ss = conv_state.to(gpu), ssm_state.to(gpu)
+    req = torch.tensor([-1, n_slots, 2], dtype=torch.int64)
+    qkv, a, b, z = make_step(sum(lens), hk, hv, 91)
+    gp = [p.to(gpu) for p in params]
+    # Leave NaNs in the memory the caching allocator hands out next, so rows the
+    # kernels did not write would not read as zeros by chance.
+    poison = torch.full((2, sum(lens), hv * 128), float("nan"), dtype=torch.bfloat16,
+                        device=gpu)
+    del poison
+    got, core = gdn_extend_step(qkv.to(gpu), b.to(gpu), a.to(gpu), z.to(gpu), *gp, 1e-6, cs,
+                                ss, req.to(gpu), lens, hk, hv, return_core=True)
+    torch.cuda.synchronize()
+    keep = torch.ones(n_slots, dtype=torch.bool)
+    keep[2] = False
+    assert torch.equal(cs.cpu()[keep], conv_state[keep]), "skipped: conv slots touched"
+    assert torch.equal(ss.cpu()[keep], ssm_state[keep]), "skipped: ssm slots touched"
+    t0, t1 = lens[0] + lens[1], sum(lens)
+    assert torch.equal(got[:t0].cpu(), torch.zeros((t0, hv * 128), dtype=torch.bfloat16))
+    assert torch.equal(core[:t0].cpu(), torch.zeros((t0, hv * 128), dtype=torch.bfloat16))
+    want_out, want_core = og.gdn_extend(qkv[t0:t1], a[t0:t1], b[t0:t1], z[t0:t1], *params,
+                                        1e-6, conv_state, ssm_state, req[2:], lens[2:], hk, hv)
+    scale = float(ssm_state.abs().max())
+    close_fraction(ss.cpu()[2], ssm_state[2], 2e-4 * scale, 1e-2 * scale, 1e-3,
+                   "valid request: ssm state")
+    assert torch.equal(cs.cpu()[2], conv_state[2]), "valid request: conv state"
+    check_outputs(core[t0:t1].cpu(), want_core, "valid request: pre-norm output")
+    check_outputs(got[t0:t1].cpu(), want_out, "valid request: normed output")
+
+
+def test_decode_out_of_pool_rows_are_zero(gpu):
+    hk, hv, n_slots = 4, 12, 6
+    conv_dim = 2 * hk * 128 + hv * 128
+    cs = torch.randn((n_slots, conv_dim, 3)).to(torch.bfloat16).to(gpu)
+    ss = torch.randn((n_slots, hv, 128, 128), device=gpu)
+    qkv, a, b, z = make_step(3, hk, hv, 8)
+    req = torch.tensor([4, -1, n_slots], dtype=torch.int64, device=gpu)
+    params = [p.to(gpu) for p in make_params(hk, hv, 3)]
+    out, core = gdn_decode_step(qkv.to(gpu), b.to(gpu), a.to(gpu), z.to(gpu), *params, 1e-6,
+                                cs, ss, req, hk, hv, return_core=True)
+    torch.cuda.synchronize()
+    assert torch.equal(out[1:].cpu(), torch.zeros((2, hv * 128), dtype=torch.bfloat16))
+    assert torch.equal(core[1:].cpu(), torch.zeros((2, hv * 128), dtype=torch.bfloat16))
+    assert torch.isfinite(out[0].float()).all()
 
 
 def test_layout_checks(gpu):

@@ -115,7 +115,15 @@ __global__ void __launch_bounds__(kThreads) gdn_recur_kernel(GdnArgs a) {
   const int hk = h / a.vpk;
   const int t = threadIdx.x;
   const int64_t r = a.req[bi];
-  if (r < 0 || r >= a.n_slots) return;   // a slot outside the pool: no work, no output
+  if (r < 0 || r >= a.n_slots) {
+    // A slot outside the pool: no state is read or written and the request's
+    // output row reads as zeros (extend: gdn_norm_ext_kernel writes them).
+    if (!a.tok && t < kDv) {
+      a.out[(int64_t)bi * a.out_rs + h * kDv + t] = 0;
+      if (a.core) a.core[(int64_t)bi * a.core_rs + h * kDv + t] = 0;
+    }
+    return;
+  }
   // Decode: request bi is row bi.  Extend (token offsets given): this kernel
   // takes the requests that extend by exactly one token, at their row.
   int row = bi;
@@ -203,13 +211,15 @@ __global__ void __launch_bounds__(kThreads) gdn_recur_kernel(GdnArgs a) {
 
 // ---------------------------------------------------------------- extend
 // Requests with several new tokens (the reference's per-request loop,
-// linear_attention.py:328-364): the conv walks each request's tokens with a
-// sliding window (one thread per (request, channel), so the channel's conv
-// state is read and written by that thread alone), and the recurrence walks
-// them with the head's state held in registers from the first token to the
-// last (one state read and one write per request and head).  The token
-// recurrence is the reference's chunked WY update (:194-242) computed one
-// token at a time; both are the same linear recurrence.
+// linear_attention.py:328-364): the conv runs over the flattened batch in
+// parallel (kConvTokens rows x kConvCh channels per thread, inputs before a
+// request's first row taken from its conv state, which is shifted afterwards
+// by its own kernel); per 32-token chunk the WY quantities are prepared for all
+// chunks at once; then one workgroup per (request, value head) carries the
+// head's state in MFMA accumulators from the first chunk to the last (one state
+// read and one write per request and head).  This is the reference's chunked
+// WY update (:194-242) with 32-token chunks; the chunk length does not change
+// the result.
 
 constexpr int kConvTokens = 8;    // tokens per thread in the extend conv
 
@@ -240,7 +250,7 @@ __global__ void __launch_bounds__(kThreads) gdn_conv_ext_kernel(GdnArgs a) {
   const int c = kConvCh * (blockIdx.x * kThreads + threadIdx.x);
   const int tb = blockIdx.y * kConvTokens;
   if (tb >= a.rows || c >= a.conv_dim) return;
-  u32x2 x[kConvTokens + 3];   // rows tb - 3 .. tb + 15 (0 outside [0, rows))
+  u32x2 x[kConvTokens + 3];   // rows tb - 3 .. tb + kConvTokens - 1 (0 outside [0, rows))
 #pragma unroll
   for (int i = 0; i < kConvTokens + 3; ++i) {
     const int tt = tb - 3 + i;
@@ -765,20 +775,26 @@ __global__ void __launch_bounds__(kThreads) gdn_chunk_ext_kernel(GdnArgs a) {
 // of it dims 4 l .. 4 l + 3, and the sum of squares is a 32-lane reduction
 // (grid: token rows x blocks of 8 value heads).  Also copies the recurrence
 // output to core_out when asked.  Rows of requests whose slot is outside the
-// pool are left untouched, as in the recurrence; rows of one-token requests
-// were written by gdn_recur_kernel.
+// pool are written as zeros (in out and core_out); rows of other one-token
+// requests were written by gdn_recur_kernel.
 constexpr int kNormHeads = 2 * kThreads / kWave;   // value heads per workgroup
 
 __global__ void __launch_bounds__(kThreads) gdn_norm_ext_kernel(GdnArgs a) {
   const int tok = blockIdx.x;
   const int lane = threadIdx.x & (kWave - 1);
   const int h = blockIdx.y * kNormHeads + 2 * wave_id() + (lane >> 5);
-  const int bo = a.owner[tok];
-  if (bo < 0) return;
-  if (min(max(a.tok[bo + 1], 0), a.rows) - min(max(a.tok[bo], 0), a.rows) == 1)
-    return;   // a one-token request: gdn_recur_kernel wrote its row
   const bool act = h < a.hv;
   const int d = 4 * (lane & 31);
+  const int bo = a.owner[tok];
+  if (bo < 0) {
+    if (act) {
+      *reinterpret_cast<u32x2*>(a.out + tok * a.out_rs + h * kDv + d) = u32x2{0u, 0u};
+      if (a.core) *reinterpret_cast<u32x2*>(a.core + tok * a.core_rs + h * kDv + d) = u32x2{0u, 0u};
+    }
+    return;
+  }
+  if (min(max(a.tok[bo + 1], 0), a.rows) - min(max(a.tok[bo], 0), a.rows) == 1)
+    return;   // a one-token request: gdn_recur_kernel wrote its row
   const int hc = act ? h : 0;
   const u32x2 ob =
       *reinterpret_cast<const u32x2*>(a.wcore + (int64_t)tok * (a.hv * kDv) + hc * kDv + d);
@@ -968,8 +984,6 @@ int32_t tf_gdn_extend(const void* qkv, int64_t qkv_row_stride, const void* a, co
   if (!token_offsets) return fail(TF_ERR_INVALID, "gdn_extend: null token_offsets");
   if (max_extend_len < 0 || max_extend_len > n_tokens)
     return fail(TF_ERR_INVALID, "gdn_extend: max_extend_len=%d", max_extend_len);
-  if (max_extend_len > 65535 * 16)
-    return fail(TF_ERR_UNSUPPORTED, "gdn_extend: max_extend_len=%d too large", max_extend_len);
   if (batch_size > 65535) return fail(TF_ERR_UNSUPPORTED, "gdn_extend: batch_size > 65535");
   GdnArgs g;
   const int32_t rc = gdn_setup(
