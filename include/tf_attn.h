@@ -150,6 +150,33 @@ int32_t tf_attn_decode_merge(const void* q, int64_t q_row_stride,
                              const void* gate, int64_t gate_row_stride, int64_t gate_head_stride,
                              tf_stream_t stream);
 
+/* tf_attn_decode_noalloc: no counterpart in the reference.  For callers that
+ * cannot allocate device memory (code under HIP graph capture, tight serving
+ * loops, harnesses that forbid hipMalloc): tf_attn_decode with the same
+ * arguments minus the workspace, whose split partials live instead in a
+ * library-owned static device array of 32 MiB per GPU (held from library load
+ * until the process ends).  It allocates nothing and calls no allocating
+ * routine.  Returns TF_ERR_UNSUPPORTED when tf_attn_decode_workspace_bytes()
+ * of the same arguments exceeds 32 MiB (e.g. more than ~1700 (request, kv
+ * head) units with one workgroup per CU).  Every call on one GPU uses that
+ * GPU's single array: calls that overlap in time on one GPU (several streams,
+ * several threads) race and must be serialised by the caller.  The stream must
+ * belong to the current device.  Results are bit-identical to tf_attn_decode.
+ */
+int32_t tf_attn_decode_noalloc(const void* q, int64_t q_row_stride,
+                               const void* k_pool, const void* v_pool, int64_t pool_slots,
+                               int32_t kv_dtype, const float* k_scale, const float* v_scale,
+                               const int64_t* req_to_token, int64_t rtt_rows,
+                               int64_t rtt_row_stride, int64_t rtt_cols,
+                               const int64_t* req_pool_indices, const int64_t* seq_lens,
+                               int32_t seq_len_override,
+                               const int32_t* items, const int32_t* q_rows, int32_t n_items,
+                               int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
+                               float scale, void* out, int64_t out_row_stride,
+                               int32_t max_seq_len, int32_t num_workgroups,
+                               const void* gate, int64_t gate_row_stride,
+                               int64_t gate_head_stride, tf_stream_t stream);
+
 /* ------------------------------------------------------------------ extend
  * Causal prefill / extend attention over cached prefix + new tokens, bf16
  * MFMA, flash-style.  Replaces the extend / mixed branch,

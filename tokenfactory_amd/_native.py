@@ -47,6 +47,18 @@ SIGNATURES = {
         _p, _i64, _i64,                # gate, gate_row_stride, gate_head_stride
         _p,                            # stream
     ]),
+    "tf_attn_decode_noalloc": (_i32, [
+        _p, _i64,                      # q, q_row_stride
+        _p, _p, _i64, _i32, _p, _p,    # k_pool, v_pool, pool_slots, kv_dtype, k_scale, v_scale
+        _p, _i64, _i64, _i64,          # req_to_token, rtt_rows, rtt_row_stride, rtt_cols
+        _p, _p, _i32,                  # req_pool_indices, seq_lens, seq_len_override
+        _p, _p, _i32,                  # items, q_rows, n_items
+        _i32, _i32, _i32, _f32,        # num_q_heads, num_kv_heads, head_dim, scale
+        _p, _i64,                      # out, out_row_stride
+        _i32, _i32,                    # max_seq_len, num_workgroups
+        _p, _i64, _i64,                # gate, gate_row_stride, gate_head_stride
+        _p,                            # stream
+    ]),
     "tf_attn_decode_partial": None,   # same signature as tf_attn_decode
     "tf_attn_decode_merge": None,
     "tf_attn_extend": (_i32, [

@@ -805,3 +805,83 @@ int32_t tf_attn_decode_merge(TF_DECODE_PARAMS) {
 }
 
 }  // extern "C"
+
+// ------------------------------------------------------------ no-allocation decode
+// tf_attn_decode for callers that cannot allocate device memory: the split
+// partials live in this library-owned array instead of a caller workspace.
+// Every GPU the library runs on holds its own copy from module load until the
+// process ends; all calls on one GPU share it (the partials need no
+// initialisation: every one the merge reads was written earlier in the same
+// call), so calls that overlap in time on one GPU race.
+static constexpr int64_t kNoAllocScratchBytes = 32LL << 20;
+static __device__ __align__(256) uint8_t scratch[kNoAllocScratchBytes];
+
+namespace tfa {
+namespace {
+
+constexpr int kMaxDevices = 64;
+
+// The device address of `scratch` on the current device, looked up once per
+// device (the host-side name is only a handle for the lookup; passing it to a
+// kernel would fault).
+int noalloc_scratch(hipStream_t stream, void** ptr) {
+  static std::mutex mu;
+  static void* cache[kMaxDevices];
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return fail(TF_ERR_HIP, "decode_noalloc: hipGetDevice: %s",
+                                   hipGetErrorString(e));
+  if (dev < 0 || dev >= kMaxDevices)
+    return fail(TF_ERR_UNSUPPORTED, "decode_noalloc: device %d", dev);
+  if (stream) {
+    hipDevice_t sdev = -1;
+    e = hipStreamGetDevice(stream, &sdev);
+    if (e != hipSuccess)
+      return fail(TF_ERR_HIP, "decode_noalloc: hipStreamGetDevice: %s", hipGetErrorString(e));
+    if (sdev != dev)
+      return fail(TF_ERR_INVALID, "decode_noalloc: the stream is on device %d, device %d is "
+                  "current (make the stream's device current)", (int)sdev, dev);
+  }
+  std::lock_guard<std::mutex> lock(mu);
+  if (!cache[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p)
+      return fail(TF_ERR_HIP, "decode_noalloc: hipGetSymbolAddress(scratch): %s",
+                  hipGetErrorString(e));
+    cache[dev] = p;
+  }
+  *ptr = cache[dev];
+  return TF_OK;
+}
+
+}  // namespace
+}  // namespace tfa
+
+extern "C" int32_t tf_attn_decode_noalloc(
+    const void* q, int64_t q_row_stride, const void* k_pool, const void* v_pool,
+    int64_t pool_slots, int32_t kv_dtype, const float* k_scale, const float* v_scale,
+    const int64_t* req_to_token, int64_t rtt_rows, int64_t rtt_row_stride, int64_t rtt_cols,
+    const int64_t* req_pool_indices, const int64_t* seq_lens, int32_t seq_len_override,
+    const int32_t* items, const int32_t* q_rows, int32_t n_items, int32_t num_q_heads,
+    int32_t num_kv_heads, int32_t head_dim, float scale, void* out, int64_t out_row_stride,
+    int32_t max_seq_len, int32_t num_workgroups, const void* gate, int64_t gate_row_stride,
+    int64_t gate_head_stride, tf_stream_t stream) {
+  using namespace tfa;
+  clear_error();
+  DecodePlan p;
+  const int rc = make_decode_plan(n_items, num_q_heads, num_kv_heads, head_dim, max_seq_len,
+                                  num_workgroups, &p);
+  if (rc != TF_OK) return rc;
+  if (p.total_bytes > kNoAllocScratchBytes)
+    return fail(TF_ERR_UNSUPPORTED,
+                "decode_noalloc: this call needs %lld bytes of split scratch, the static buffer "
+                "holds %lld (fewer requests or workgroups per call, or tf_attn_decode with a "
+                "workspace)", (long long)p.total_bytes, (long long)kNoAllocScratchBytes);
+  void* ws = nullptr;
+  const int rc2 = noalloc_scratch(reinterpret_cast<hipStream_t>(stream), &ws);
+  if (rc2 != TF_OK) return rc2;
+  void* workspace = ws;
+  const int64_t workspace_bytes = kNoAllocScratchBytes;
+  return decode_launch(TF_DECODE_ARGS, kPhasePartial | kPhaseMerge);
+}
