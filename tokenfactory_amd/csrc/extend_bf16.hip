@@ -76,11 +76,32 @@ constexpr float kRescaleLog2 = 8.f;
 constexpr int kQkAhead = 2;                          // K fragments in flight
 constexpr int kPvAhead = 2;                          // V fragments in flight
 
+// A wave's 32 rows x 256 dims of bf16 (Q on the way in, the output on the
+// way out), row-major with 16-byte chunk c of row r at chunk c ^ r: the
+// row-contiguous global side and the MFMA-fragment side both access it
+// without bank conflicts beyond two-way.
+constexpr int kTileBytes = kRowsPerWave * kRowBytes;   // 16 KB
+
 struct __attribute__((aligned(16))) Smem {
-  uint8_t k[kStages * kKStage];
-  uint8_t v[kVStages * kVStage];
+  union {
+    struct {
+      uint8_t k[kStages * kKStage];
+      uint8_t v[kVStages * kVStage];
+    };
+    uint8_t rows[kWaves][kTileBytes];   // Q in the prologue, the output at the end
+  };
   int32_t slots[2 * kSlotChunk];   // 8 KB: key k's slot id at slots[k % 2048]
 };
+
+__device__ __forceinline__ int swz_chunk(int r, int c) { return (c ^ r) & 31; }
+
+// x through an empty asm: what is computed from it cannot be hoisted out of
+// the block (the epilogue's row arithmetic would otherwise be computed in the
+// prologue and kept, or spilled, across the whole tile loop).
+__device__ __forceinline__ int opaque(int x) {
+  asm volatile("" : "+v"(x));
+  return x;
+}
 
 __device__ __forceinline__ int vswz(int n) { return 10 * (n & 1) + 4 * ((n >> 1) & 1); }
 
@@ -373,15 +394,32 @@ __global__ void __launch_bounds__(kThreads) extend_bf16_kernel(ExtendArgs a) {
     for (int m2 = 0; m2 < 4; ++m2) vaddr[m2] = base + 64 * (m2 ^ (sw >> 2));
   }
 
+  // Q: the wave's 32 rows (padding rows repeat the last real row) are loaded
+  // row-contiguously, lane L taking 16-byte chunk L % 32 of row 2 i + L / 32,
+  // together with the slot ids of the first 1024 keys.
+  uint8_t* const my_rows = sm.rows[w];
+  {
+    u32x4 qv[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int r = 2 * i + g;
+      const int rho = min(row0 + kRowsPerWave * w + r, rows_total - 1);
+      const int t = rho / G, h = rho - t * G;
+      qv[i] = ld_g16(a.q + (int64_t)(q_start + t) * a.q_stride + (int64_t)(hk * G + h) * kD + 8 * n);
+    }
+    slot_issue(rtt, 0, kend, w, lane, sm.slots);
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int r = 2 * i + g;
+      st_s16(my_rows + r * kRowBytes + 16 * swz_chunk(r, n), qv[i]);
+    }
+  }
   // Q^T fragments: lane (g, n) holds q[row n][16 kk + 8 g .. +8].
   u32x4 qf[16];
-  {
-    const int t = rho_c / G, h = rho_c - t * G;
-    const __bf16* qp = a.q + (int64_t)(q_start + t) * a.q_stride + (int64_t)(hk * G + h) * kD;
 #pragma unroll
-    for (int kk = 0; kk < 16; ++kk) qf[kk] = ld_g16(qp + 16 * kk + 8 * g);
-  }
-  // Consume Q here so that the compiler waits for these loads before the
+  for (int kk = 0; kk < 16; ++kk)
+    qf[kk] = ld_s16(my_rows + n * kRowBytes + 16 * swz_chunk(n, 2 * kk + g));
+  // Consume Q here so that the compiler waits for these reads before the
   // loop; inside it, vmcnt belongs to the staging loads.
 #pragma unroll
   for (int kk = 0; kk < 16; ++kk) asm volatile("" ::"v"(qf[kk]));
@@ -391,11 +429,10 @@ __global__ void __launch_bounds__(kThreads) extend_bf16_kernel(ExtendArgs a) {
 #pragma unroll
   for (int i = 0; i < 8; ++i) acc[i] = f32x16{};
 
-  // ---- prologue: slot ids of the first 1024 keys, then tiles 0 and 1 into
-  // stages 0 and 1. Tiles past the last one are stand-ins for the last tile
-  // (its slots are staged, so every load stays inside the pool) and are never
-  // read.
-  slot_issue(rtt, 0, kend, w, lane, sm.slots);
+  // ---- prologue: the slot ids (issued with Q) land, every wave has its Q
+  // out of the shared rows, then tiles 0 and 1 go into stages 0 and 1. Tiles
+  // past the last one are stand-ins for the last tile (its slots are staged,
+  // so every load stays inside the pool) and are never read.
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
 #pragma unroll
@@ -473,31 +510,43 @@ __global__ void __launch_bounds__(kThreads) extend_bf16_kernel(ExtendArgs a) {
     rescale();
     pv_phase<false>(sm.v + (last % kVStages) * kVStage, vaddr, acc, pt, st);
   }
-  // The last steps staged stand-in tiles nobody reads; they must land before
-  // the workgroup's LDS can be handed to another workgroup.
+  // The last steps staged stand-in tiles nobody reads; they must land (and
+  // every wave must be done with the stages) before the stage memory holds
+  // the output rows.
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
 
-  const float lt = row.l + __shfl_xor(row.l, 32, kWave);
-  const int rho = row0 + kRowsPerWave * w + n;
-  if (rho >= rows_total) return;
-  const int t = rho / G, h = rho - t * G;
-  const float inv = 1.f / lt;
-  __bf16* o = a.out + (int64_t)(q_start + t) * a.out_stride + (int64_t)(hk * G + h) * kD;
-  const __bf16* gt = a.gate ? a.gate + (int64_t)(q_start + t) * a.gate_stride +
-                                  (int64_t)(hk * G + h) * a.gate_hstride
-                            : nullptr;
+  // Output: O^T / l into the wave's rows in LDS (lane (g, n) holds dims
+  // 32 mt + 8 rq + 4 g .. +3 of row n), then row-contiguous 16-byte stores
+  // (with the output gate), lane L writing chunk L % 32 of row 2 i + L / 32.
+  const float inv = 1.f / (row.l + __shfl_xor(row.l, 32, kWave));
+  const int ln = opaque(lane);   // lane coordinates recomputed here, see opaque()
+  const int ne = ln & 31, ge = ln >> 5;
 #pragma unroll
   for (int mt = 0; mt < 8; ++mt) {
 #pragma unroll
     for (int rq = 0; rq < 4; ++rq) {
-      const int off = 32 * mt + 8 * rq + 4 * g;
-      u32x2 v = {pack_bf16(acc[mt][4 * rq + 0] * inv, acc[mt][4 * rq + 1] * inv),
-                 pack_bf16(acc[mt][4 * rq + 2] * inv, acc[mt][4 * rq + 3] * inv)};
-      if (gt) {
-        const u32x2 gv = ld_g8(gt + off);
-        v = u32x2{gate_pair(v[0], gv[0]), gate_pair(v[1], gv[1])};
+      const u32x2 v = {pack_bf16(acc[mt][4 * rq + 0] * inv, acc[mt][4 * rq + 1] * inv),
+                       pack_bf16(acc[mt][4 * rq + 2] * inv, acc[mt][4 * rq + 3] * inv)};
+      st_s8(my_rows + ne * kRowBytes + 16 * swz_chunk(ne, 4 * mt + rq) + 8 * ge, v);
+    }
+  }
+  const int rho0 = row0 + kRowsPerWave * w + ge;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const int r = 2 * i + ge;
+    const int rho = rho0 + 2 * i;
+    if (rho < rows_total) {
+      u32x4 v = ld_s16(my_rows + r * kRowBytes + 16 * swz_chunk(r, ne));
+      const int t = rho / G, h = rho - t * G;
+      if (a.gate) {
+        const u32x4 gv = ld_g16(a.gate + (int64_t)(q_start + t) * a.gate_stride +
+                                (int64_t)(hk * G + h) * a.gate_hstride + 8 * ne);
+#pragma unroll
+        for (int k = 0; k < 4; ++k) v[k] = gate_pair(v[k], gv[k]);
       }
-      *reinterpret_cast<u32x2*>(o + off) = v;
+      *reinterpret_cast<u32x4*>(a.out + (int64_t)(q_start + t) * a.out_stride +
+                                (int64_t)(hk * G + h) * kD + 8 * ne) = v;
     }
   }
 }
