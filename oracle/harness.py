@@ -28,16 +28,30 @@ class HostBatch:
             setattr(self, name, None if t is None else t.cpu())
 
 
+def pool_rows(entries, pool_slots, single):
+    """The pool row each ``req_to_token`` entry reads: the batched branches
+    clamp negative entries to slot 0 (``full_attention.py:217-219``); the
+    ``bsz == 1`` branch indexes the pool directly (``:188-190``), so an entry
+    ``-S <= v < 0`` reads slot ``S + v`` as torch indexing does.  Entries the
+    reference would reject (past the pool, or below ``-S``) are clamped into
+    the pool, as the kernels do."""
+    if single:
+        entries = torch.where(entries < 0, entries + pool_slots, entries)
+    return entries.clamp(0, pool_slots - 1)
+
+
 def compact_pools(wl):
-    """(k_rows, v_rows, req_to_token) restricted to the slots the batch reads."""
+    """(k_rows, v_rows, req_to_token) restricted to the slots the batch reads;
+    the returned table indexes the compacted rows (no negative entries)."""
     b = wl.batch
     width = b.max_seq_len
     sub = b.req_to_token[b.req_pool_indices, :width]
-    used, inv = torch.unique(sub.clamp(min=0), return_inverse=True)
+    rows = pool_rows(sub, wl.k_pool.shape[0], b.batch_size == 1)
+    used, inv = torch.unique(rows, return_inverse=True)
     kp = wl.k_pool[used].cpu()
     vp = wl.v_pool[used].cpu()
     rtt = torch.full((b.batch_size, width + 1), -1, dtype=torch.long)
-    rtt[:, :width] = torch.where(sub >= 0, inv, torch.full_like(inv, -1)).cpu()
+    rtt[:, :width] = inv.cpu()
     return kp, vp, rtt
 
 

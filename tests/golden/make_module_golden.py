@@ -34,6 +34,8 @@ def bits(t):
 
 
 def main(ref_root: str) -> None:
+    # The reference tree is read-only: importing it must not write bytecode there.
+    sys.dont_write_bytecode = True
     sys.path.insert(0, ref_root)
     from qwen3_8.config import Qwen3_8Config
     from qwen3_8.forward_batch import ForwardBatch

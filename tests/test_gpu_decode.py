@@ -146,3 +146,16 @@ def test_full_size_decode_b64_sampled(gpu):
     # the workgroups; only fp32 summation order may differ.
     assert_attn_close(run(sub), out[pick], atol=4e-3, rtol=4e-3, norm_rel=4e-3,
                       what="batch composition")
+
+
+@pytest.mark.parametrize("bsz", [1, 3])
+def test_negative_slot_entries(gpu, bsz):
+    """A -1 inside a request's req_to_token row: the bsz == 1 branch reads the
+    pool's last slot (torch indexing, full_attention.py:188-190), the batched
+    branch slot 0 (clamp, :217-219); the oracle follows the same rules."""
+    lens = [300, 77, 1000][:bsz]
+    wl = small_case(lens, [1] * bsz, hq=24, hkv=4, d=256, seed=40 + bsz, device=gpu,
+                    dtype=torch.bfloat16, q_std=3.0)
+    for b in range(bsz):
+        wl.batch.req_to_token[wl.rows[b], [5, lens[b] // 2]] = -1
+    check(wl, 0, what=f"-1 entries, bsz={bsz}")

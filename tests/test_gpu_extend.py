@@ -115,3 +115,13 @@ def test_full_size_extend_prefix_sampled(gpu):
                   rows=[wl.rows[i] for i in pick])
     want = torch.cat([out[starts[i]:starts[i + 1]] for i in pick])
     assert_attn_close(want, restatement(sub), what="extend full-size sample")
+
+
+@pytest.mark.parametrize("fp8", [False, True])
+def test_negative_slot_entries_bsz1(gpu, fp8):
+    """bsz == 1 extend over a row with -1 entries reads the pool's last slot
+    there (full_attention.py:188-190), as the oracle does."""
+    wl = workloads.build("neg", [400], [120], num_q_heads=24, num_kv_heads=4, head_dim=256,
+                         pool_slots=1024, device=gpu, seed=44, kv_fp8=fp8)
+    wl.batch.req_to_token[wl.rows[0], [0, 150, 300]] = -1
+    check(wl, "-1 entries, bsz=1" + (", fp8" if fp8 else ""))

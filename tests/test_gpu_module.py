@@ -105,3 +105,82 @@ def test_full_attention_fp8_projections(gpu, monkeypatch):
         ref, _, _ = ofl.block_fp8_linear(x.cpu(), lin.weight.cpu(), lin.weight_scale_inv.cpu())
         rms = float(ref.pow(2).mean().sqrt())
         assert torch.allclose(got.cpu().float(), ref, atol=2e-2 * rms, rtol=1e-2), name
+
+
+@pytest.mark.parametrize("name", mg.CASES)
+def test_full_attention_on_fp8_kv_pool(gpu, name, monkeypatch):
+    """``FullAttnKVPool.from_config`` with an fp8-e4m3 pool driving
+    ``FullAttention.forward`` (the per-layer ``get_full_kv_scales`` path):
+
+    * the pool is filled with the golden pool's rows through ``write_kv``
+      (quantise-on-write): every dequantised value within half an e4m3 step
+      (2^-4 relative, or 2^-10 scaled below the normal range) of the input;
+    * the K / V rows the forward writes quantise the reference module's
+      written K / V the same way;
+    * the attention the module computes equals the oracle's attention over the
+      same dequantised pool (bf16 tolerance: 2e-2 + 1e-2 |ref|, rel-norm 1e-2).
+    """
+    from oracle.harness import reference_attention
+    from oracle.kv_quant import dequantize_e4m3
+    from tokenfactory_amd import workloads
+    from tokenfactory_amd.kv_pool import FullAttnKVPool
+
+    d, meta = mg.load()
+    cfg = mg.config(meta)
+    cfg.layer_types = ["linear_attention"] * 3 + ["full_attention"] + ["linear_attention"] * 3 + \
+        ["full_attention"]
+    S = meta["pool_slots"]
+    pool = FullAttnKVPool.from_config(cfg, S, device=gpu, dtype=torch.float8_e4m3fn)
+    assert pool.full_layer_map == {3: 0, 7: 1} and pool.is_fp8
+    assert pool.k_buffer.shape == (2, S, cfg.num_key_value_heads, cfg.head_dim)
+    kf = mg.bf16(d["k_pool0"]).to(gpu)
+    vf = mg.bf16(d["v_pool0"]).to(gpu)
+    ks, vs = float(kf.abs().max()) / 448.0, float(vf.abs().max()) / 448.0
+    pool.set_kv_scales(3, ks, vs)
+    pool.write_kv(3, torch.arange(S, device=gpu), kf.to(torch.bfloat16), vf.to(torch.bfloat16))
+
+    def within_e4m3_step(deq, x, scale, what):
+        bound = torch.maximum(x.abs() * 2.0 ** -4, torch.full_like(x, scale * 2.0 ** -10))
+        assert ((deq - x).abs() <= bound * 1.0001).all(), what
+
+    kb, vb = pool.get_full_kv_buffers(3)
+    k_sc, v_sc = pool.get_full_kv_scales(3)
+    assert float(k_sc) == pytest.approx(ks) and float(v_sc) == pytest.approx(vs)
+    within_e4m3_step(dequantize_e4m3(kb.cpu(), ks), kf.cpu(), ks, "pool K")
+    within_e4m3_step(dequantize_e4m3(vb.cpu(), vs), vf.cpu(), vs, "pool V")
+
+    mod = FullAttention(cfg, layer_idx=3, dtype=torch.bfloat16).to(gpu)
+    mg.load_weights(mod, d)
+    captured = {}
+    inner = fa.slot_based_attention
+
+    def spy(q, k_buf, v_buf, batch, *, gate=None, **kw):
+        captured["q"] = q.clone()
+        captured["attn"] = inner(q, k_buf, v_buf, batch, **kw).clone()
+        return inner(q, k_buf, v_buf, batch, gate=gate, **kw)
+
+    monkeypatch.setattr(fa, "slot_based_attention", spy)
+    batch = mg.batch(d, meta, name, gpu)
+    hidden = mg.bf16(d[f"{name}_hidden"]).to(device=gpu, dtype=torch.bfloat16)
+    pos = torch.from_numpy(d[f"{name}_positions"]).to(gpu)
+    print(f"[module fp8 pool] case={name}", flush=True)
+    with torch.no_grad():
+        out = mod(hidden, pos, pool, batch)
+    torch.cuda.synchronize()
+    assert torch.isfinite(out.float()).all()
+    loc = torch.from_numpy(d[f"{name}_out_cache_loc"])
+    for what, buf, sc in (("k_written", kb, ks), ("v_written", vb, vs)):
+        # the write saturates at +-448 x scale (the scale came from the pool
+        # before this step); the module's bf16 K differs from the fp32
+        # reference by ~2^-8, on top of the quantisation step
+        want = mg.expected(d, name, what).clamp(-448.0 * sc, 448.0 * sc)
+        deq = dequantize_e4m3(buf.cpu()[loc], sc)
+        bound = want.abs() * (2.0 ** -4 + 2.0 ** -7) + sc * 2.0 ** -9 + 1e-2
+        assert ((deq - want).abs() <= bound).all(), f"{name} {what}"
+    c = meta["cases"][name]
+    wl = workloads.Workload(
+        name=name, q=captured["q"], k_pool=kb, v_pool=vb, batch=batch, seq_lens=list(c["seq"]),
+        ext_lens=list(c["ext"]), rows=list(c["req"]), num_q_heads=cfg.num_attention_heads,
+        num_kv_heads=cfg.num_key_value_heads, head_dim=cfg.head_dim, scale=mod.scaling,
+        k_scale=k_sc, v_scale=v_sc)
+    assert_attn_close(captured["attn"], reference_attention(wl), what=f"{name} fp8-pool attention")

@@ -267,6 +267,28 @@ def test_gather_ref_matches_explicit_loops_and_clamps_padding():
             np.testing.assert_array_equal(got[b, t], want)
 
 
+@pytest.mark.parametrize("entry", [-1, -3])
+def test_negative_slot_ids_follow_each_branch(entry):
+    """A negative req_to_token entry v: the bsz == 1 branch indexes the pool
+    directly, reading slot S + v (torch indexing, full_attention.py:188-190);
+    the batched branches clamp it to slot 0 (:217-219).  With one visible key
+    the output is exactly that key's V row (G = 2 heads per kv head)."""
+    S = 40
+    one = small_case([1], [1], hq=4, hkv=2, d=8, seed=21, pool=S)
+    one.batch.req_to_token[one.rows[0], 0] = entry
+    got = restatement(one)
+    want = one.v_pool[S + entry].repeat_interleave(2, dim=0)
+    torch.testing.assert_close(got[0], want, rtol=0, atol=0)
+    two = small_case([1, 1], [1, 1], hq=4, hkv=2, d=8, seed=22, pool=S)
+    two.batch.req_to_token[two.rows[0], 0] = entry
+    got = restatement(two)
+    torch.testing.assert_close(got[0], two.v_pool[0].repeat_interleave(2, dim=0), rtol=0,
+                               atol=0)
+    slot = int(two.batch.req_to_token[two.rows[1], 0])
+    torch.testing.assert_close(got[1], two.v_pool[slot].repeat_interleave(2, dim=0), rtol=0,
+                               atol=0)
+
+
 def test_forward_batch_defaults_follow_reference_rules():
     from tokenfactory_amd import ForwardBatch
     fb = ForwardBatch(batch_size=2, req_pool_indices=torch.tensor([3, 1]),

@@ -293,6 +293,11 @@ class SlotAttentionCall:
             # Pure decode: batch entry b is query row b; nothing to upload.
             self.n_dec = bsz
         else:
+            if torch.cuda.is_current_stream_capturing():
+                # The host plan reaches the device through a reused pinned
+                # staging slot: a captured copy would replay stale plans.
+                raise RuntimeError("a host-planned extend step cannot be captured in a graph; "
+                                   "build the call with device_plan=True")
             work = plan_extend(ext_lens, n_q, n_kv, decode_to_decode_kernel=True)
             items, rows = plan_decode_items(ext_lens)
             self.n_work, self.n_dec = len(work), len(items)

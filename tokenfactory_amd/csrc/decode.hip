@@ -461,7 +461,7 @@ decode_kernel(DecodeArgs a) {
       // ---- stage the slot ids (and, once per segment, the Q^T fragments)
       __syncthreads();
       for (int i = tid; i < n_loc; i += kWaves * kWave)
-        sm.u.loop.slots[i] = (int32_t)clamp_i64(rtt[c0 + i], 0, a.pool_slots - 1);
+        sm.u.loop.slots[i] = (int32_t)pool_row(rtt[c0 + i], a.pool_slots, a.seq_override > 0);
       if (sub == t0 && w == 0) {
         const __bf16* qp = a.q + (int64_t)qrow * a.q_stride + (int64_t)hq * kD;
 #pragma unroll

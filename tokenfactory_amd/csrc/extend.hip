@@ -173,11 +173,11 @@ __device__ __forceinline__ void slot_load(const int64_t* rtt, int chunk, int ken
 }
 
 __device__ __forceinline__ void slot_store(const SlotPrefetch& p, int chunk, int tid,
-                                           int64_t pool_slots, int32_t* slots) {
+                                           int64_t pool_slots, bool wrap, int32_t* slots) {
   int32_t* buf = slots + (chunk & 1) * kSlotChunk;
 #pragma unroll
   for (int i = 0; i < kSlotChunk / kThreads; ++i)
-    buf[tid + i * kThreads] = (int32_t)clamp_i64(p.v[i], 0, pool_slots - 1);
+    buf[tid + i * kThreads] = (int32_t)pool_row(p.v[i], pool_slots, wrap);
 }
 
 // S^T (64 keys x 32 rows) = K_tile Q^T: s[hh][r] is key 32 hh + 8 (r / 4) + 4 g + r % 4.
@@ -488,7 +488,7 @@ extend_kernel(ExtendArgs a) {
   // slots are staged, so every load stays inside the pool) and are never read.
   SlotPrefetch spf;
   slot_load(rtt, 0, kend, tid, spf);
-  slot_store(spf, 0, tid, a.pool_slots, sm.slots);
+  slot_store(spf, 0, tid, a.pool_slots, a.seq_override > 0, sm.slots);
   __syncthreads();
   const int last = n_tiles - 1;
   TileRegs<FP8> regs;
@@ -518,7 +518,7 @@ extend_kernel(ExtendArgs a) {
     if ((j / kTilesPerSlotChunk + 1) * kSlotChunk < kend) {
       if (j % kTilesPerSlotChunk == 4) slot_load(rtt, j / kTilesPerSlotChunk + 1, kend, tid, spf);
       if (j % kTilesPerSlotChunk == 8)
-        slot_store(spf, j / kTilesPerSlotChunk + 1, tid, a.pool_slots, sm.slots);
+        slot_store(spf, j / kTilesPerSlotChunk + 1, tid, a.pool_slots, a.seq_override > 0, sm.slots);
     }
     const int k0 = j * kBN;
     if (k0 + kBN > w_full) mask_tile(sa, k0, g, limit);
@@ -591,7 +591,8 @@ extern "C" int32_t tf_attn_extend(const void* q, int64_t q_row_stride, const voi
     return fail(TF_ERR_INVALID, "extend: seq_lens is null and no override");
   if (kv_dtype == TF_DTYPE_FP8_E4M3 && (!k_scale || !v_scale))
     return fail(TF_ERR_INVALID, "extend: fp8 pool needs k_scale and v_scale");
-  if (pool_slots < 1 || rtt_rows < 1 || rtt_cols < 1 || rtt_row_stride < rtt_cols)
+  if (pool_slots < 1 || pool_slots > INT32_MAX || rtt_rows < 1 || rtt_cols < 1 ||
+      rtt_row_stride < rtt_cols)
     return fail(TF_ERR_INVALID, "extend: bad pool/req_to_token extents");
   if (!aligned16(q) || !aligned16(out) || !aligned16(k_pool) || !aligned16(v_pool) ||
       (q_row_stride * 2) % 16 || (out_row_stride * 2) % 16 || !aligned16(work))

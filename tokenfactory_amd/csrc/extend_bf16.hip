@@ -167,6 +167,7 @@ struct Stager {
   uint8_t* v_dst;
   uint32_t slot_bytes;
   int32_t smax;
+  bool wrap;     // bsz == 1 call: negative slot ids index from the pool's end
   int tile;
   int w;
   int g;
@@ -177,6 +178,7 @@ struct Stager {
   // Row `slot` of K and V: one 32 x 32 -> 64-bit multiply-add per address
   // (slot ids and the slot stride fit 32 bits).
   __device__ __forceinline__ void issue(int32_t sl, int p) const {
+    if (wrap && sl < 0) sl += smax + 1;
     const uint64_t off = (uint64_t)(uint32_t)min(max(sl, 0), smax) * slot_bytes;
     dma16(sb.k + off, lds_addr(k_dst + (2 * w + p) * kKPair));
     dma16(sb.v[p & 1] + off, lds_addr(v_dst + (4 * w + 2 * p) * kRowBytes));
@@ -373,6 +375,7 @@ __global__ void __launch_bounds__(kThreads) extend_bf16_kernel(ExtendArgs a) {
   st.slots = sm.slots;
   st.slot_bytes = (uint32_t)a.hkv * kRowBytes;
   st.smax = (int32_t)min(a.pool_slots - 1, (int64_t)INT32_MAX);
+  st.wrap = a.seq_override > 0;
   st.w = w;
   st.g = g;
   auto stage_for = [&](int j) {

@@ -132,4 +132,15 @@ __device__ __forceinline__ int64_t clamp_i64(int64_t v, int64_t lo, int64_t hi) 
   return v < lo ? lo : (v > hi ? hi : v);
 }
 
+// The pool row a req_to_token entry `v` reads.  The reference's batched
+// branches clamp (`.clamp(min=0)`, full_attention.py:217-219), so a negative
+// entry reads slot 0; its bsz == 1 branch indexes the pool directly (:188-190),
+// where a negative entry v >= -S reads slot S + v as torch indexing does
+// (`wrap`).  Anything else outside the pool is clamped into it, so no entry
+// can address memory outside the pool (the reference raises there).
+__device__ __forceinline__ int64_t pool_row(int64_t v, int64_t pool_slots, bool wrap) {
+  if (wrap && v < 0) v += pool_slots;
+  return clamp_i64(v, 0, pool_slots - 1);
+}
+
 }  // namespace tfa

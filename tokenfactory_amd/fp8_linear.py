@@ -15,6 +15,7 @@ There is no non-native path: without the library every call raises.
 """
 from __future__ import annotations
 
+import contextlib
 import math
 from typing import Optional, Sequence
 
@@ -33,6 +34,14 @@ def _ptr(t: Optional[torch.Tensor]) -> int:
 def _stream_ptr(stream, device) -> int:
     s = stream if stream is not None else torch.cuda.current_stream(device)
     return s.cuda_stream
+
+
+def on_stream(stream):
+    """Context that makes ``stream`` current (a no-op for None), so that the
+    temporaries a call allocates and the torch ops it runs are ordered on the
+    stream its kernels run on, and the caching allocator reuses their memory
+    only after that stream is done with it."""
+    return torch.cuda.stream(stream) if stream is not None else contextlib.nullcontext()
 
 
 K_SLICE = 128   # the GEMM's K granularity (one weight-scale block)
@@ -65,15 +74,16 @@ def quantize_activations(x2d: torch.Tensor, stream=None, padded_cols: Optional[i
     width = cols if padded_cols is None else padded_cols
     if width < cols:
         raise ValueError("quantize_activations: padded_cols < cols")
-    xq = torch.empty((rows, width), dtype=torch.float8_e4m3fn, device=x2d.device)
-    if width > cols:
-        xq.view(torch.uint8)[:, cols:].zero_()
-    scale = torch.empty((1,), dtype=torch.float32, device=x2d.device)
-    ws = torch.empty((_native.TF_FP8_QUANT_WORKSPACE_BYTES,), dtype=torch.uint8,
-                     device=x2d.device)
-    _native.call("tf_fp8_act_quant", _ptr(x2d), _native.TF_DTYPE_BF16, rows, cols,
-                 x2d.stride(0), _ptr(xq), xq.stride(0), _ptr(scale), _ptr(ws), ws.numel(),
-                 _stream_ptr(stream, x2d.device))
+    with on_stream(stream):
+        xq = torch.empty((rows, width), dtype=torch.float8_e4m3fn, device=x2d.device)
+        if width > cols:
+            xq.view(torch.uint8)[:, cols:].zero_()
+        scale = torch.empty((1,), dtype=torch.float32, device=x2d.device)
+        ws = torch.empty((_native.TF_FP8_QUANT_WORKSPACE_BYTES,), dtype=torch.uint8,
+                         device=x2d.device)
+        _native.call("tf_fp8_act_quant", _ptr(x2d), _native.TF_DTYPE_BF16, rows, cols,
+                     x2d.stride(0), _ptr(xq), xq.stride(0), _ptr(scale), _ptr(ws), ws.numel(),
+                     _stream_ptr(stream, x2d.device))
     return xq, scale
 
 
@@ -111,25 +121,27 @@ def block_fp8_gemm(xq: torch.Tensor, x_scale: torch.Tensor, weight: torch.Tensor
         raise ValueError("block_fp8_gemm: bias must be a contiguous bf16 [out_features]")
     if x_scale.dtype != torch.float32 or x_scale.numel() != 1:
         raise ValueError("block_fp8_gemm: x_scale must be a 1-element float32 tensor")
-    if out is None:
-        out = torch.empty((m, n), dtype=torch.bfloat16, device=xq.device)
-    elif out.dtype != torch.bfloat16 or tuple(out.shape) != (m, n) or out.stride(1) != 1:
+    if out is not None and (out.dtype != torch.bfloat16 or tuple(out.shape) != (m, n)
+                            or out.stride(1) != 1):
         raise ValueError("block_fp8_gemm: out must be bf16 [m, n] with contiguous rows")
-    ws = weight_scale_inv
-    if kp != k:
-        xq, weight = _pad_cols(xq, kp), _pad_cols(weight, kp)
-        if ws is None:        # one all-ones block over the true K (fp8_triton.py:132-135)
-            block_w = kp
     # split-K scratch for small m (0 bytes when the call does not split)
     nbytes = _native.load().tf_fp8_block_gemm_workspace_bytes(m, n, kp) if m > 0 else 0
     if nbytes < 0:
         raise ValueError("block_fp8_gemm: bad shape")
-    scratch = torch.empty((nbytes,), dtype=torch.uint8, device=xq.device) if nbytes else None
-    _native.call("tf_fp8_block_gemm", _ptr(xq), xq.stride(0), _ptr(x_scale),
-                 _ptr(weight), weight.stride(0), _ptr(ws),
-                 0 if ws is None else ws.stride(0), 0 if ws is None else ws.stride(1),
-                 block_h, block_w, _ptr(bias), m, n, kp, _ptr(out), out.stride(0),
-                 _ptr(scratch), nbytes, _stream_ptr(stream, xq.device))
+    with on_stream(stream):
+        if out is None:
+            out = torch.empty((m, n), dtype=torch.bfloat16, device=xq.device)
+        ws = weight_scale_inv
+        if kp != k:
+            xq, weight = _pad_cols(xq, kp), _pad_cols(weight, kp)
+            if ws is None:        # one all-ones block over the true K (fp8_triton.py:132-135)
+                block_w = kp
+        scratch = torch.empty((nbytes,), dtype=torch.uint8, device=xq.device) if nbytes else None
+        _native.call("tf_fp8_block_gemm", _ptr(xq), xq.stride(0), _ptr(x_scale),
+                     _ptr(weight), weight.stride(0), _ptr(ws),
+                     0 if ws is None else ws.stride(0), 0 if ws is None else ws.stride(1),
+                     block_h, block_w, _ptr(bias), m, n, kp, _ptr(out), out.stride(0),
+                     _ptr(scratch), nbytes, _stream_ptr(stream, xq.device))
     return out
 
 

@@ -24,7 +24,7 @@ import torch
 import torch.nn as nn
 
 from . import _native
-from .fp8_linear import Fp8Linear
+from .fp8_linear import Fp8Linear, on_stream
 
 HEAD_DIM = 128
 CONV_KERNEL = 4
@@ -84,18 +84,19 @@ def gdn_decode_step(qkv: torch.Tensor, b: torch.Tensor, a: torch.Tensor, z: torc
     _check_common(qkv, b, a, z, conv_weight, a_log, dt_bias, norm_weight, layer_conv_state,
                   layer_ssm_state, req_indices, num_v_heads)
     cs, ss = layer_conv_state, layer_ssm_state
-    out = torch.empty((bsz, value_dim), dtype=torch.bfloat16, device=qkv.device)
-    core = torch.empty_like(out) if return_core else None
-    ws = torch.empty((bsz, 2 * num_k_heads * HEAD_DIM + value_dim), dtype=torch.bfloat16,
-                     device=qkv.device)
     s = stream if stream is not None else torch.cuda.current_stream(qkv.device)
-    _native.call("tf_gdn_decode", _ptr(qkv), _rows(qkv, "qkv"), _ptr(a), _ptr(b),
-                 _rows(a, "a"), _ptr(z), _rows(z, "z"), _ptr(conv_weight), _ptr(a_log),
-                 _ptr(dt_bias), _ptr(norm_weight), float(eps), _ptr(cs), cs.stride(0), _ptr(ss),
-                 ss.stride(0), _ptr(req_indices), bsz, cs.shape[0], num_k_heads, num_v_heads,
-                 HEAD_DIM, HEAD_DIM, CONV_KERNEL, _ptr(out), out.stride(0), _ptr(core),
-                 0 if core is None else core.stride(0), _ptr(ws), ws.numel() * 2,
-                 s.cuda_stream)
+    with on_stream(stream):
+        out = torch.empty((bsz, value_dim), dtype=torch.bfloat16, device=qkv.device)
+        core = torch.empty_like(out) if return_core else None
+        ws = torch.empty((bsz, 2 * num_k_heads * HEAD_DIM + value_dim), dtype=torch.bfloat16,
+                         device=qkv.device)
+        _native.call("tf_gdn_decode", _ptr(qkv), _rows(qkv, "qkv"), _ptr(a), _ptr(b),
+                     _rows(a, "a"), _ptr(z), _rows(z, "z"), _ptr(conv_weight), _ptr(a_log),
+                     _ptr(dt_bias), _ptr(norm_weight), float(eps), _ptr(cs), cs.stride(0),
+                     _ptr(ss), ss.stride(0), _ptr(req_indices), bsz, cs.shape[0], num_k_heads,
+                     num_v_heads, HEAD_DIM, HEAD_DIM, CONV_KERNEL, _ptr(out), out.stride(0),
+                     _ptr(core), 0 if core is None else core.stride(0), _ptr(ws),
+                     ws.numel() * 2, s.cuda_stream)
     return (out, core) if return_core else out
 
 
@@ -118,25 +119,25 @@ def gdn_extend_step(qkv: torch.Tensor, b: torch.Tensor, a: torch.Tensor, z: torc
     offsets = [0]
     for e in lens:
         offsets.append(offsets[-1] + e)
-    tok = torch.tensor(offsets, dtype=torch.int32).to(qkv.device, non_blocking=True)
     value_dim = num_v_heads * HEAD_DIM
-    out = torch.empty((n_tok, value_dim), dtype=torch.bfloat16, device=qkv.device)
-    core = torch.empty_like(out) if return_core else None
     ws_bytes = _native.load().tf_gdn_extend_workspace_bytes(n_tok, len(lens), num_k_heads,
                                                            num_v_heads)
     if ws_bytes < 0:
         raise ValueError("gdn_extend_step: bad head counts")
-    ws = torch.empty((max(ws_bytes, 1),), dtype=torch.uint8, device=qkv.device)
     s = stream if stream is not None else torch.cuda.current_stream(qkv.device)
     cs, ss = layer_conv_state, layer_ssm_state
-    _native.call("tf_gdn_extend", _ptr(qkv), _rows(qkv, "qkv"), _ptr(a), _ptr(b),
-                 _rows(a, "a"), _ptr(z), _rows(z, "z"), _ptr(conv_weight), _ptr(a_log),
-                 _ptr(dt_bias), _ptr(norm_weight), float(eps), _ptr(cs), cs.stride(0), _ptr(ss),
-                 ss.stride(0), _ptr(req_indices), _ptr(tok), len(lens), n_tok, max(lens),
-                 cs.shape[0],
-                 num_k_heads, num_v_heads, HEAD_DIM, HEAD_DIM, CONV_KERNEL, _ptr(out),
-                 out.stride(0), _ptr(core), 0 if core is None else core.stride(0), _ptr(ws),
-                 ws.numel(), s.cuda_stream)
+    with on_stream(stream):
+        tok = torch.tensor(offsets, dtype=torch.int32).to(qkv.device, non_blocking=True)
+        out = torch.empty((n_tok, value_dim), dtype=torch.bfloat16, device=qkv.device)
+        core = torch.empty_like(out) if return_core else None
+        ws = torch.empty((max(ws_bytes, 1),), dtype=torch.uint8, device=qkv.device)
+        _native.call("tf_gdn_extend", _ptr(qkv), _rows(qkv, "qkv"), _ptr(a), _ptr(b),
+                     _rows(a, "a"), _ptr(z), _rows(z, "z"), _ptr(conv_weight), _ptr(a_log),
+                     _ptr(dt_bias), _ptr(norm_weight), float(eps), _ptr(cs), cs.stride(0),
+                     _ptr(ss), ss.stride(0), _ptr(req_indices), _ptr(tok), len(lens), n_tok,
+                     max(lens), cs.shape[0], num_k_heads, num_v_heads, HEAD_DIM, HEAD_DIM,
+                     CONV_KERNEL, _ptr(out), out.stride(0), _ptr(core),
+                     0 if core is None else core.stride(0), _ptr(ws), ws.numel(), s.cuda_stream)
     return (out, core) if return_core else out
 
 
