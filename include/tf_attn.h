@@ -252,6 +252,40 @@ int32_t tf_attn_plan_device(const int64_t* extend_lens, int32_t batch_size,
                             int32_t work_capacity, int32_t* dec_items, int32_t* dec_rows,
                             int32_t dec_capacity, int32_t* status, tf_stream_t stream);
 
+/* ------------------------------------------------------------------ req_to_token sync
+ * Brings the resident device req_to_token table up to date for one batch: the
+ * per-step incremental sync of engine/model_runner.py:147-167, which copies
+ * each request's rewritten prefix positions from the host table
+ * (req_to_token_pool.py:30-35 moves dirty_from back on such a rewrite) and
+ * then this step's out_cache_loc slice into the request's row.  Here the
+ * whole batch is one kernel.  For request b, row r = req_pool_indices[b]:
+ *   req_to_token[r, patch_from[b] : prefix_lens[b]]
+ *       = patch_vals[patch_offsets[b] : patch_offsets[b] + prefix_lens[b] - patch_from[b]]
+ *   req_to_token[r, prefix_lens[b] : seq_lens[b]]
+ *       = out_cache_loc[o_b : o_b + seq_lens[b] - prefix_lens[b]],
+ *         o_b = sum over b' < b of (seq_lens[b'] - prefix_lens[b'])
+ * (the flattened order of the batch's new tokens, model_runner.py:118-135).
+ * patch_from[b] >= prefix_lens[b] means no rewritten positions; patch_from,
+ * patch_offsets and patch_vals may all be NULL (none in the batch).
+ * req_pool_indices, prefix_lens, seq_lens, patch_from, patch_offsets: int64
+ * device arrays of batch_size entries; out_cache_loc: out_cache_loc_len int64
+ * entries; patch_vals: patch_vals_len int64 entries.  Rows must be distinct
+ * within one call.  Every length is read from device memory, so a call with a
+ * fixed batch_size can be captured in a HIP graph and replayed after the
+ * arrays are refilled.  A request whose row or range lies outside the table
+ * (r outside [0, rtt_rows), not 0 <= prefix <= seq <= rtt_cols) writes nothing
+ * and takes no out_cache_loc entries; entries past out_cache_loc_len and patch
+ * runs outside [0, prefix) or past patch_vals_len are not written.
+ * At most 4096 requests per call; num_workgroups 0 = 64.
+ */
+int32_t tf_req_to_token_sync(int64_t* req_to_token, int64_t rtt_rows, int64_t rtt_row_stride,
+                             int64_t rtt_cols, const int64_t* req_pool_indices,
+                             const int64_t* prefix_lens, const int64_t* seq_lens,
+                             const int64_t* out_cache_loc, int64_t out_cache_loc_len,
+                             const int64_t* patch_from, const int64_t* patch_offsets,
+                             const int64_t* patch_vals, int64_t patch_vals_len,
+                             int32_t batch_size, int32_t num_workgroups, tf_stream_t stream);
+
 /* ------------------------------------------------------------------ KV write
  * k_pool[out_cache_loc[t]] = k[t]; v_pool[out_cache_loc[t]] = v[t]
  * (full_attention.py:146-149).  k / v: [n_tokens, num_kv_heads, head_dim] in

@@ -12,7 +12,7 @@ from pathlib import Path
 from typing import Optional
 
 LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libtf_attn.so"
-ABI_VERSION = 10
+ABI_VERSION = 11
 
 TF_DTYPE_BF16 = 0
 TF_DTYPE_FP8_E4M3 = 1
@@ -81,6 +81,13 @@ SIGNATURES = {
         _p, _p,                        # status, stream
     ]),
     "tf_attn_plan_decode_items": (_i32, [_p, _i32, _p, _p, _i32]),
+    "tf_req_to_token_sync": (_i32, [
+        _p, _i64, _i64, _i64,          # req_to_token, rtt_rows, rtt_row_stride, rtt_cols
+        _p, _p, _p,                    # req_pool_indices, prefix_lens, seq_lens
+        _p, _i64,                      # out_cache_loc, out_cache_loc_len
+        _p, _p, _p, _i64,              # patch_from, patch_offsets, patch_vals, patch_vals_len
+        _i32, _i32, _p,                # batch_size, num_workgroups, stream
+    ]),
     "tf_kv_write": (_i32, [
         _p, _p, _i64, _i32,            # k, v, src_row_stride, src_dtype
         _p, _i64,                      # out_cache_loc, n_tokens

@@ -194,6 +194,116 @@ __global__ void __launch_bounds__(kPlanThreads) plan_kernel(PlanArgs a) {
   }
 }
 
+// ---------------------------------------------------------------------------
+// req_to_token sync: the per-step incremental update of the resident device
+// req_to_token table (engine/model_runner.py:147-167) as one kernel.  Request
+// b of the batch owns two runs of flat elements, its rewritten prefix positions
+// [patch_from, prefix) read from patch_vals, then its new positions
+// [prefix, seq) read from out_cache_loc; every workgroup scans the run lengths
+// of the whole batch into LDS and then takes flat elements in a grid-stride
+// loop, finding each element's request by binary search.
+constexpr int kSyncMaxBatch = kPlanMaxBatch;
+
+struct SyncArgs {
+  int64_t* table;
+  int64_t rows, stride, cols;
+  const int64_t* rpi;
+  const int64_t* prefix;
+  const int64_t* seq;
+  const int64_t* loc;
+  int64_t loc_len;
+  const int64_t* pfrom;   // NULL: no rewritten prefixes
+  const int64_t* poff;
+  const int64_t* pvals;
+  int64_t pvals_len;
+  int32_t batch;
+};
+
+struct SyncSmem {
+  int64_t flat[kSyncMaxBatch + 1];   // first flat element of request b
+  int64_t loc[kSyncMaxBatch];        // first out_cache_loc entry of request b
+  int64_t wsum[kPlanThreads / kWave];
+};
+
+// What request b writes.  A request whose row or range is outside the table
+// (row outside [0, rows), not 0 <= prefix <= seq <= cols) writes nothing and
+// takes no out_cache_loc entries; a patch run outside [0, prefix) or past the
+// end of patch_vals is dropped.
+struct SyncReq {
+  int64_t row, prefix, pfrom, poff, n_patch, n_new;
+};
+
+__device__ __forceinline__ SyncReq sync_req(const SyncArgs& a, int b) {
+  SyncReq q{0, 0, 0, 0, 0, 0};
+  const int64_t r = a.rpi[b], p = a.prefix[b], s = a.seq[b];
+  if (r < 0 || r >= a.rows || p < 0 || p > s || s > a.cols) return q;
+  q.row = r;
+  q.prefix = p;
+  q.n_new = s - p;
+  if (a.pfrom) {
+    const int64_t f = a.pfrom[b], o = a.poff[b];
+    if (f >= 0 && f < p && o >= 0 && o <= a.pvals_len - (p - f)) {
+      q.pfrom = f;
+      q.poff = o;
+      q.n_patch = p - f;
+    }
+  }
+  return q;
+}
+
+__global__ void __launch_bounds__(kPlanThreads) rtt_sync_kernel(SyncArgs a) {
+  __shared__ SyncSmem sm;
+  const int tid = threadIdx.x;
+  int64_t n_el[kPlanPer], n_loc[kPlanPer];
+  int64_t el = 0, lc = 0;
+#pragma unroll
+  for (int k = 0; k < kPlanPer; ++k) {
+    const int b = tid * kPlanPer + k;
+    n_el[k] = n_loc[k] = 0;
+    if (b < a.batch) {
+      const SyncReq q = sync_req(a, b);
+      n_el[k] = q.n_patch + q.n_new;
+      n_loc[k] = q.n_new;
+    }
+    el += n_el[k];
+    lc += n_loc[k];
+  }
+  int64_t total, total_loc;
+  int64_t e0 = block_scan(el, sm.wsum, total);
+  int64_t l0 = block_scan(lc, sm.wsum, total_loc);
+#pragma unroll
+  for (int k = 0; k < kPlanPer; ++k) {
+    sm.flat[tid * kPlanPer + k] = e0;
+    sm.loc[tid * kPlanPer + k] = l0;
+    e0 += n_el[k];
+    l0 += n_loc[k];
+  }
+  if (tid == 0) sm.flat[kSyncMaxBatch] = total;
+  __syncthreads();
+
+  const int64_t step = (int64_t)gridDim.x * kPlanThreads;
+  for (int64_t idx = (int64_t)blockIdx.x * kPlanThreads + tid; idx < total; idx += step) {
+    int lo = 0, hi = a.batch - 1;   // last request with flat <= idx
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) >> 1;
+      if (sm.flat[mid] <= idx) lo = mid; else hi = mid - 1;
+    }
+    const SyncReq q = sync_req(a, lo);
+    const int64_t j = idx - sm.flat[lo];
+    int64_t pos, val;
+    if (j < q.n_patch) {
+      pos = q.pfrom + j;
+      val = a.pvals[q.poff + j];
+    } else {
+      const int64_t li = sm.loc[lo] + (j - q.n_patch);
+      if (li >= a.loc_len) continue;
+      pos = q.prefix + (j - q.n_patch);
+      val = a.loc[li];
+    }
+    a.table[q.row * a.stride + pos] = val;
+  }
+}
+
 }  // namespace
 }  // namespace tfa
 
@@ -241,6 +351,56 @@ int32_t tf_attn_plan_device(const int64_t* extend_lens, int32_t batch_size,
   hipLaunchKernelGGL(plan_kernel, dim3(1), dim3(kPlanThreads), 0,
                      reinterpret_cast<hipStream_t>(stream), a);
   return launch_status("tf_attn_plan_device launch");
+}
+
+int32_t tf_req_to_token_sync(int64_t* req_to_token, int64_t rtt_rows, int64_t rtt_row_stride,
+                             int64_t rtt_cols, const int64_t* req_pool_indices,
+                             const int64_t* prefix_lens, const int64_t* seq_lens,
+                             const int64_t* out_cache_loc, int64_t out_cache_loc_len,
+                             const int64_t* patch_from, const int64_t* patch_offsets,
+                             const int64_t* patch_vals, int64_t patch_vals_len,
+                             int32_t batch_size, int32_t num_workgroups, tf_stream_t stream) {
+  using namespace tfa;
+  clear_error();
+  if (batch_size < 0 || batch_size > kSyncMaxBatch)
+    return fail(TF_ERR_UNSUPPORTED, "req_to_token_sync: batch_size=%d (at most %d)",
+                batch_size, kSyncMaxBatch);
+  if (num_workgroups < 0 || num_workgroups > 4096)
+    return fail(TF_ERR_INVALID, "req_to_token_sync: num_workgroups=%d", num_workgroups);
+  if (batch_size == 0) return TF_OK;
+  if (!req_to_token || !req_pool_indices || !prefix_lens || !seq_lens)
+    return fail(TF_ERR_INVALID, "req_to_token_sync: null pointer argument");
+  if (rtt_rows < 1 || rtt_cols < 1 || rtt_row_stride < rtt_cols)
+    return fail(TF_ERR_INVALID, "req_to_token_sync: table %lld x %lld, row stride %lld",
+                (long long)rtt_rows, (long long)rtt_cols, (long long)rtt_row_stride);
+  if (out_cache_loc_len < 0 || (out_cache_loc_len > 0 && !out_cache_loc))
+    return fail(TF_ERR_INVALID, "req_to_token_sync: out_cache_loc of %lld entries",
+                (long long)out_cache_loc_len);
+  const bool patches = patch_from || patch_offsets || patch_vals;
+  if (patches && (!patch_from || !patch_offsets || (patch_vals_len > 0 && !patch_vals)))
+    return fail(TF_ERR_INVALID,
+                "req_to_token_sync: patch_from, patch_offsets and patch_vals go together");
+  if (patch_vals_len < 0)
+    return fail(TF_ERR_INVALID, "req_to_token_sync: patch_vals_len=%lld",
+                (long long)patch_vals_len);
+  SyncArgs a;
+  a.table = req_to_token;
+  a.rows = rtt_rows;
+  a.stride = rtt_row_stride;
+  a.cols = rtt_cols;
+  a.rpi = req_pool_indices;
+  a.prefix = prefix_lens;
+  a.seq = seq_lens;
+  a.loc = out_cache_loc;
+  a.loc_len = out_cache_loc_len;
+  a.pfrom = patches ? patch_from : nullptr;
+  a.poff = patches ? patch_offsets : nullptr;
+  a.pvals = patches ? patch_vals : nullptr;
+  a.pvals_len = patches ? patch_vals_len : 0;
+  a.batch = batch_size;
+  hipLaunchKernelGGL(rtt_sync_kernel, dim3(num_workgroups ? num_workgroups : 64),
+                     dim3(kPlanThreads), 0, reinterpret_cast<hipStream_t>(stream), a);
+  return launch_status("tf_req_to_token_sync launch");
 }
 
 }  // extern "C"
