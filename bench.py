@@ -45,8 +45,8 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--only", default="decode,extend,mixed,fp8,prep,gate,plan,oproj,gdn",
-                    help="comma list of decode,extend,mixed,fp8,prep,copy")
+    ap.add_argument("--only", default="decode,extend,mixed,fp8,prep,gate,plan,rtt,oproj,gdn",
+                    help="comma list of decode,extend,mixed,fp8,prep,gate,plan,rtt,oproj,gdn,copy")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--workgroups", type=int, default=0,
                     help="decode persistent grid size (0 = one per CU)")
@@ -448,6 +448,94 @@ def _plan_step(torch, wl, SlotAttentionCall, args, n, time):
             "device_planned_cpu_ms": dev_ms[1], "graph_replay_cpu_ms": graph_ms[1]}
 
 
+def bench_rtt_sync(torch, args):
+    """Per-step sync of the resident device req_to_token table, wall clock per
+    step: the reference's per-request loop (engine/model_runner.py:147-167: a
+    host-to-device copy of each rewritten prefix run, a slice copy of each
+    request's out_cache_loc) against DeviceReqToTokenTable.sync (one pinned
+    copy + one kernel), and the kernel alone replayed from a HIP graph for the
+    decode-only step."""
+    import time
+    import numpy as np
+    from tokenfactory_amd.req_to_token import DeviceReqToTokenTable
+    rng = np.random.default_rng(7)
+    max_reqs, max_ctx = 512, 32768
+    n = max(20, args.steps * 2)
+    rows = rng.permutation(max_reqs)[:132].tolist()
+    ext_rows, dec_rows = rows[:4], rows[4:]
+    dec_seq = rng.integers(512, 16384, size=128).tolist()
+    ext_prefix = rng.integers(0, 8192, size=4).tolist()
+    host = [[] for _ in range(max_reqs)]
+    for r, s in zip(dec_rows, dec_seq):
+        host[r] = rng.integers(1, 1 << 21, size=s).tolist()
+    for r, p in zip(ext_rows, ext_prefix):
+        host[r] = rng.integers(1, 1 << 21, size=p + 2048).tolist()
+    cases = {
+        "decode_128": (dec_rows, [s - 1 for s in dec_seq], dec_seq, {}),
+        "mixed_restore": (ext_rows + dec_rows, ext_prefix + [s - 1 for s in dec_seq],
+                          [p + 2048 for p in ext_prefix] + dec_seq,
+                          {r: 0 for r in ext_rows}),
+    }
+    ref_tensor = torch.full((max_reqs, max_ctx), -1, dtype=torch.long, device="cuda")
+    table = DeviceReqToTokenTable(max_reqs, max_ctx, device="cuda")
+    res = {}
+    for tag, (rr, pp, ss, synced_at) in cases.items():
+        loc_list = [x for r, p, s in zip(rr, pp, ss) for x in host[r][p:s]]
+        loc = torch.tensor(loc_list, dtype=torch.long, device="cuda")
+        cursors = [synced_at.get(r, p) for r, p in zip(rr, pp)]
+
+        def ref_step():
+            off = 0
+            for r, p, s, c in zip(rr, pp, ss, cursors):
+                if c < p:
+                    ref_tensor[r, c:p] = torch.tensor(host[r][c:p], dtype=torch.long,
+                                                      device="cuda")
+                ref_tensor[r, p:s] = loc[off:off + s - p]
+                off += s - p
+
+        def our_step():
+            for r, c in zip(rr, cursors):
+                table.synced_lens[r] = c
+            table.sync(rr, pp, ss, loc, host)
+
+        def wall(fn):
+            for _ in range(3):
+                fn()
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            for _ in range(n):
+                fn()
+            torch.cuda.synchronize()
+            return (time.perf_counter() - t0) / n * 1e3
+
+        r = {"reference_loop_ms": wall(ref_step), "sync_ms": wall(our_step)}
+        torch.cuda.synchronize()
+        if not torch.equal(table.tensor, ref_tensor):
+            raise RuntimeError(f"req_to_token sync differs from the reference loop ({tag})")
+        if not synced_at:
+            dev = [torch.tensor(x, dtype=torch.long, device="cuda") for x in (rr, pp, ss)]
+            side = torch.cuda.Stream()
+            side.wait_stream(torch.cuda.current_stream())
+            with torch.cuda.stream(side):
+                table.sync_from_device(dev[0], dev[1], dev[2], loc)
+            torch.cuda.current_stream().wait_stream(side)
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graph):
+                table.sync_from_device(dev[0], dev[1], dev[2], loc)
+            r["graph_replay_ms"] = wall(graph.replay)
+        r["patched_positions"] = sum(p - c for p, c in zip(pp, cursors))
+        r["new_positions"] = len(loc_list)
+        res[tag] = r
+        log(f"req_to_token sync {tag}: reference loop {r['reference_loop_ms']*1e3:.0f} us, "
+            f"one kernel {r['sync_ms']*1e3:.0f} us"
+            + (f", graph replay {r['graph_replay_ms']*1e3:.0f} us" if "graph_replay_ms" in r
+               else ""))
+    res["workload"] = ("512 x 32768 table; decode_128: 128 decode rows (contexts U[512, 16k]); "
+                       "mixed_restore: those plus 4 requests extending 2048 tokens after a "
+                       "prefix of U[0, 8k) rewritten since the last sync")
+    return res
+
+
 def bench_copy(torch, args):
     """A plain device copy of known size, the reference point for HBM counters."""
     n = 1 << 30
@@ -582,6 +670,8 @@ def main():
         secondary["qk_prep_20k"] = bench_prep(torch, args)
     if "plan" in only:
         secondary["step_planning"] = bench_plan(torch, workloads, SlotAttentionCall, args)
+    if "rtt" in only:
+        secondary["req_to_token_sync"] = bench_rtt_sync(torch, args)
     if "gate" in only:
         secondary["output_gate"] = bench_gate(torch, workloads, SlotAttentionCall, args)
         torch.cuda.empty_cache()

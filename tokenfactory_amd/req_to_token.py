@@ -34,9 +34,9 @@ class DeviceReqToTokenTable:
             raise ValueError(f"table {max_reqs} x {max_context_len}")
         self.max_reqs = max_reqs
         self.max_context_len = max_context_len
-        self.device = torch.device(device)
         self.tensor = torch.full((max_reqs, max_context_len), -1, dtype=torch.long,
-                                 device=self.device)
+                                 device=device)
+        self.device = self.tensor.device
         self.synced_lens: List[int] = [0] * max_reqs
 
     # engine/model_runner.py:86-95 (reset_req_linear_state / restore_req_linear_state)
