@@ -132,10 +132,12 @@ def bench_decode(torch, workloads, SlotAttentionCall, args):
     return res
 
 
-def bench_extend(torch, workloads, SlotAttentionCall, args):
-    log("building extend_prefix (16 requests, 4 radix groups)")
-    wl = workloads.extend_prefix(device="cuda")
-    call = SlotAttentionCall(wl.q, wl.k_pool, wl.v_pool, wl.batch, scaling=wl.scale)
+def bench_extend(torch, workloads, SlotAttentionCall, args, seed=13, kv_fp8=False):
+    log(f"building extend_prefix (16 requests, 4 radix groups, seed {seed}"
+        f"{', fp8-e4m3 KV' if kv_fp8 else ''})")
+    wl = workloads.extend_prefix(device="cuda", seed=seed, kv_fp8=kv_fp8)
+    call = SlotAttentionCall(wl.q, wl.k_pool, wl.v_pool, wl.batch, scaling=wl.scale,
+                             k_scale=wl.k_scale, v_scale=wl.v_scale)
     # About 2 ms per step: half the step count, and the full warm-up so that
     # the clocks have settled (MFMA-heavy launches ramp over the first ~20 ms).
     steps = max(3, args.steps // 2)
@@ -144,17 +146,20 @@ def bench_extend(torch, workloads, SlotAttentionCall, args):
     k_spread = last_spread()
     flops = wl.extend_flops()
     tf = flops / (k_ms * 1e-3)
-    log(f"extend_prefix: {ms*1e3:.1f} us/step, {tf/1e12:.1f} TFLOP/s "
-        f"({tf/MFMA_BF16_PEAK*100:.1f}% of bf16 MFMA peak)")
-    return {"workload": "extend_prefix: 16 requests in 4 radix-prefix groups of 4, prefix "
-                        "U[0,4k] shared per group, new tokens U[512,2k], causal, 24q/4kv, "
-                        "head_dim 256, bf16",
+    prefixes = sorted(set(L - e for L, e in zip(wl.seq_lens, wl.ext_lens)))
+    log(f"extend_prefix seed {seed}{' fp8' if kv_fp8 else ''}: {ms*1e3:.1f} us/step, "
+        f"{tf/1e12:.1f} TFLOP/s ({tf/MFMA_BF16_PEAK*100:.1f}% of bf16 MFMA peak)")
+    return {"workload": f"extend_prefix seed {seed}: 16 requests in 4 radix-prefix groups of 4, "
+                        f"prefix U[0,4k] shared per group (drawn: {prefixes}), new tokens "
+                        f"U[512,2k], causal, 24q/4kv, head_dim 256, "
+                        + ("fp8-e4m3 KV (per-tensor scales amax/448) read as bf16, bf16 "
+                           "queries" if kv_fp8 else "bf16"),
             "value": flops / (ms * 1e-3) / 1e12, "unit": "TFLOP/s", "ms_per_step": ms,
             "steps": steps, "flops_per_step": flops, "kernel_ms": k_ms,
             "kernel_ms_p10_p50_p90": k_spread,
             "roofline": {"bound": "mfma", "achieved": tf / 1e12, "peak": MFMA_BF16_PEAK / 1e12,
                          "unit": "TFLOP/s", "frac": tf / MFMA_BF16_PEAK,
-                         "kernel": "extend_bf16_kernel"}}
+                         "kernel": "extend_kernel<fp8>" if kv_fp8 else "extend_bf16_kernel"}}
 
 
 def bench_mixed(torch, workloads, SlotAttentionCall, args):
@@ -659,6 +664,12 @@ def main():
         dec = bench_decode(torch, workloads, SlotAttentionCall, args)
     if "extend" in only:
         secondary["extend_prefix"] = bench_extend(torch, workloads, SlotAttentionCall, args)
+        torch.cuda.empty_cache()
+        secondary["extend_prefix_seed22"] = bench_extend(torch, workloads, SlotAttentionCall,
+                                                         args, seed=22)
+        torch.cuda.empty_cache()
+        secondary["extend_prefix_fp8"] = bench_extend(torch, workloads, SlotAttentionCall,
+                                                      args, kv_fp8=True)
         torch.cuda.empty_cache()
     if "mixed" in only:
         secondary["mixed"] = bench_mixed(torch, workloads, SlotAttentionCall, args)

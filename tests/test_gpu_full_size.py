@@ -124,12 +124,16 @@ def test_full_size_fp8_128k_decode(gpu):
     assert_attn_close(run(wl, decode_workgroups=17), out, what="fp8 128k: 17 workgroups", **INV)
 
 
-def test_full_size_extend_prefix_heavy_rows(gpu):
+@pytest.mark.parametrize("seed,kv_fp8", [(13, False), (22, False), (13, True)],
+                         ids=["seed13", "seed22", "seed13-fp8"])
+def test_full_size_extend_prefix_heavy_rows(gpu, seed, kv_fp8):
     """16 requests in 4 radix groups (prefix U[0, 4k] shared per group, 512..2k new
     tokens): the last 64 rows of the two requests with the most keys and the
     first 64 rows of the one with the longest prefix against the oracle; every
-    row against each prefix group run as its own batch."""
-    wl = workloads.extend_prefix(device=gpu)
+    row against each prefix group run as its own batch.  Seed 13 draws long
+    prefixes (mean 3.5k), seed 22 typical ones (mean 2.0k); the fp8 case reads
+    an e4m3 pool and is checked against the oracle over the dequantised pool."""
+    wl = workloads.extend_prefix(device=gpu, seed=seed, kv_fp8=kv_fp8)
     out = run(wl)
     torch.cuda.synchronize()
     assert torch.isfinite(out.float()).all()

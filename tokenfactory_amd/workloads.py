@@ -251,7 +251,7 @@ def decode_b64(device="cuda", seed=11, batch=64, lo=1024, hi=8192, pool_slots=(1
 
 
 def extend_prefix(device="cuda", seed=13, n_groups=4, per_group=4, prefix_hi=4096,
-                  new_lo=512, new_hi=2048, pool_slots=1 << 18) -> Workload:
+                  new_lo=512, new_hi=2048, pool_slots=1 << 18, kv_fp8=False) -> Workload:
     rng = np.random.default_rng(seed)
     prefixes = rng.integers(0, prefix_hi + 1, size=n_groups).tolist()
     groups, seq, ext = [], [], []
@@ -263,7 +263,7 @@ def extend_prefix(device="cuda", seed=13, n_groups=4, per_group=4, prefix_hi=409
             ext.append(n)
     return build("extend_prefix", seq, ext, num_q_heads=24, num_kv_heads=4, head_dim=256,
                  pool_slots=pool_slots, device=device, seed=seed, prefix_groups=groups,
-                 shared_prefix_lens=prefixes)
+                 shared_prefix_lens=prefixes, kv_fp8=kv_fp8)
 
 
 def mixed(device="cuda", seed=17, n_extend=4, extend_new=2048, prefix_hi=8192, n_decode=128,
