@@ -18,7 +18,7 @@ REPO_DIR = PKG_DIR.parent
 CSRC = PKG_DIR / "csrc"
 LIB_DIR = PKG_DIR / "_lib"
 LIB_PATH = LIB_DIR / "libtf_attn.so"
-SOURCES = ["abi.hip", "decode.hip", "extend.hip", "extend_bf16.hip", "fp8_linear.hip",
+SOURCES = ["abi.hip", "decode.hip", "extend.hip", "fp8_linear.hip",
            "gdn.hip", "kv_ops.hip", "plan.hip", "qk_prep.hip"]
 ARCH = "gfx950"
 
@@ -46,12 +46,12 @@ def compile_flags() -> list:
 
 
 # Per-file flags on top of compile_flags(): MFMA accumulators in VGPRs.
-# extend_bf16.hip: two waves per SIMD, O^T, Q^T and S^T all in the 256 VGPRs
+# extend.hip: two waves per SIMD, O^T, Q^T and S^T all in the 256 VGPRs
 # of a wave.  fp8_linear.hip: the GEMM folds each MFMA product into fp32
 # accumulators with a VALU FMA, which reads VGPRs only.  gdn.hip: the chunked
 # recurrence feeds its accumulators (state, P, Delta) back to VALU work and
 # MFMA operands.
-EXTRA_FLAGS = {"extend_bf16.hip": ["-mllvm", "--amdgpu-mfma-vgpr-form=1"],
+EXTRA_FLAGS = {"extend.hip": ["-mllvm", "--amdgpu-mfma-vgpr-form=1"],
                "fp8_linear.hip": ["-mllvm", "--amdgpu-mfma-vgpr-form=1"],
                "gdn.hip": ["-mllvm", "--amdgpu-mfma-vgpr-form=1"]}
 

@@ -1,41 +1,45 @@
-// Causal prefill / extend attention over an fp8-e4m3 KV pool (bf16 MFMA), and
-// the tf_attn_extend entry point (bf16 pools run extend_bf16.hip's kernel).
+// Causal prefill / extend attention over a bf16 or fp8-e4m3 KV pool (bf16
+// MFMA), and the tf_attn_extend entry point.
 //
 // Replaces the reference's extend / mixed branch (qwen3_8/full_attention.py:244-283)
-// and the ext_len > 1 case of its bsz == 1 branch (:179-213).  The reference
-// pads queries to [B, max_ext, Hq, D], gathers and GQA-expands the whole padded
-// context and runs a dense masked SDPA; here each request is processed at its
-// own length and nothing is padded or expanded.
+// and the ext_len > 1 case of its bsz == 1 branch (:179-213).
+// The reference pads queries to [B, max_ext, Hq, D], gathers and GQA-expands
+// the whole padded context and runs a dense masked SDPA; here each request is
+// processed at its own length and nothing is padded or expanded.
 //
 // Work item (from tf_attn_plan_extend): (request b, kv head hk, row0).  The
 // rows of a (b, hk) pair are the ext_b * G flattened (token t, q head h) pairs
-// of the kv head's q-head group, row = t * G + h; an item covers 256 of them
-// and runs as two workgroups of 128 rows (32 per wave), so all G heads of a
-// GQA group share every K/V tile.
+// of the kv head's q-head group, row = t * G + h; an item covers 256 of them,
+// 32 per wave (one 32-row MFMA block) over 8 waves, so all G heads of a GQA
+// group share every K/V tile staged in LDS.
 // Row (t, h) attends to context positions 0 .. P + t, P = L - ext.
 //
-// Each wave computes, per 64-key tile j, with v_mfma_f32_32x32x16_bf16:
-//   S^T[key, row] = K Q^T        (Q^T register-resident, K from LDS)
-//   online softmax of S^T        (a row's 64 scores live in lanes n and n + 32)
-//   O^T[dim, row] += V^T P^T     (V^T from LDS, P^T packed straight from S^T)
-// so each lane owns one row: its max, sum and 128 of its output dims.  The
-// e4m3 rows are widened to bf16 (exactly) on their way into LDS.
+// Per 32-key tile each wave computes, with v_mfma_f32_32x32x16_bf16,
+//   S^T[key, row] = K Q^T        (Q^T register-resident, K from LDS),
+//   the online softmax per row (a row's 32 scores live in lanes n and n + 32),
+//   O^T[dim, row] += V^T P^T     (V^T read from row-major V in LDS with
+//                                 ds_read_b64_tr_b16, P^T packed from S^T),
+// so each lane owns one row: its max, sum and 128 output dims.
 //
-// Software pipeline (one barrier per tile, no wave-dependent branches around
-// the accumulator so it stays in AGPRs):
-//   * the QK^T MFMAs of tile j + 1 are issued next to the softmax of tile j,
-//     and the exps of tile j next to its PV MFMAs, so VALU work hides under
-//     matrix-core time;
-//   * tile j + 2 is gathered from HBM into registers while tile j is computed
-//     (slot ids come from an LDS slot buffer refilled 1024 keys at a time, so
-//     no load waits on a dependent slot lookup in global memory);
-//   * K lands in LDS row-major with a 16-byte pad per key row, V is transposed
-//     in registers and lands as V^T rows of 64 keys, chunk-swizzled; both are
-//     double-buffered (K(j+2) overwrites K(j) during PV(j); V(j+2) is written
-//     at the start of the next tile, after every wave has finished PV(j)).
-//   * The running max is raised lazily: the accumulator is rescaled only when
-//     some row's max grows by more than 2^8, otherwise the old max stays the
-//     reference point (exact in exact arithmetic; p <= 2^8 fits bf16's range).
+// Two waves per SIMD, half a step apart.  O^T (128 registers) and Q^T (64)
+// of a 32-row block leave room for a second wave on each SIMD.  Waves 0-3
+// ("lead") run QK^T(j), softmax(j), PV(j) between barriers j - 1 and j; waves
+// 4-7 ("trail", one per SIMD beside a lead wave) run PV(j - 1), QK^T(j),
+// softmax(j).  So while one wave of a SIMD works through its softmax the other
+// issues MFMAs, and each wave's waits (LDS, barrier, MFMA results) are covered
+// by the other wave's work.
+//
+// Staging: K and V rows go from global memory straight into LDS
+// (global_load_lds_dwordx4, 1 KB = two keys per instruction, 2 + 2 per wave
+// per tile) two tiles ahead, into 3 K stages and 4 V stages (the trailing
+// waves read V one tile later than K), one barrier per tile.  Slot ids reach
+// LDS the same way, 1024 keys at a time (the low dword of each req_to_token
+// entry).  fp8 pools: the e4m3 rows go into LDS the same way (one K and one V
+// instruction per wave per tile) and one step later each lane widens the 16
+// bytes it loaded into the bf16 stages (exact), so the MFMA side is the bf16
+// kernel's; scores and outputs are scaled by k_scale / v_scale.
+// The running max is raised lazily: the accumulators are rescaled only when a
+// row's max grows by more than 2^8 (exact in exact arithmetic; p <= 2^8).
 #include <math.h>
 
 #include <type_traits>
@@ -46,353 +50,356 @@
 namespace tfa {
 namespace {
 
+typedef __attribute__((address_space(3))) void lds_void;
+typedef short i16x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
+
 constexpr int kD = 256;
-constexpr int kWaves = 4;
+constexpr int kWaves = 8;
+constexpr int kLeadWaves = kWaves / 2;
 constexpr int kThreads = kWaves * kWave;
-constexpr int kRowsPerWave = 32;
-static_assert(2 * kWaves * kRowsPerWave == kExtendItemRows, "two workgroups per item");
-constexpr int kBN = 64;                         // keys per tile
-constexpr int kKStride = 2 * kD + 16;           // bytes per K row in LDS (padded)
-constexpr int kKStage = kBN * kKStride;         // 33792
-constexpr int kVtStride = 2 * kBN;              // bytes per V^T row (64 keys)
-constexpr int kVtStage = kD * kVtStride;        // 32768
-constexpr int kSlotChunk = 1024;                // keys per slot-buffer refill
+constexpr int kRowsPerWave = 32;                     // one 32-row MFMA block
+static_assert(kWaves * kRowsPerWave == kExtendItemRows, "item rows");
+constexpr int kBN = 32;                              // keys per tile
+constexpr int kRowBytes = 2 * kD;                    // 512
+// K: key pairs (2i, 2i + 1) at i * kKPair, 32 bytes of padding after each
+// pair; key n's 16-byte chunk c sits at chunk c ^ (n & 1) of its row.  The
+// MFMA-operand reads (16 consecutive keys, one chunk) then hit 16 distinct
+// 16-byte bank groups.
+constexpr int kKPair = 2 * kRowBytes + 32;           // 1056
+constexpr int kKStage = (kBN / 2) * kKPair;          // 16896
+// V: row-major, 512 B per key; key n's chunk c sits at chunk c ^ vswz(n),
+// vswz(n) = 10 (n & 1) + 4 ((n >> 1) & 1), which makes every transposing read
+// (4 keys x 64 B per 32 lanes) conflict-free.
+constexpr int kVStage = kBN * kRowBytes;             // 16384
+constexpr int kAhead = 2;                            // tiles staged ahead
+// bf16 pools: the DMA fills the K / V stages the MFMAs read, 3 K stages and 4
+// V stages (the trailing waves read V one tile later than K).  fp8 pools: the
+// DMA fills two e4m3 stages and the widened tile goes into the bf16 stages one
+// step before it is read, so 2 K and 3 V stages suffice.
+template <bool FP8> constexpr int kStagesOf = FP8 ? 2 : kAhead + 1;
+template <bool FP8> constexpr int kVStagesOf = FP8 ? 3 : kAhead + 2;
+constexpr int kF8Half = kBN * kD;                    // 8 KB: one tile of e4m3 K (or V)
+constexpr int kF8Stage = 2 * kF8Half;                // K then V
+constexpr int kSlotChunk = 1024;
 constexpr int kSlotMask = 2 * kSlotChunk - 1;
 constexpr int kTilesPerSlotChunk = kSlotChunk / kBN;
-constexpr float kRescaleLog2 = 8.f;             // lazy-rescale threshold (log2 units)
+constexpr float kRescaleLog2 = 8.f;
+constexpr int kQkAhead = 2;                          // K fragments in flight
+constexpr int kPvAhead = 2;                          // V fragments in flight
 
+// A wave's 32 rows x 256 dims of bf16 (Q on the way in, the output on the
+// way out), row-major with 16-byte chunk c of row r at chunk c ^ r: the
+// row-contiguous global side and the MFMA-fragment side both access it
+// without bank conflicts beyond two-way.
+constexpr int kTileBytes = kRowsPerWave * kRowBytes;   // 16 KB
 
-struct __attribute__((aligned(16))) ExtendSmem {
-  uint8_t k[2 * kKStage];          // 66 KB
-  uint8_t vt[2 * kVtStage];        // 64 KB
+template <bool FP8>
+struct __attribute__((aligned(16))) Smem {
+  union {
+    struct {
+      uint8_t k[kStagesOf<FP8> * kKStage];
+      uint8_t v[kVStagesOf<FP8> * kVStage];
+      uint8_t f8[FP8 ? 2 * kF8Stage : 16];   // e4m3 rows as they arrive
+    };
+    uint8_t rows[kWaves][kTileBytes];   // Q in the prologue, the output at the end
+  };
   int32_t slots[2 * kSlotChunk];   // 8 KB: key k's slot id at slots[k % 2048]
 };
+static_assert(sizeof(Smem<true>) <= 160 * 1024 && sizeof(Smem<false>) <= 160 * 1024, "LDS");
 
-// One tile's gathered rows for this thread: the 8 keys run0 + {0..3, 8..11}
-// (run0 = 16 (grp / 2) + 4 (grp % 2), grp = tid / 32), 16 bytes each (chunk
-// tid % 32 of the head row: dims 8c .. 8c + 7; fp8 rows keep 8 bytes in .xy).
-// Those 8 keys are exactly V^T positions 8 grp .. 8 grp + 7 (see exp_pv_tile).
+__device__ __forceinline__ int swz_chunk(int r, int c) { return (c ^ r) & 31; }
+
+// x through an empty asm: what is computed from it cannot be hoisted out of
+// the block (the epilogue's row arithmetic would otherwise be computed in the
+// prologue and kept, or spilled, across the whole tile loop).
+__device__ __forceinline__ int opaque(int x) {
+  asm volatile("" : "+v"(x));
+  return x;
+}
+
+__device__ __forceinline__ int vswz(int n) { return 10 * (n & 1) + 4 * ((n >> 1) & 1); }
+
+// ---------------------------------------------------------------- staging
+// global_load_lds_dword{,x4} as inline assembly: lane l's 4 / 16 bytes land at
+// LDS address M0 + 4 l / 16 l.  The compiler's wait-count pass does not see
+// these loads (its own waits only get more conservative), so every reader of
+// the staged data synchronises explicitly: s_waitcnt vmcnt, then a barrier.
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return (uint32_t)(uintptr_t)(const lds_void*)p;
+}
+__device__ __forceinline__ void dma4(const void* gptr, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dword %0, off"
+               :: "v"(gptr), "s"(lds) : "m0");
+}
+__device__ __forceinline__ void dma16(const void* gptr, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off"
+               :: "v"(gptr), "s"(lds) : "m0");
+}
+
+// The tile issued one step earlier must have landed; the loads per wave of the
+// tile issued in this step (4 for bf16 rows, 2 for e4m3 rows) may still be in
+// flight.
 template <bool FP8>
-struct TileRegs {
-  u32x4 k[8];
-  u32x4 v[8];
+__device__ __forceinline__ void vm_wait_staged() {
+  static_assert(kAhead == 2, "vmcnt immediate");
+  if (FP8)
+    asm volatile("s_waitcnt vmcnt(2)" ::: "memory");
+  else
+    asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
+}
+
+// Slot ids of keys [chunk * 1024, +1024) clamped to [0, kend): wave w moves
+// 128 of them (2 dword instructions) into slot-buffer half chunk & 1.
+__device__ __forceinline__ void slot_issue(const int64_t* rtt, int chunk, int kend, int w,
+                                           int lane, int32_t* slots) {
+  const int key0 = chunk * kSlotChunk + 128 * w;
+  const uint32_t dst = lds_addr(slots + (chunk & 1) * kSlotChunk + 128 * w);
+#pragma unroll
+  for (int i = 0; i < 2; ++i) dma4(rtt + min(key0 + 64 * i + lane, kend - 1), dst + 256 * i);
+}
+
+// Per-lane global bases: lane l loads 16-byte chunk (l % 32) ^ (key & 1) of a
+// K row and chunk (l % 32) ^ vswz(key) of a V row; key & 1 = l / 32 and
+// vswz(key) = 10 (l / 32) + 4 (p & 1) for instruction p.
+struct StageBases {
+  const uint8_t* k;
+  const uint8_t* v[2];   // by p & 1
 };
 
-__device__ __forceinline__ int run_key(int j) { return 8 * (j >> 2) + (j & 3); }
-
-template <bool FP8>
-__device__ __forceinline__ void gather_tile(const int32_t* slots, const uint8_t* kb,
-                                            const uint8_t* vb, uint32_t lane_off,
-                                            int64_t slot_bytes, int key0, int run0,
-                                            TileRegs<FP8>& r) {
-  const u32x4 s0 = *reinterpret_cast<const u32x4*>(slots + ((key0 + run0) & kSlotMask));
-  const u32x4 s1 = *reinterpret_cast<const u32x4*>(slots + ((key0 + run0 + 8) & kSlotMask));
-  int64_t off[8];
-#pragma unroll
-  for (int j = 0; j < 8; ++j) off[j] = (int64_t)(j < 4 ? s0[j] : s1[j - 4]) * slot_bytes + lane_off;
-  // K rows first: store_k consumes them a whole tile earlier than store_vt
-  // consumes the V rows.
-#pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    if (FP8) {
-      const u32x2 x = ld_g8(kb + off[j]);
-      r.k[j] = u32x4{x[0], x[1], 0u, 0u};
-    } else {
-      r.k[j] = ld_g16(kb + off[j]);
-    }
-  }
-#pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    if (FP8) {
-      const u32x2 y = ld_g8(vb + off[j]);
-      r.v[j] = u32x4{y[0], y[1], 0u, 0u};
-    } else {
-      r.v[j] = ld_g16(vb + off[j]);
-    }
-  }
+__device__ __forceinline__ StageBases stage_bases(const uint8_t* kb, const uint8_t* vb, int lane) {
+  const int pos = lane & 31, g = lane >> 5;
+  StageBases sb;
+  sb.k = kb + 16 * (pos ^ g);
+  sb.v[0] = vb + 16 * (pos ^ (10 * g));
+  sb.v[1] = vb + 16 * (pos ^ (10 * g + 4));
+  return sb;
 }
 
-template <bool FP8>
-__device__ __forceinline__ void gather_k(const int32_t* slots, const uint8_t* kb, uint32_t lane_off,
-                                         int64_t slot_bytes, int key0, int run0,
-                                         TileRegs<FP8>& r) {
-  const u32x4 s0 = *reinterpret_cast<const u32x4*>(slots + ((key0 + run0) & kSlotMask));
-  const u32x4 s1 = *reinterpret_cast<const u32x4*>(slots + ((key0 + run0 + 8) & kSlotMask));
-#pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    const int64_t off = (int64_t)(j < 4 ? s0[j] : s1[j - 4]) * slot_bytes + lane_off;
-    if (FP8) {
-      const u32x2 x = ld_g8(kb + off);
-      r.k[j] = u32x4{x[0], x[1], 0u, 0u};
-    } else {
-      r.k[j] = ld_g16(kb + off);
-    }
+// What one step stages: wave w moves keys 4w .. 4w + 3 of `tile`; instruction
+// p moves keys 4w + 2p + {0, 1}, lane l filling 16-byte position l % 32 of key
+// 4w + 2p + l / 32.  The slot id is clamped into the pool where it is used, so
+// that a stray req_to_token entry can never address memory outside the pool.
+struct Stager {
+  StageBases sb;
+  const int32_t* slots;
+  uint8_t* k_dst;
+  uint8_t* v_dst;
+  uint32_t slot_bytes;
+  int32_t smax;
+  bool wrap;     // bsz == 1 call: negative slot ids index from the pool's end
+  int tile;
+  int w;
+  int g;
+
+  __device__ __forceinline__ int32_t slot(int p) const {
+    return slots[(tile * kBN + 4 * w + 2 * p + g) & kSlotMask];
   }
-}
-
-template <bool FP8>
-__device__ __forceinline__ void store_k(uint8_t* kst, int run0, int c, const TileRegs<FP8>& r) {
-  uint8_t* p = kst + run0 * kKStride + 16 * c;
-#pragma unroll
-  for (int j = 0; j < 8; ++j)
-    st_s16(p + run_key(j) * kKStride, FP8 ? e4m3x8_to_bf16x8(r.k[j][0], r.k[j][1]) : r.k[j]);
-}
-
-// V^T row `dim` holds the tile's 64 keys in 8 chunks of 8 positions; chunk pc
-// is stored at chunk pc ^ swz(dim), swz(dim) = (dim ^ (dim >> 3)) & 7, which
-// keeps both these writes and the PV reads free of bank conflicts.
-template <bool FP8>
-__device__ __forceinline__ void store_vt(uint8_t* vst, int grp, int c, const TileRegs<FP8>& r) {
-  u32x4 in[8];
-#pragma unroll
-  for (int j = 0; j < 8; ++j) in[j] = FP8 ? e4m3x8_to_bf16x8(r.v[j][0], r.v[j][1]) : r.v[j];
-  const int y = (grp ^ c) & 7;
-  uint8_t* p = vst + 8 * c * kVtStride;
-#pragma unroll
-  for (int d = 0; d < 8; ++d) {
-    u32x4 o;
-#pragma unroll
-    for (int w = 0; w < 4; ++w) o[w] = pair_sel(in[2 * w + 1][d >> 1], in[2 * w][d >> 1], d & 1);
-    st_s16(p + d * kVtStride + 16 * (y ^ d), o);
+  // Row `slot` of K and V: one 32 x 32 -> 64-bit multiply-add per address
+  // (slot ids and the slot stride fit 32 bits).
+  __device__ __forceinline__ void issue(int32_t sl, int p) const {
+    if (wrap && sl < 0) sl += smax + 1;
+    const uint64_t off = (uint64_t)(uint32_t)min(max(sl, 0), smax) * slot_bytes;
+    dma16(sb.k + off, lds_addr(k_dst + (2 * w + p) * kKPair));
+    dma16(sb.v[p & 1] + off, lds_addr(v_dst + (4 * w + 2 * p) * kRowBytes));
   }
-}
-
-// Slot ids of keys [chunk * 1024, chunk * 1024 + 1024) clamped to the needed
-// range [0, kend): loaded into registers (4 per thread) a few tiles before
-// they are written to slot-buffer half (chunk & 1), so the req_to_token read
-// latency hides under compute.
-struct SlotPrefetch {
-  int64_t v[kSlotChunk / kThreads];
+  // The phases' interface: slot ids read at one MFMA, loads issued at the
+  // next two.
+  struct Ids {
+    int32_t s[2];
+  };
+  __device__ __forceinline__ Ids fetch() const { return Ids{{slot(0), slot(1)}}; }
+  __device__ __forceinline__ void issue_part(const Ids& ids, int p) const { issue(ids.s[p], p); }
 };
 
-__device__ __forceinline__ void slot_load(const int64_t* rtt, int chunk, int kend, int tid,
-                                          SlotPrefetch& p) {
-  const int k0 = chunk * kSlotChunk;
+// fp8 pools: wave w moves the e4m3 rows of keys 4w .. 4w + 3 of `tile`, one
+// instruction for K and one for V (1 KB each); lane l fills 16-byte chunk
+// l % 16 of key 4w + l / 16, row-major in the e4m3 stage (256 bytes per key).
+struct Stager8 {
+  const uint8_t* k;     // pool bases + kv head + this lane's chunk
+  const uint8_t* v;
+  const int32_t* slots;
+  uint8_t* dst;         // e4m3 stage + this wave's 4 keys
+  uint32_t slot_bytes;
+  int32_t smax;
+  bool wrap;
+  int tile;
+  int key;              // 4w + l / 16
+
+  struct Ids {
+    int32_t s;
+  };
+  __device__ __forceinline__ Ids fetch() const {
+    return Ids{slots[(tile * kBN + key) & kSlotMask]};
+  }
+  __device__ __forceinline__ void issue_part(const Ids& ids, int p) const {
+    int32_t sl = ids.s;
+    if (wrap && sl < 0) sl += smax + 1;
+    const uint64_t off = (uint64_t)(uint32_t)min(max(sl, 0), smax) * slot_bytes;
+    if (p == 0)
+      dma16(k + off, lds_addr(dst));
+    else
+      dma16(v + off, lds_addr(dst + kF8Half));
+  }
+};
+
+// Widens the e4m3 K and V bytes this lane staged (key `key`, dims 16c .. 16c +
+// 15) into the bf16 stages, in the layouts the MFMA operand reads expect (see
+// Stager::issue): exact, every e4m3 value is a bf16 value.  Each lane reads only
+// the bytes its own load wrote, so s_waitcnt vmcnt orders it; no barrier.
+__device__ __forceinline__ void widen_tile(const uint8_t* f8, uint8_t* kdst, uint8_t* vdst,
+                                           int key, int c) {
+  const uint8_t* src = f8 + key * kD + 16 * c;
+  uint8_t* krow = kdst + (key >> 1) * kKPair + (key & 1) * kRowBytes;
+  uint8_t* vrow = vdst + key * kRowBytes;
+  const int ks = key & 1, vs = vswz(key);
 #pragma unroll
-  for (int i = 0; i < kSlotChunk / kThreads; ++i) p.v[i] = rtt[min(k0 + tid + i * kThreads, kend - 1)];
+  for (int h = 0; h < 2; ++h) {
+    const u32x2 kx = *reinterpret_cast<const u32x2*>(src + 8 * h);
+    const u32x2 vx = *reinterpret_cast<const u32x2*>(src + kF8Half + 8 * h);
+    st_s16(krow + 16 * ((2 * c + h) ^ ks), e4m3x8_to_bf16x8(kx[0], kx[1]));
+    st_s16(vrow + 16 * ((2 * c + h) ^ vs), e4m3x8_to_bf16x8(vx[0], vx[1]));
+  }
 }
 
-__device__ __forceinline__ void slot_store(const SlotPrefetch& p, int chunk, int tid,
-                                           int64_t pool_slots, bool wrap, int32_t* slots) {
-  int32_t* buf = slots + (chunk & 1) * kSlotChunk;
-#pragma unroll
-  for (int i = 0; i < kSlotChunk / kThreads; ++i)
-    buf[tid + i * kThreads] = (int32_t)pool_row(p.v[i], pool_slots, wrap);
+// ---------------------------------------------------------------- MFMAs
+// Register file: at two waves per SIMD each wave has 256 registers; O^T
+// (8 tiles x 16 fp32), Q^T (64) and S^T (16) all live in VGPRs.  This file is
+// compiled with -mllvm --amdgpu-mfma-vgpr-form=1, which makes the builtin
+// MFMAs read and write their accumulators in VGPRs, so no AGPR copies are
+// needed and the compiler sees, and spaces, every MFMA dependency itself.
+// ---------------------------------------------------------------- PV operand
+// A operand of step q4 for output dims 32 mt + n: register j of lane (g, n)
+// is V[key 16 q4 + 8 (j / 4) + 4 g + j % 4][32 mt + n], the key order in which
+// P^T leaves the S^T accumulator.  ds_read_b64_tr_b16 hands lane i of each
+// 16-lane group element i % 4 of the 8 bytes addressed by lane 4 k + (i % 16) / 4
+// as its element k, so lane L addresses V[key 4 g + (L % 16) / 4 (+8)]
+// [dims 32 mt + 16 ((L / 16) % 2) + 4 (L % 4) .. +3]; vaddr[mt % 4] holds that
+// offset (swizzle included) for q4 = 0.
+__device__ __forceinline__ u32x4 v_frag(const uint8_t* vst, const int (&vaddr)[4], int f) {
+  const int q4 = f >> 3, mt = f & 7;
+  const uint8_t* p = vst + vaddr[mt & 3] + 256 * (mt >> 2) + 16 * q4 * kRowBytes;
+  const u32x2 lo = __builtin_bit_cast(
+      u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(p)));
+  const u32x2 hi = __builtin_bit_cast(
+      u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(p + 8 * kRowBytes)));
+  return u32x4{lo[0], lo[1], hi[0], hi[1]};
 }
 
-// S^T (64 keys x 32 rows) = K_tile Q^T: s[hh][r] is key 32 hh + 8 (r / 4) + 4 g + r % 4.
-// K fragments are read kQkAhead steps ahead of the MFMAs that consume them.
-constexpr int kQkAhead = 3;
-__device__ __forceinline__ void qk_tile(const uint8_t* kst, int kread, const u32x4 (&qf)[16],
-                                        f32x16 (&s)[2]) {
-  u32x4 fr[kQkAhead + 1][2];
+// ---------------------------------------------------------------- phases
+// Each MFMA phase is one stream of 16 MFMAs with the other work placed one
+// item per MFMA (sched_barrier regions, MFMA first in each region): the
+// fragment reads kQkAhead / kPvAhead MFMAs ahead and, when the phase carries
+// the step's staging, the slot-id reads at MFMA 0 and the two K / V row pairs
+// at MFMAs 2 and 3.
+template <bool kStage, class S>
+__device__ __forceinline__ void qk_phase(const uint8_t* kst, int kaddr, const u32x4 (&qf)[16],
+                                         f32x16& s, const S& st) {
+  u32x4 fr[kQkAhead + 1];
+  __builtin_amdgcn_s_setprio(1);
 #pragma unroll
-  for (int p = 0; p < kQkAhead; ++p)
-#pragma unroll
-    for (int hh = 0; hh < 2; ++hh) fr[p][hh] = ld_s16(kst + kread + hh * 32 * kKStride + 32 * p);
-  s[0] = f32x16{};
-  s[1] = f32x16{};
+  for (int i = 0; i < kQkAhead; ++i) fr[i] = ld_s16(kst + kaddr + 32 * i);
+  typename S::Ids ids;
 #pragma unroll
   for (int kk = 0; kk < 16; ++kk) {
-    if (kk + kQkAhead < 16) {
-#pragma unroll
-      for (int hh = 0; hh < 2; ++hh)
-        fr[(kk + kQkAhead) % (kQkAhead + 1)][hh] =
-            ld_s16(kst + kread + hh * 32 * kKStride + 32 * (kk + kQkAhead));
-    }
-#pragma unroll
-    for (int hh = 0; hh < 2; ++hh) s[hh] = mfma_32x32x16(fr[kk % (kQkAhead + 1)][hh], qf[kk], s[hh]);
-  }
-  // Keep the reads kQkAhead steps ahead: the scheduler would otherwise sink
-  // them next to their MFMAs and expose the LDS latency.
-  __builtin_amdgcn_sched_group_barrier(0x100, 2 * kQkAhead, 0);
-#pragma unroll
-  for (int i = 0; i < 32 - 2 * kQkAhead; ++i) {
+    __builtin_amdgcn_sched_barrier(0);
     __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-    __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-  }
-  __builtin_amdgcn_sched_group_barrier(0x008, 2 * kQkAhead, 0);
-}
-
-// Sets the scores of keys past this lane's last visible key to -inf.
-__device__ __forceinline__ void mask_tile(f32x16 (&s)[2], int k0, int g, int limit) {
-#pragma unroll
-  for (int hh = 0; hh < 2; ++hh)
-#pragma unroll
-    for (int r = 0; r < 16; ++r)
-      if (k0 + 32 * hh + 8 * (r >> 2) + 4 * g + (r & 3) > limit) s[hh][r] = -INFINITY;
-}
-
-// Phase A of a pipelined step: S^T of tile j + 1 (as qk_tile) with the tile
-// staging spread one item per MFMA, so that LDS writes, global-load issue and
-// the V transpose overlap matrix-core work instead of stalling in a burst:
-//   MFMA 0:      slot ids of K tile kt and V tile vt from the LDS slot buffer
-//   MFMAs 0-7:   K rows in registers -> K stage k_dst (one key per MFMA)
-//   MFMAs 8-15:  V rows in registers -> transposed V^T stage v_dst (8 dims each)
-//   MFMAs 16-23: global loads of tile kt's K rows into the registers just freed
-//   MFMAs 24-31: global loads of tile vt's V rows
-template <bool FP8>
-__device__ __forceinline__ void qk_tile_staged(
-    const uint8_t* kst, int kread, const u32x4 (&qf)[16], f32x16 (&s)[2], TileRegs<FP8>& r,
-    uint8_t* k_dst, uint8_t* v_dst, int run0, int grp, int c, const int32_t* slots,
-    const uint8_t* kb, const uint8_t* vb, uint32_t lane_off, int64_t slot_bytes, int kt, int vt) {
-  u32x4 fr[kQkAhead + 1][2];
-#pragma unroll
-  for (int p = 0; p < kQkAhead; ++p)
-#pragma unroll
-    for (int hh = 0; hh < 2; ++hh) fr[p][hh] = ld_s16(kst + kread + hh * 32 * kKStride + 32 * p);
-  s[0] = f32x16{};
-  s[1] = f32x16{};
-  u32x4 sk[2], sv[2];
-  u32x4 vin[8];
-  uint8_t* const kp = k_dst + run0 * kKStride + 16 * c;
-  const int y = (grp ^ c) & 7;
-  uint8_t* const vp = v_dst + 8 * c * kVtStride;
-#pragma unroll
-  for (int i = 0; i < 32; ++i) {
-    const int kk = i >> 1, hh = i & 1;
-    __builtin_amdgcn_sched_barrier(0);
-    if (hh == 0 && kk + kQkAhead < 16) {
-#pragma unroll
-      for (int h2 = 0; h2 < 2; ++h2)
-        fr[(kk + kQkAhead) % (kQkAhead + 1)][h2] =
-            ld_s16(kst + kread + h2 * 32 * kKStride + 32 * (kk + kQkAhead));
-    }
-    s[hh] = mfma_32x32x16(fr[kk % (kQkAhead + 1)][hh], qf[kk], s[hh]);
-    if (i == 0) {
-      const int kk0 = kt * kBN + run0, vk0 = vt * kBN + run0;
-      sk[0] = *reinterpret_cast<const u32x4*>(slots + (kk0 & kSlotMask));
-      sk[1] = *reinterpret_cast<const u32x4*>(slots + ((kk0 + 8) & kSlotMask));
-      sv[0] = *reinterpret_cast<const u32x4*>(slots + (vk0 & kSlotMask));
-      sv[1] = *reinterpret_cast<const u32x4*>(slots + ((vk0 + 8) & kSlotMask));
-    }
-    if (i < 8) {
-      st_s16(kp + run_key(i) * kKStride,
-             FP8 ? e4m3x8_to_bf16x8(r.k[i][0], r.k[i][1]) : r.k[i]);
-    } else if (i < 16) {
-      const int d = i - 8;
-      if (d == 0) {
-#pragma unroll
-        for (int j = 0; j < 8; ++j) vin[j] = FP8 ? e4m3x8_to_bf16x8(r.v[j][0], r.v[j][1]) : r.v[j];
-      }
-      u32x4 o;
-#pragma unroll
-      for (int w = 0; w < 4; ++w) o[w] = pair_sel(vin[2 * w + 1][d >> 1], vin[2 * w][d >> 1], d & 1);
-      st_s16(vp + d * kVtStride + 16 * (y ^ d), o);
-    } else if (i < 24) {
-      const int j = i - 16;
-      const int64_t off = (int64_t)(j < 4 ? sk[0][j] : sk[1][j - 4]) * slot_bytes + lane_off;
-      if (FP8) {
-        const u32x2 x = ld_g8(kb + off);
-        r.k[j] = u32x4{x[0], x[1], 0u, 0u};
-      } else {
-        r.k[j] = ld_g16(kb + off);
-      }
-    } else {
-      const int j = i - 24;
-      const int64_t off = (int64_t)(j < 4 ? sv[0][j] : sv[1][j - 4]) * slot_bytes + lane_off;
-      if (FP8) {
-        const u32x2 x = ld_g8(vb + off);
-        r.v[j] = u32x4{x[0], x[1], 0u, 0u};
-      } else {
-        r.v[j] = ld_g16(vb + off);
-      }
+    __builtin_amdgcn_sched_group_barrier(0x7f7, 64, 0);
+    if (kk + kQkAhead < 16)
+      fr[(kk + kQkAhead) % (kQkAhead + 1)] = ld_s16(kst + kaddr + 32 * (kk + kQkAhead));
+    s = mfma_32x32x16(fr[kk % (kQkAhead + 1)], qf[kk], kk == 0 ? f32x16{} : s);
+    if (kStage) {
+      if (kk == 0)
+        ids = st.fetch();
+      else if (kk == 2 || kk == 3)
+        st.issue_part(ids, kk - 2);
     }
   }
   __builtin_amdgcn_sched_barrier(0);
 }
 
-// Online softmax of one tile's scores (raw, unscaled) for this lane's row, in
-// two halves so that the rare accumulator rescale can sit between them and the
-// exps stay in the same scheduling region as the PV MFMAs that consume them.
-//
-// softmax_max: the row max over the tile; the reference max m is raised only
-// when some row of the wave outgrew it by more than 2^kRescaleLog2 (returns
-// true, wave-uniform, with alpha = the factor for the accumulator and l).
-__device__ __forceinline__ bool softmax_max(const f32x16 (&s)[2], float& m, float& l, float sl2,
-                                            float& alpha) {
-  float mx = s[0][0];
-#pragma unroll
-  for (int r = 1; r < 16; ++r) mx = fmaxf(mx, s[0][r]);
-#pragma unroll
-  for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[1][r]);
-  mx = wave_max_xor(mx, 32);
-  const bool grow = (mx - m) * sl2 > kRescaleLog2;
-  const bool any = __ballot(grow) != 0;
-  const float mnew = any ? fmaxf(m, mx) : m;
-  alpha = any ? fast_exp2((m - mnew) * sl2) : 1.f;
-  l *= alpha;
-  m = mnew;
-  return any;
-}
-
-// Exp half of the softmax fused with O^T += V^T P^T.
-//
-// p = 2^(s sl2 - m sl2) for the tile's 32 scores of this lane, l += sum p, and
-// P^T packed as the B operands of four 16-key steps: step q4 takes scores
-// 8 q4 .. 8 q4 + 7 (keys 16 q4 + 8 (j / 4) + 4 g + j % 4), and its A operand for
-// output dims 32 mt + n is V^T row 32 mt + n, positions 16 q4 + 8 g .. +8.
-// The exps of step q4 + 1 are issued one per MFMA of step q4, and the V^T
-// reads kPvAhead MFMAs ahead; scheduling barriers keep that order.
-constexpr int kPvAhead = 6;
-__device__ __forceinline__ void exp_pv_tile(const uint8_t* vst, const int (&vb)[4][2],
-                                            const f32x16 (&s)[2], float m, float& l,
-                                            float sl2, f32x16 (&acc)[8]) {
-  const float moff = m == -INFINITY ? 0.f : m * sl2;
-  float p[32];
-  u32x4 pt[4];
-  auto ex = [&](int i) { p[i] = fast_exp2(fmaf(s[i >> 4][i & 15], sl2, -moff)); };
-  auto pack = [&](int q4) {
-#pragma unroll
-    for (int k = 0; k < 4; ++k) pt[q4][k] = pack_bf16(p[8 * q4 + 2 * k], p[8 * q4 + 2 * k + 1]);
-  };
-  auto vread = [&](int i) {
-    return ld_s16(vst + vb[i / 8][i & 1] + 32 * kVtStride * (i % 8));
-  };
+template <bool kStage, class S>
+__device__ __forceinline__ void pv_phase(const uint8_t* vst, const int (&vaddr)[4],
+                                         f32x16 (&acc)[8], const u32x4 (&pt)[2],
+                                         const S& st) {
   u32x4 fr[kPvAhead + 1];
+  __builtin_amdgcn_s_setprio(0);
 #pragma unroll
-  for (int i = 0; i < kPvAhead; ++i) fr[i] = vread(i);
+  for (int f = 0; f < kPvAhead; ++f) fr[f] = v_frag(vst, vaddr, f);
+  typename S::Ids ids;
 #pragma unroll
-  for (int i = 0; i < 8; ++i) ex(i);
-  pack(0);
-#pragma unroll
-  for (int i = 0; i < 32; ++i) {
+  for (int f = 0; f < 16; ++f) {
     __builtin_amdgcn_sched_barrier(0);
-    acc[i % 8] = mfma_32x32x16(fr[i % (kPvAhead + 1)], pt[i / 8], acc[i % 8]);
-    if (i + kPvAhead < 32) fr[(i + kPvAhead) % (kPvAhead + 1)] = vread(i + kPvAhead);
-    if (i < 24) {
-      ex(8 + i);
-      if (i % 8 == 7) pack(i / 8 + 1);
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+    __builtin_amdgcn_sched_group_barrier(0x7f7, 64, 0);
+    if (f + kPvAhead < 16) fr[(f + kPvAhead) % (kPvAhead + 1)] = v_frag(vst, vaddr, f + kPvAhead);
+    acc[f & 7] = mfma_32x32x16(fr[f % (kPvAhead + 1)], pt[f >> 3], acc[f & 7]);
+    if (kStage) {
+      if (f == 0)
+        ids = st.fetch();
+      else if (f == 2 || f == 3)
+        st.issue_part(ids, f - 2);
     }
   }
   __builtin_amdgcn_sched_barrier(0);
-  float ps[4] = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-  for (int i = 0; i < 32; ++i) ps[i & 3] += p[i];
-  l += (ps[0] + ps[1]) + (ps[2] + ps[3]);
 }
 
-// Multiplies an accumulator tile held in AGPRs by a per-lane factor one
-// register at a time, so the tile never has to live in VGPRs.
-__device__ __forceinline__ void scale_acc(f32x16& x, float f) {
+// ---------------------------------------------------------------- softmax
+// Softmax state of the lane's row: reference max m (raw score units),
+// moff = m * sl2, running sum l of p = 2^(s sl2 - moff) (this lane's half).
+struct Row {
+  float m, moff, l;
+};
+
+__device__ __forceinline__ void mask_tile(f32x16& s, int k0, int g, int limit) {
 #pragma unroll
-  for (int i = 0; i < 16; ++i) {
-    float e = x[i];
-    float tmp;
-    asm volatile(
-        "v_accvgpr_read_b32 %1, %0\n\t"
-        "v_mul_f32 %1, %1, %2\n\t"
-        "v_accvgpr_write_b32 %0, %1"
-        : "+a"(e), "=&v"(tmp)
-        : "v"(f));
-    x[i] = e;
+  for (int r = 0; r < 16; ++r)
+    if (k0 + 8 * (r >> 2) + 4 * g + (r & 3) > limit) s[r] = -INFINITY;
+}
+
+// Max of lanes n and n + 32 (the two halves of a row's scores).
+__device__ __forceinline__ float half_swap_max(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false,
+                                                  false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+
+// Row max of the tile, the lazy reference-max update, and P^T packed to bf16:
+// pt[q4] holds p for keys 16 q4 + 8 (j / 4) + 4 g + j % 4, two per dword, the
+// B operand of PV step q4.  Returns whether any row of the wave raised its
+// reference max (alpha is then the lane's factor for the accumulators).
+__device__ __forceinline__ bool softmax_tile(const f32x16& s, Row& row, float sl2,
+                                             u32x4 (&pt)[2], float& alpha) {
+  float mx = s[0];
+#pragma unroll
+  for (int r = 1; r < 16; ++r) mx = fmaxf(mx, s[r]);
+  mx = half_swap_max(mx);
+  // Lazy reference max, per row: raised only when the row outgrew it by more
+  // than 2^kRescaleLog2.  The wave-wide vote only decides whether the rescale
+  // runs at all.
+  const bool grow = (mx - row.m) * sl2 > kRescaleLog2;
+  const float mnew = grow ? mx : row.m;
+  alpha = grow ? fast_exp2((row.m - mnew) * sl2) : 1.f;
+  row.l *= alpha;
+  row.m = mnew;
+  row.moff = mnew * sl2;
+#pragma unroll
+  for (int q4 = 0; q4 < 2; ++q4) {
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const float p0 = fast_exp2(fmaf(s[8 * q4 + 2 * k], sl2, -row.moff));
+      const float p1 = fast_exp2(fmaf(s[8 * q4 + 2 * k + 1], sl2, -row.moff));
+      pt[q4][k] = pack_bf16(p0, p1);
+      row.l += p0 + p1;
+    }
   }
+  return __ballot(grow) != 0;
 }
 
 template <bool FP8>
-__global__ void __launch_bounds__(kThreads)
-extend_kernel(ExtendArgs a) {
-  __shared__ ExtendSmem sm;
+__global__ void __launch_bounds__(kThreads) extend_mfma_kernel(ExtendArgs a) {
+  __shared__ Smem<FP8> sm;
+  constexpr int kKS = kStagesOf<FP8>, kVS = kVStagesOf<FP8>;
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -400,11 +407,10 @@ extend_kernel(ExtendArgs a) {
   const int g = lane >> 5;
   const int n = lane & 31;
 
-  // Two workgroups per 256-row work item, 128 rows each.
-  const int32_t* wk = a.work + 8 * (int64_t)(blockIdx.x >> 1);
+  const int32_t* wk = a.work + 8 * (int64_t)blockIdx.x;
   const int b = wk[0];
   const int hk = wk[1];
-  const int row0 = wk[2] + kWaves * kRowsPerWave * (int)(blockIdx.x & 1);
+  const int row0 = wk[2];
   const int q_start = wk[3];
   const int ext = wk[4];
   const int G = a.group;
@@ -420,141 +426,237 @@ extend_kernel(ExtendArgs a) {
   const int64_t rrow = clamp_i64(a.rpi[b], 0, a.rtt_rows - 1);
   const int64_t* rtt = a.rtt + rrow * a.rtt_stride;
 
-  // This lane's row; padding lanes (row_ok false) compute a valid duplicate row
-  // and never write it.
-  const int rho = row0 + kRowsPerWave * w + n;
-  const bool row_ok = rho < rows_total;
-  const int t = row_ok ? rho / G : ext - 1;
-  const int h = row_ok ? rho - t * G : 0;
-  const int limit = P + t;  // last visible key
+  // This lane's row; padding lanes compute a valid duplicate row and never
+  // write it.
+  const int rho_c = min(row0 + kRowsPerWave * w + n, rows_total - 1);
+  const int limit = P + rho_c / G;   // last visible key
 
-  // Keys [0, kend) are needed by the block; keys below w_full are visible to
-  // every row of this wave.
-  const int blk_last_row = min(row0 + kWaves * kRowsPerWave, rows_total) - 1;
+  // Keys [0, kend) are needed by the item; keys below w_full are visible to
+  // every row of this wave. Every wave runs all n_tiles tiles (keys past a
+  // row's limit are masked; key 0 is visible to every row, so each row's max
+  // is finite after tile 0).
+  const int blk_last_row = min(row0 + kExtendItemRows, rows_total) - 1;
   const int kend = min(L, P + blk_last_row / G + 1);
   if (kend <= 0) return;
   const int n_tiles = (kend + kBN - 1) / kBN;
-  // Every wave runs all n_tiles tiles (keys past a row's limit are masked, and
-  // key 0 is visible to every row, so each row's max is finite after tile 0).
+  const int last = n_tiles - 1;
   const int w_first = row0 + kRowsPerWave * w;
   const int w_full = w_first < rows_total ? P + w_first / G + 1 : 0;
 
-  const float kscale = FP8 ? a.k_scale[0] : 1.f;
-  const float vscale = FP8 ? a.v_scale[0] : 1.f;
-  const float sl2 = a.scale_log2 * kscale;
+  // fp8 pools: scores and outputs are computed from the e4m3 values and
+  // scaled by k_scale / v_scale (folded into the exponent scale and 1 / l).
+  const float sl2 = FP8 ? a.scale_log2 * a.k_scale[0] : a.scale_log2;
+  typename std::conditional<FP8, Stager8, Stager>::type st;
+  if constexpr (FP8) {
+    st.k = a.k_pool + (int64_t)hk * kD + 16 * (lane & 15);
+    st.v = a.v_pool + (int64_t)hk * kD + 16 * (lane & 15);
+    st.slot_bytes = (uint32_t)a.hkv * kD;
+    st.key = 4 * w + (lane >> 4);
+  } else {
+    st.sb = stage_bases(a.k_pool + (int64_t)hk * kRowBytes,
+                        a.v_pool + (int64_t)hk * kRowBytes, lane);
+    st.slot_bytes = (uint32_t)a.hkv * kRowBytes;
+    st.w = w;
+    st.g = g;
+  }
+  st.slots = sm.slots;
+  st.smax = (int32_t)min(a.pool_slots - 1, (int64_t)INT32_MAX);
+  st.wrap = a.seq_override > 0;
+  auto stage_at = [&](int tile, int j) {   // tile `tile` into the stages of step j
+    st.tile = tile;
+    if constexpr (FP8) {
+      st.dst = sm.f8 + (j & 1) * kF8Stage + 4 * w * kD;
+    } else {
+      st.k_dst = sm.k + (j % kKS) * kKStage;
+      st.v_dst = sm.v + (j % kVS) * kVStage;
+    }
+  };
+  auto stage_for = [&](int j) { stage_at(min(j + kAhead, last), j + kAhead); };
+  // fp8: tile t's e4m3 rows (issued one step earlier) widened into the bf16
+  // stages; only this lane's own loads need to have landed.
+  auto widen = [&](int t) {
+    if constexpr (FP8) {
+      if (t <= last) {
+        vm_wait_staged<true>();
+        widen_tile(sm.f8 + (t & 1) * kF8Stage, sm.k + (t % kKS) * kKStage,
+                   sm.v + (t % kVS) * kVStage, 4 * w + (lane >> 4), lane & 15);
+      }
+    }
+  };
 
-  // Gather mapping.
-  const int grp = tid >> 5;
-  const int c = tid & 31;
-  const int run0 = 16 * (grp >> 1) + 4 * (grp & 1);
-  constexpr int kRowBytes = FP8 ? kD : 2 * kD;
-  const int64_t slot_bytes = (int64_t)a.hkv * kRowBytes;
-  const uint8_t* kb = a.k_pool + (int64_t)hk * kRowBytes;
-  const uint8_t* vb = a.v_pool + (int64_t)hk * kRowBytes;
-  const uint32_t lane_off = (FP8 ? 8 : 16) * c;
-
-  // LDS read offsets of this lane.
-  const int kread = n * kKStride + 16 * g;
-  int vbo[4][2];
+  // LDS read offsets of this lane (see Stager::issue / v_frag).
+  const int kaddr = (n >> 1) * kKPair + (n & 1) * kRowBytes + 16 * (g ^ (n & 1));
+  int vaddr[4];
   {
-    const int z = (n ^ (n >> 3)) & 7;
+    const int s16 = lane & 15;
+    const int r = s16 >> 2;                    // key within the 4-key group
+    const int sw = vswz(r);
+    const int c = 2 * ((lane >> 4) & 1) + ((s16 & 3) >> 1);
+    const int base = (4 * g + r) * kRowBytes + 16 * (c ^ (sw & 3)) + 8 * (s16 & 1);
 #pragma unroll
-    for (int q4 = 0; q4 < 4; ++q4)
-#pragma unroll
-      for (int p = 0; p < 2; ++p) vbo[q4][p] = n * kVtStride + 16 * (((2 * q4 + g) ^ z ^ (4 * p)) & 7);
+    for (int m2 = 0; m2 < 4; ++m2) vaddr[m2] = base + 64 * (m2 ^ (sw >> 2));
   }
 
+  // Q: the wave's 32 rows (padding rows repeat the last real row) are loaded
+  // row-contiguously, lane L taking 16-byte chunk L % 32 of row 2 i + L / 32,
+  // together with the slot ids of the first 1024 keys.
+  uint8_t* const my_rows = sm.rows[w];
+  {
+    u32x4 qv[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int r = 2 * i + g;
+      const int rho = min(row0 + kRowsPerWave * w + r, rows_total - 1);
+      const int t = rho / G, h = rho - t * G;
+      qv[i] = ld_g16(a.q + (int64_t)(q_start + t) * a.q_stride + (int64_t)(hk * G + h) * kD + 8 * n);
+    }
+    slot_issue(rtt, 0, kend, w, lane, sm.slots);
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int r = 2 * i + g;
+      st_s16(my_rows + r * kRowBytes + 16 * swz_chunk(r, n), qv[i]);
+    }
+  }
   // Q^T fragments: lane (g, n) holds q[row n][16 kk + 8 g .. +8].
   u32x4 qf[16];
-  {
-    const __bf16* qp = a.q + (int64_t)(q_start + t) * a.q_stride + (int64_t)(hk * G + h) * kD;
 #pragma unroll
-    for (int kk = 0; kk < 16; ++kk) qf[kk] = ld_g16(qp + 16 * kk + 8 * g);
-  }
+  for (int kk = 0; kk < 16; ++kk)
+    qf[kk] = ld_s16(my_rows + n * kRowBytes + 16 * swz_chunk(n, 2 * kk + g));
+  // Consume Q here so that the compiler waits for these reads before the
+  // loop; inside it, vmcnt belongs to the staging loads.
+#pragma unroll
+  for (int kk = 0; kk < 16; ++kk) asm volatile("" ::"v"(qf[kk]));
 
-  float m = -INFINITY;
-  float l = 0.f;
+  Row row{-INFINITY, 0.f, 0.f};
   f32x16 acc[8];
 #pragma unroll
   for (int i = 0; i < 8; ++i) acc[i] = f32x16{};
 
-  uint8_t* const kst0 = sm.k;
-  uint8_t* const kst1 = sm.k + kKStage;
-  uint8_t* const vst0 = sm.vt;
-  uint8_t* const vst1 = sm.vt + kVtStage;
-
-  // ---- prologue: K(0), K(1), V(0) in LDS; K(2) and V(1) in registers; S(0)
-  // computed. Tiles past the last one are stand-ins for the last tile (its
-  // slots are staged, so every load stays inside the pool) and are never read.
-  SlotPrefetch spf;
-  slot_load(rtt, 0, kend, tid, spf);
-  slot_store(spf, 0, tid, a.pool_slots, a.seq_override > 0, sm.slots);
+  // ---- prologue: the slot ids (issued with Q) land, every wave has its Q
+  // out of the shared rows, then tiles 0 and 1 go into stages 0 and 1. Tiles
+  // past the last one are stand-ins for the last tile (its slots are staged,
+  // so every load stays inside the pool) and are never read.
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
-  const int last = n_tiles - 1;
-  TileRegs<FP8> regs;
-  gather_tile<FP8>(sm.slots, kb, vb, lane_off, slot_bytes, 0, run0, regs);
-  store_k<FP8>(kst0, run0, c, regs);
-  store_vt<FP8>(vst0, grp, c, regs);
-  gather_tile<FP8>(sm.slots, kb, vb, lane_off, slot_bytes, min(1, last) * kBN, run0, regs);
-  store_k<FP8>(kst1, run0, c, regs);
-  gather_k<FP8>(sm.slots, kb, lane_off, slot_bytes, min(2, last) * kBN, run0, regs);
-  __syncthreads();
-
-  f32x16 sa[2];
-  qk_tile(kst0, kread, qf, sa);
-
-  // Step j: phase A computes S^T of tile j + 1 while K(j + 2) and V(j + 1)
-  // move from registers to LDS and the loads of K(j + 3) and V(j + 2) are
-  // issued; phase B is the softmax and PV of tile j. One barrier per step.
-  for (int j = 0; j < n_tiles; ++j) {
-    const int odd = j & 1;
-    uint8_t* const k_this = odd ? kst1 : kst0;   // K(j) stage, gets K(j + 2)
-    uint8_t* const k_next = odd ? kst0 : kst1;   // K(j + 1)
-    uint8_t* const v_this = odd ? vst1 : vst0;   // V(j)
-    uint8_t* const v_next = odd ? vst0 : vst1;   // gets V(j + 1)
-
-    // Slot ids of the next 1024 keys: loaded at tile 4 of a chunk, written at
-    // tile 8, first read by the loads issued at tile 13.
-    if ((j / kTilesPerSlotChunk + 1) * kSlotChunk < kend) {
-      if (j % kTilesPerSlotChunk == 4) slot_load(rtt, j / kTilesPerSlotChunk + 1, kend, tid, spf);
-      if (j % kTilesPerSlotChunk == 8)
-        slot_store(spf, j / kTilesPerSlotChunk + 1, tid, a.pool_slots, a.seq_override > 0, sm.slots);
-    }
-    const int k0 = j * kBN;
-    if (k0 + kBN > w_full) mask_tile(sa, k0, g, limit);
-    f32x16 sn[2];
-    qk_tile_staged<FP8>(k_next, kread, qf, sn, regs, k_this, v_next, run0, grp, c, sm.slots,
-                        kb, vb, lane_off, slot_bytes, min(j + 3, last), min(j + 2, last));
-    float alpha;
-    if (softmax_max(sa, m, l, sl2, alpha)) {
 #pragma unroll
-      for (int i = 0; i < 8; ++i) scale_acc(acc[i], alpha);
-    }
-    exp_pv_tile(v_this, vbo, sa, m, l, sl2, acc);
-    sa[0] = sn[0];
-    sa[1] = sn[1];
-    __syncthreads();
+  for (int tl = 0; tl < kAhead; ++tl) {
+    stage_at(min(tl, last), tl);
+    const auto ids = st.fetch();
+#pragma unroll
+    for (int p = 0; p < 2; ++p) st.issue_part(ids, p);
   }
+  widen(0);
+  vm_wait_staged<FP8>();
+  __syncthreads();
 
-  if (!row_ok) return;
-  l += __shfl_xor(l, 32, kWave);
-  const float inv = vscale / l;
-  __bf16* o = a.out + (int64_t)(q_start + t) * a.out_stride + (int64_t)(hk * G + h) * kD;
-  const __bf16* gt = a.gate ? a.gate + (int64_t)(q_start + t) * a.gate_stride +
-                                  (int64_t)(hk * G + h) * a.gate_hstride
-                            : nullptr;
+  // bf16: K tile t lives in K stage t % 3, V tile t in V stage t % 4.
+  // Between barriers j - 1 and j every wave stages tile j + 2; lead waves read
+  // K(j) and V(j), trailing waves V(j - 1) and K(j).  The stages tile j + 2
+  // overwrites held tiles j - 1 (K) and j - 2 (V), whose last reads came
+  // before barrier j - 1.
+  // fp8: e4m3 tile t lives in e4m3 stage t % 2, its widened rows in K stage
+  // t % 2 and V stage t % 3.  Between barriers j - 1 and j every wave stages
+  // tile j + 2 (over tile j, widened before barrier j - 1) and widens tile
+  // j + 1 (over K(j - 1) and V(j - 2), last read before barrier j - 1).
+  f32x16 s;
+  u32x4 pt[2];
+  float alpha;
+  auto slot_chunk = [&](int j) {
+    // Slot ids of the next 1024 keys: issued at tile 4 of chunk c into the
+    // half that served chunk c - 1 (last read when tile 32 c - 1 was staged,
+    // before barrier 32 c - 3), first read when tile 32 (c + 1) is staged.
+    if (j % kTilesPerSlotChunk == 4 && (j / kTilesPerSlotChunk + 1) * kSlotChunk < kend)
+      slot_issue(rtt, j / kTilesPerSlotChunk + 1, kend, w, lane, sm.slots);
+  };
+  // Softmax of tile j; `grew` records whether a row's reference max was
+  // raised, and rescale() then scales O^T, which must hold exactly the tiles
+  // before j (it runs right before PV(j)).
+  bool grew = false;
+  auto softmax_step = [&](int j) {
+    const int k0 = j * kBN;
+    if (k0 + kBN > w_full) mask_tile(s, k0, g, limit);
+    grew = softmax_tile(s, row, sl2, pt, alpha) && j > 0;
+  };
+  auto rescale = [&]() {
+    if (grew) {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) acc[i] *= alpha;
+    }
+  };
+  auto step_end = [&]() {
+    // Tile j + 1 was issued one step earlier: only this step's tile loads
+    // may still be in flight.
+    vm_wait_staged<FP8>();
+    __syncthreads();
+  };
+
+  if (w < kLeadWaves) {
+    for (int j = 0; j < n_tiles; ++j) {
+      slot_chunk(j);
+      stage_for(j);
+      qk_phase<true>(sm.k + (j % kKS) * kKStage, kaddr, qf, s, st);
+      softmax_step(j);
+      widen(j + 1);
+      rescale();
+      pv_phase<false>(sm.v + (j % kVS) * kVStage, vaddr, acc, pt, st);
+      step_end();
+    }
+  } else {
+    stage_for(0);
+    qk_phase<true>(sm.k, kaddr, qf, s, st);
+    widen(1);
+    softmax_step(0);
+    step_end();
+    for (int j = 1; j < n_tiles; ++j) {
+      slot_chunk(j);
+      stage_for(j);
+      rescale();
+      pv_phase<true>(sm.v + ((j - 1) % kVS) * kVStage, vaddr, acc, pt, st);
+      qk_phase<false>(sm.k + (j % kKS) * kKStage, kaddr, qf, s, st);
+      widen(j + 1);
+      softmax_step(j);
+      step_end();
+    }
+    rescale();
+    pv_phase<false>(sm.v + (last % kVS) * kVStage, vaddr, acc, pt, st);
+  }
+  // The last steps staged stand-in tiles nobody reads; they must land (and
+  // every wave must be done with the stages) before the stage memory holds
+  // the output rows.
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+
+  // Output: O^T / l into the wave's rows in LDS (lane (g, n) holds dims
+  // 32 mt + 8 rq + 4 g .. +3 of row n), then row-contiguous 16-byte stores
+  // (with the output gate), lane L writing chunk L % 32 of row 2 i + L / 32.
+  const float inv = (FP8 ? a.v_scale[0] : 1.f) / (row.l + __shfl_xor(row.l, 32, kWave));
+  const int ln = opaque(lane);   // lane coordinates recomputed here, see opaque()
+  const int ne = ln & 31, ge = ln >> 5;
 #pragma unroll
   for (int mt = 0; mt < 8; ++mt) {
 #pragma unroll
     for (int rq = 0; rq < 4; ++rq) {
-      const int off = 32 * mt + 8 * rq + 4 * g;
-      u32x2 v = {pack_bf16(acc[mt][4 * rq + 0] * inv, acc[mt][4 * rq + 1] * inv),
-                 pack_bf16(acc[mt][4 * rq + 2] * inv, acc[mt][4 * rq + 3] * inv)};
-      if (gt) {
-        const u32x2 gv = ld_g8(gt + off);
-        v = u32x2{gate_pair(v[0], gv[0]), gate_pair(v[1], gv[1])};
+      const u32x2 v = {pack_bf16(acc[mt][4 * rq + 0] * inv, acc[mt][4 * rq + 1] * inv),
+                       pack_bf16(acc[mt][4 * rq + 2] * inv, acc[mt][4 * rq + 3] * inv)};
+      st_s8(my_rows + ne * kRowBytes + 16 * swz_chunk(ne, 4 * mt + rq) + 8 * ge, v);
+    }
+  }
+  const int rho0 = row0 + kRowsPerWave * w + ge;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const int r = 2 * i + ge;
+    const int rho = rho0 + 2 * i;
+    if (rho < rows_total) {
+      u32x4 v = ld_s16(my_rows + r * kRowBytes + 16 * swz_chunk(r, ne));
+      const int t = rho / G, h = rho - t * G;
+      if (a.gate) {
+        const u32x4 gv = ld_g16(a.gate + (int64_t)(q_start + t) * a.gate_stride +
+                                (int64_t)(hk * G + h) * a.gate_hstride + 8 * ne);
+#pragma unroll
+        for (int k = 0; k < 4; ++k) v[k] = gate_pair(v[k], gv[k]);
       }
-      *reinterpret_cast<u32x2*>(o + off) = v;
+      *reinterpret_cast<u32x4*>(a.out + (int64_t)(q_start + t) * a.out_stride +
+                                (int64_t)(hk * G + h) * kD + 8 * ne) = v;
     }
   }
 }
@@ -633,8 +735,9 @@ extern "C" int32_t tf_attn_extend(const void* q, int64_t q_row_stride, const voi
 
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   if (kv_dtype == TF_DTYPE_FP8_E4M3)
-    hipLaunchKernelGGL(extend_kernel<true>, dim3(2u * (unsigned)n_work), dim3(kThreads), 0, s, a);
+    hipLaunchKernelGGL(extend_mfma_kernel<true>, dim3((unsigned)n_work), dim3(kThreads), 0, s, a);
   else
-    launch_extend_bf16(a, n_work, s);
+    hipLaunchKernelGGL(extend_mfma_kernel<false>, dim3((unsigned)n_work), dim3(kThreads), 0, s, a);
   return launch_status("tf_attn_extend launch");
 }
+

@@ -54,7 +54,5 @@ struct ExtendArgs {
   const __bf16* gate;             // optional output gate (NULL: none)
   int64_t gate_stride, gate_hstride;
 };
-// bf16 pool: one 256-thread workgroup per work item (extend_bf16.hip).
-void launch_extend_bf16(const ExtendArgs& a, int32_t n_work, hipStream_t stream);
 
 }  // namespace tfa
