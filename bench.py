@@ -235,6 +235,9 @@ def bench_prep(torch, args):
     q = qg[:, :, :d]
     fn = lambda: qk_norm_rope_kv_write(q, k, v, qw, kw, 1e-6, pos, invf, 64, [11, 11, 10],
                                        True, kp, vp, loc, out=out)
+    for _ in range(max(1, args.warmup)):
+        fn()
+    torch.cuda.synchronize()
     k_ms = time_kernel(torch, [None], args.steps, lambda c: fn())
     # read q, k, v and positions / slots; write q_out, K, V rows
     nbytes = T * ((hq + 2 * hkv) * d * 2 * 2 + 16)

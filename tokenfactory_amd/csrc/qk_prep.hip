@@ -83,16 +83,59 @@ __device__ __forceinline__ int mrope_row(const PrepArgs& a, int i) {
   return i < a.sec0 ? 0 : (i < a.sec0 + a.sec1 ? 1 : 2);
 }
 
-// One workgroup per token: the bf16 cos / sin of the token's rotary_dim / 2
-// frequencies are computed once into LDS; each wave instruction then covers two
-// rows (lanes 0-31 and 32-63, 16 bytes = 8 elements per lane), and the 4 waves
-// take the token's rows in pairs, all loads of a group issued before use.
-constexpr int kRowGroup = 4;   // row pairs per wave in flight
+// One wave per token, four waves per workgroup.  A token's rows (Hq q heads,
+// then Hkv k heads, then Hkv v heads) are taken 8 at a time ("groups"): lane l
+// works on row 8g + l / 8 and, in load j (j = 0..3), on the 8 elements
+// 64 j + 8 (l % 8) .. +7 of it, so one 16-byte load per lane covers 8 rows and
+// a row's sum of squares is reduced over 8 lanes with three DPP steps.  The
+// rotary part of every row (its first rotary_dim elements) then fills whole
+// loads, so the RoPE arithmetic runs on full waves; the rotate-half partner
+// of a chunk comes from a wave-private LDS copy of the normalised rows.  The
+// bf16 cos / sin of the token's rotary_dim / 2 frequencies are computed once
+// per token (one sincos per lane) into a wave-private LDS table.  The loads of
+// two groups (8 KB) are issued before either is used; the projection rows are
+// read once and the outputs written once, so both go through non-temporal
+// accesses (streaming, no cache reuse: 147 -> 136 us on a 20k-token step).
+constexpr int kGroupsInFlight = 2;
+constexpr int kChunks = kD / 8;                 // 16-byte chunks per row
+
+struct PrepSmem {
+  float w[2][kD];                                 // q_norm, k_norm weights
+  float tab[kWaves][2][kD / 2];                   // bf16 cos, sin per frequency
+  u32x4 rows[kWaves][8][kChunks];                 // normalised rows (RoPE partners)
+};
 
 __device__ __forceinline__ const __bf16* row_ptr(const PrepArgs& a, int64_t t, int r) {
   if (r < a.hq) return a.q + t * a.q_tok + (int64_t)r * a.q_head;
   if (r < a.hq + a.hkv) return a.k + t * a.k_tok + (int64_t)(r - a.hq) * kD;
   return a.v + t * a.v_tok + (int64_t)(r - a.hq - a.hkv) * kD;
+}
+
+// Sum over the 8 lanes of a row; every lane gets the same bits (each step adds
+// the same two operands in every lane of a pair).
+__device__ __forceinline__ float row_sum8(float v) {
+  v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(
+                                     0, __builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, false));
+  v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(
+                                     0, __builtin_bit_cast(int, v), 0x4E, 0xF, 0xF, false));
+  v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(
+                                     0, __builtin_bit_cast(int, v), 0x141, 0xF, 0xF, false));
+  return v;
+}
+
+__device__ __forceinline__ void unpack8(const u32x4& r, float (&x)[8]) {
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    x[2 * k] = __uint_as_float(r[k] << 16);
+    x[2 * k + 1] = __uint_as_float(r[k] & 0xffff0000u);
+  }
+}
+
+__device__ __forceinline__ u32x4 pack8(const float (&x)[8]) {
+  u32x4 o;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) o[k] = pack_bf16(x[2 * k], x[2 * k + 1]);
+  return o;
 }
 
 __global__ void __launch_bounds__(kThreads)
@@ -101,110 +144,142 @@ qk_prep_kernel(PrepArgs a) {
   // rounds) before it is added: no fused multiply-adds, which would skip the
   // reference's intermediate bf16 rounding of y c and rot s.
 #pragma clang fp contract(off)
-  __shared__ float cs[2][kD / 2];
+  __shared__ PrepSmem sm;
   const int lane = threadIdx.x & 63;
-  const int l = lane & 31;            // 8 elements 8l .. 8l + 7 of the row
-  const int half = lane >> 5;         // which row of the pair
   const int w = wave_id();
-  const int64_t t = blockIdx.x;
+  const int rsub = lane >> 3;         // row of the group
+  const int col = lane & 7;           // chunk column: chunk 8 j + col in load j
   const int rows = a.hq + 2 * a.hkv;
+  const int n_groups = (rows + 7) >> 3;
   const int h = a.rotary_dim >> 1;
+  const int hc = h >> 3;              // rotary chunks per half
+  const int rot_loads = (a.rotary_dim + 63) >> 6;
 
-  // First group's loads go out before the cos / sin work.
-  u32x4 raw[kRowGroup];
-  auto load_group = [&](int g0) {
-#pragma unroll
-    for (int k = 0; k < kRowGroup; ++k) {
-      const int r = 2 * (g0 + kWaves * k) + half;
-      if (r < rows) raw[k] = ld_g16(row_ptr(a, t, r) + 8 * l);
-    }
-  };
-  load_group(w);
-  for (int i = threadIdx.x; i < h; i += kThreads) {
-    const float pf = (float)a.pos[(int64_t)mrope_row(a, i) * a.pos_stride + t];
-    const float ang = pf * a.inv_freq[i];
-    cs[0][i] = bf16r(cosf(ang));
-    cs[1][i] = bf16r(sinf(ang));
-  }
+  for (int i = threadIdx.x; i < 2 * kD; i += kThreads)
+    sm.w[i / kD][i % kD] = (i < kD ? a.qw : a.kw)[i % kD];
   __syncthreads();
 
-  const int64_t slot = a.loc[t];
-  const bool slot_ok = slot >= 0 && slot < a.pool_slots;
-  const int hl = h >> 3;                        // lanes per rotary half
-  const bool rot_lane = l < 2 * hl;
-  const int partner = (half << 5) + (l < hl ? l + hl : l - hl);
-
-  for (int g0 = w; 2 * g0 < rows; g0 += kWaves * kRowGroup) {
-    if (g0 != w) load_group(g0);
+  for (int64_t t = (int64_t)blockIdx.x * kWaves + w; t < a.n_tokens;
+       t += (int64_t)gridDim.x * kWaves) {
+    const int64_t slot = a.loc[t];
+    const bool slot_ok = slot >= 0 && slot < a.pool_slots;
+    for (int g0 = 0; g0 < n_groups; g0 += kGroupsInFlight) {
+      u32x4 raw[kGroupsInFlight][4];
 #pragma unroll
-    for (int k = 0; k < kRowGroup; ++k) {
-      const int r = 2 * (g0 + kWaves * k) + half;
-      // Both halves of a wave run the shuffles below together; a half past
-      // the last row computes on stale data and stores nothing.
-      if (2 * (g0 + kWaves * k) >= rows) break;
-      const bool live = r < rows;
-      const int kind = !live ? 2 : (r < a.hq ? 0 : (r < a.hq + a.hkv ? 1 : 2));
-      const int head = kind == 0 ? r : (kind == 1 ? r - a.hq : r - a.hq - a.hkv);
-      float x[8];
+      for (int gi = 0; gi < kGroupsInFlight; ++gi) {
+        const int r = 8 * (g0 + gi) + rsub;
+        if (g0 + gi < n_groups && r < rows) {
+          const __bf16* src = row_ptr(a, t, r) + 8 * col;
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        x[2 * j] = __uint_as_float(raw[k][j] << 16);
-        x[2 * j + 1] = __uint_as_float(raw[k][j] & 0xffff0000u);
-      }
-      // q / k rows: RMSNorm then partial RoPE (v rows pass through; the
-      // shuffles are executed by every lane so both halves stay converged).
-      float ss = 0.f;
-#pragma unroll
-      for (int j = 0; j < 8; ++j) ss += x[j] * x[j];
-#pragma unroll
-      for (int m = 16; m >= 1; m >>= 1) ss += __shfl_xor(ss, m, kWave);
-      if (kind != 2) {
-        const float rs = rsqrtf(ss / (float)kD + a.eps);
-        const float* wt = (kind == 0 ? a.qw : a.kw) + 8 * l;
-        const f32x4 w0 = *reinterpret_cast<const f32x4*>(wt);
-        const f32x4 w1 = *reinterpret_cast<const f32x4*>(wt + 4);
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          x[j] = bf16r(w0[j] * (x[j] * rs));
-          x[4 + j] = bf16r(w1[j] * (x[4 + j] * rs));
+          for (int j = 0; j < 4; ++j) raw[gi][j] = ld_nt16(src + 64 * j);
         }
       }
-      float p[8];
-#pragma unroll
-      for (int j = 0; j < 8; ++j) p[j] = __shfl(x[j], rot_lane ? partner : lane, kWave);
-      if (kind != 2 && rot_lane) {
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          const int e = 8 * l + j;
-          const int i = e < h ? e : e - h;
-          const float rot = e < h ? -p[j] : p[j];
-          x[j] = bf16r(bf16r(x[j] * cs[0][i]) + bf16r(rot * cs[1][i]));
+      if (g0 == 0) {
+        // The token's cos / sin table, while the loads are in flight.
+        for (int i = lane; i < h; i += kWave) {
+          const float pf = (float)a.pos[(int64_t)mrope_row(a, i) * a.pos_stride + t];
+          float sn, cs;
+          sincosf(pf * a.inv_freq[i], &sn, &cs);
+          sm.tab[w][0][i] = bf16r(cs);
+          sm.tab[w][1][i] = bf16r(sn);
         }
       }
-      if (!live) continue;
-      u32x4 o;
 #pragma unroll
-      for (int j = 0; j < 4; ++j) o[j] = pack_bf16(x[2 * j], x[2 * j + 1]);
-      if (kind == 0) {
-        *reinterpret_cast<u32x4*>(a.q_out + t * a.q_out_tok + (int64_t)head * kD + 8 * l) = o;
-        continue;
-      }
-      if (!slot_ok) continue;
-      uint8_t* pool = kind == 1 ? a.k_pool : a.v_pool;
-      const int64_t base = (slot * a.hkv + head) * kD + 8 * l;  // element index
-      if (!a.fp8) {
-        *reinterpret_cast<u32x4*>(pool + base * 2) = o;
-      } else {
-        const float sc = kind == 1 ? a.k_scale[0] : a.v_scale[0];
-        u32x2 f;
+      for (int gi = 0; gi < kGroupsInFlight; ++gi) {
+        if (g0 + gi >= n_groups) break;
+        const int r = 8 * (g0 + gi) + rsub;
+        const bool live = r < rows;
+        const int kind = !live ? 2 : (r < a.hq ? 0 : (r < a.hq + a.hkv ? 1 : 2));
+        const int head = kind == 0 ? r : (kind == 1 ? r - a.hq : r - a.hq - a.hkv);
+        u32x4 o[4];
+        if (kind == 2) {
 #pragma unroll
-        for (int j = 0; j < 2; ++j) {
-          uint32_t b4 = __builtin_amdgcn_cvt_pk_fp8_f32(sat448(x[4 * j] / sc),
-                                                        sat448(x[4 * j + 1] / sc), 0u, false);
-          f[j] = __builtin_amdgcn_cvt_pk_fp8_f32(sat448(x[4 * j + 2] / sc),
-                                                 sat448(x[4 * j + 3] / sc), b4, true);
+          for (int j = 0; j < 4; ++j) o[j] = raw[gi][j];
+        } else {
+          float x[4][8];
+          float ss = 0.f;
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            unpack8(raw[gi][j], x[j]);
+#pragma unroll
+            for (int k = 0; k < 8; ++k) ss += x[j][k] * x[j][k];
+          }
+          ss = row_sum8(ss);
+          const float rs = rsqrtf(ss / (float)kD + a.eps);
+          const float* wt = sm.w[kind] + 8 * col;
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            const f32x4 w0 = *reinterpret_cast<const f32x4*>(wt + 64 * j);
+            const f32x4 w1 = *reinterpret_cast<const f32x4*>(wt + 64 * j + 4);
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+              x[j][k] = bf16r(w0[k] * (x[j][k] * rs));
+              x[j][4 + k] = bf16r(w1[k] * (x[j][4 + k] * rs));
+            }
+            o[j] = pack8(x[j]);
+          }
+          // RoPE on the rotary chunks: chunk c pairs with c + hc (c < hc) or
+          // c - hc, element 8c + k with frequency (8c + k) mod h.
+          if (rot_loads > 0) {
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+              if (j < rot_loads && 8 * j + col < 2 * hc) sm.rows[w][rsub][8 * j + col] = o[j];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+              const int c = 8 * j + col;
+              if (j < rot_loads && c < 2 * hc) {
+                const bool lo = c < hc;
+                float pv[8];
+                unpack8(sm.rows[w][rsub][lo ? c + hc : c - hc], pv);
+                const int i0 = 8 * (lo ? c : c - hc);
+                const f32x4 c0 = *reinterpret_cast<const f32x4*>(&sm.tab[w][0][i0]);
+                const f32x4 c1 = *reinterpret_cast<const f32x4*>(&sm.tab[w][0][i0 + 4]);
+                const f32x4 s0 = *reinterpret_cast<const f32x4*>(&sm.tab[w][1][i0]);
+                const f32x4 s1 = *reinterpret_cast<const f32x4*>(&sm.tab[w][1][i0 + 4]);
+#pragma unroll
+                for (int k = 0; k < 8; ++k) {
+                  const float cv = k < 4 ? c0[k] : c1[k - 4];
+                  const float sv = k < 4 ? s0[k] : s1[k - 4];
+                  const float rot = lo ? -pv[k] : pv[k];
+                  x[j][k] = bf16r(bf16r(x[j][k] * cv) + bf16r(rot * sv));
+                }
+                o[j] = pack8(x[j]);
+              }
+            }
+          }
         }
-        *reinterpret_cast<u32x2*>(pool + base) = f;
+        if (!live) continue;
+        if (kind == 0) {
+          __bf16* dst = a.q_out + t * a.q_out_tok + (int64_t)head * kD + 8 * col;
+#pragma unroll
+          for (int j = 0; j < 4; ++j)
+            __builtin_nontemporal_store(o[j], reinterpret_cast<u32x4*>(dst + 64 * j));
+          continue;
+        }
+        if (!slot_ok) continue;
+        uint8_t* pool = kind == 1 ? a.k_pool : a.v_pool;
+        const int64_t base = (slot * a.hkv + head) * kD + 8 * col;   // element index
+        if (!a.fp8) {
+#pragma unroll
+          for (int j = 0; j < 4; ++j)
+            __builtin_nontemporal_store(o[j], reinterpret_cast<u32x4*>(pool + (base + 64 * j) * 2));
+        } else {
+          const float sc = kind == 1 ? a.k_scale[0] : a.v_scale[0];
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            float x[8];
+            unpack8(o[j], x);
+            u32x2 f;
+#pragma unroll
+            for (int q = 0; q < 2; ++q) {
+              const uint32_t b4 = __builtin_amdgcn_cvt_pk_fp8_f32(
+                  sat448(x[4 * q] / sc), sat448(x[4 * q + 1] / sc), 0u, false);
+              f[q] = __builtin_amdgcn_cvt_pk_fp8_f32(sat448(x[4 * q + 2] / sc),
+                                                     sat448(x[4 * q + 3] / sc), b4, true);
+            }
+            __builtin_nontemporal_store(f, reinterpret_cast<u32x2*>(pool + base + 64 * j));
+          }
+        }
       }
     }
   }
@@ -293,8 +368,10 @@ extern "C" int32_t tf_qk_norm_rope_kv_write(
   a.k_scale = k_scale;
   a.v_scale = v_scale;
 
-  if (n_tokens > 0x7fffffff) return fail(TF_ERR_INVALID, "qk_prep: too many tokens");
-  hipLaunchKernelGGL(qk_prep_kernel, dim3((unsigned)n_tokens), dim3(kThreads), 0,
+  // One token per wave, four per workgroup.
+  const int64_t blocks = (n_tokens + kWaves - 1) / kWaves;
+  if (blocks > INT32_MAX) return fail(TF_ERR_INVALID, "qk_prep: too many tokens");
+  hipLaunchKernelGGL(qk_prep_kernel, dim3((unsigned)blocks), dim3(kThreads), 0,
                      reinterpret_cast<hipStream_t>(stream), a);
   return launch_status("tf_qk_norm_rope_kv_write launch");
 }
