@@ -309,6 +309,26 @@ def bench_oproj(torch, args):
         res[f"m{m}"] = {"gemm_ms": t_gemm, "quant_ms": t_quant, "gemm_tflops": tf,
                         "gemm_frac_of_fp8_peak": tf / FP8_PEAK_TFLOPS,
                         "gemm_gbps": wbytes / (t_gemm * 1e-3) / 1e9}
+        if m <= 512:
+            # Decode-sized calls are short enough that per-launch events add
+            # host latency: the device time per call from a graph of 20 calls
+            # (GEMM and split-K reduction kernels back to back).
+            side = torch.cuda.Stream()
+            side.wait_stream(torch.cuda.current_stream())
+            with torch.cuda.stream(side):
+                gemm(None)
+            torch.cuda.current_stream().wait_stream(side)
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graph, stream=side):
+                for _ in range(20):
+                    gemm(None)
+            t_graph = time_steps(torch, [None], 5, 2, lambda c: [graph.replay]) / 20
+            res[f"m{m}"].update({"gemm_graph_ms": t_graph,
+                                 "gemm_graph_gbps": wbytes / (t_graph * 1e-3) / 1e9,
+                                 "gemm_graph_frac_of_hbm": wbytes / (t_graph * 1e-3) / HBM_PEAK})
+            log(f"o_proj fp8 m={m}: gemm device time {t_graph*1e3:.1f} us per call in a graph "
+                f"({wbytes / t_graph / 1e6:.0f} GB/s, {wbytes / (t_graph * 1e-3) / HBM_PEAK * 100:.1f}% "
+                f"of HBM)")
         log(f"o_proj fp8 m={m}: gemm {t_gemm*1e3:.1f} us = {tf:.0f} TFLOP/s "
             f"({tf / FP8_PEAK_TFLOPS * 100:.1f}% of fp8 peak, {wbytes / t_gemm / 1e6:.0f} GB/s), "
             f"activation quant {t_quant*1e3:.1f} us")

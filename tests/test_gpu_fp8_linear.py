@@ -185,3 +185,21 @@ def test_gemm_rejects_bad_layouts(gpu):
     xq = torch.zeros((4, 256), dtype=torch.float8_e4m3fn, device=gpu)
     with pytest.raises(NotImplementedError):  # block_w not a multiple of 128
         fl.block_fp8_gemm(xq, sx, wq, torch.ones((1, 4), device=gpu), None, 128, 64)
+
+
+def test_gemm_split_k_repeats_bit_identically(gpu):
+    """Split-K sums its partials in a fixed order: repeated calls (with other
+    shapes, and other split counts, in between) give identical bits."""
+    print("[fp8 gemm] split-K repeats", flush=True)
+    wq, ws = make_weight(5120, 6144, 128, 128, 41, gpu)
+    outs = {}
+    for m in (64, 100, 64, 8, 64, 100):
+        x = make_x(m, 6144, m, gpu)
+        xq, sx = fl.quantize_activations(x)
+        got = fl.block_fp8_gemm(xq, sx, wq, ws, None)
+        torch.cuda.synchronize()
+        if m in outs:
+            assert torch.equal(got, outs[m]), f"m={m}: a repeated call differs"
+        else:
+            outs[m] = got.clone()
+    gemm_case(gpu, 64, 5120, 6144, seed=64)

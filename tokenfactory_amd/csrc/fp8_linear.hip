@@ -429,14 +429,17 @@ Shape gemm_shape(int64_t m) {
 }
 
 // Split-K factor: when the output tiles alone leave most CUs idle (M up to 512,
-// the weight-streaming regime), K is split until ~320 workgroups stream it.
+// the weight-streaming regime), K is split so that the workgroups fill the 256
+// CUs in one round (320 workgroups, one and a quarter rounds, took 1.4 times
+// as long at M = 64).
+constexpr int kCUs = 256;
 int gemm_splits(int64_t m, int64_t n, int64_t k) {
   const Shape sh = gemm_shape(m);
   if (m > 512 || n % 4) return 1;
   const int64_t tiles = ((m + 32 * sh.mt - 1) / (32 * sh.mt)) * ((n + 64 * sh.wn - 1) / (64 * sh.wn));
   const int64_t kb = k / kKSlice;
-  if (tiles >= 128 || kb < 4) return 1;
-  return (int)std::max<int64_t>(1, std::min<int64_t>({kb / 2, (320 + tiles - 1) / tiles, 16}));
+  if (tiles >= kCUs / 2 || kb < 4) return 1;
+  return (int)std::max<int64_t>(1, std::min<int64_t>({kb / 2, kCUs / tiles, 16}));
 }
 
 template <int MT, int WN, int STAGES>
