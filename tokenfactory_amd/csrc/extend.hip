@@ -473,16 +473,22 @@ __global__ void __launch_bounds__(kThreads) extend_mfma_kernel(ExtendArgs a) {
   };
   auto stage_for = [&](int j) { stage_at(min(j + kAhead, last), j + kAhead); };
   // fp8: tile t's e4m3 rows (issued one step earlier) widened into the bf16
-  // stages; only this lane's own loads need to have landed.
-  auto widen = [&](int t) {
+  // stages; only this lane's own loads need to have landed (after the step's
+  // own loads when it staged one, `all` when it staged nothing).
+  auto widen = [&](int t, auto all) {
     if constexpr (FP8) {
       if (t <= last) {
-        vm_wait_staged<true>();
+        if constexpr (decltype(all)::value)
+          asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        else
+          vm_wait_staged<true>();
         widen_tile(sm.f8 + (t & 1) * kF8Stage, sm.k + (t % kKS) * kKStage,
                    sm.v + (t % kVS) * kVStage, 4 * w + (lane >> 4), lane & 15);
       }
     }
   };
+  using Staged = std::true_type;
+  using Unstaged = std::false_type;
 
   // LDS read offsets of this lane (see Stager::issue / v_frag).
   const int kaddr = (n >> 1) * kKPair + (n & 1) * kRowBytes + 16 * (g ^ (n & 1));
@@ -545,7 +551,7 @@ __global__ void __launch_bounds__(kThreads) extend_mfma_kernel(ExtendArgs a) {
 #pragma unroll
     for (int p = 0; p < 2; ++p) st.issue_part(ids, p);
   }
-  widen(0);
+  widen(0, Unstaged{});
   vm_wait_staged<FP8>();
   __syncthreads();
 
@@ -583,46 +589,77 @@ __global__ void __launch_bounds__(kThreads) extend_mfma_kernel(ExtendArgs a) {
       for (int i = 0; i < 8; ++i) acc[i] *= alpha;
     }
   };
-  auto step_end = [&]() {
+  auto step_end = [&](auto staged) {
     // Tile j + 1 was issued one step earlier: only this step's tile loads
-    // may still be in flight.
-    vm_wait_staged<FP8>();
+    // may still be in flight (none after a step that staged nothing).
+    if constexpr (decltype(staged)::value)
+      vm_wait_staged<FP8>();
+    else
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
   };
+  // bf16 pools: steps j < n_stage stage tile j + 2, which exists; the last two
+  // steps stage nothing (no stand-in loads for the epilogue to wait for), so
+  // their waits cover every outstanding load.  No slot-id chunk is due in
+  // them.  fp8 pools stage in every step (stand-in tiles past the last): the
+  // separate tail steps cost that variant a register spill.
+  constexpr bool kTail = !FP8;
+  const int n_stage = kTail ? max(n_tiles - kAhead, 0) : n_tiles;
 
   if (w < kLeadWaves) {
-    for (int j = 0; j < n_tiles; ++j) {
-      slot_chunk(j);
-      stage_for(j);
-      qk_phase<true>(sm.k + (j % kKS) * kKStage, kaddr, qf, s, st);
+    auto lead_step = [&](int j, auto staged) {
+      constexpr bool kS = decltype(staged)::value;
+      if constexpr (kS) {
+        slot_chunk(j);
+        stage_for(j);
+      }
+      qk_phase<kS>(sm.k + (j % kKS) * kKStage, kaddr, qf, s, st);
       softmax_step(j);
-      widen(j + 1);
+      widen(j + 1, std::integral_constant<bool, !kS>{});
       rescale();
       pv_phase<false>(sm.v + (j % kVS) * kVStage, vaddr, acc, pt, st);
-      step_end();
-    }
+      step_end(staged);
+    };
+    int j = 0;
+    for (; j < n_stage; ++j) lead_step(j, Staged{});
+    if constexpr (kTail)
+      for (; j < n_tiles; ++j) lead_step(j, Unstaged{});
   } else {
-    stage_for(0);
-    qk_phase<true>(sm.k, kaddr, qf, s, st);
-    widen(1);
-    softmax_step(0);
-    step_end();
-    for (int j = 1; j < n_tiles; ++j) {
-      slot_chunk(j);
-      stage_for(j);
+    auto trail_step = [&](int j, auto staged) {   // j >= 1
+      constexpr bool kS = decltype(staged)::value;
+      if constexpr (kS) {
+        slot_chunk(j);
+        stage_for(j);
+      }
       rescale();
-      pv_phase<true>(sm.v + ((j - 1) % kVS) * kVStage, vaddr, acc, pt, st);
+      pv_phase<kS>(sm.v + ((j - 1) % kVS) * kVStage, vaddr, acc, pt, st);
       qk_phase<false>(sm.k + (j % kKS) * kKStage, kaddr, qf, s, st);
-      widen(j + 1);
+      widen(j + 1, std::integral_constant<bool, !kS>{});
       softmax_step(j);
-      step_end();
+      step_end(staged);
+    };
+    if (!kTail || n_stage > 0) {
+      stage_for(0);
+      qk_phase<true>(sm.k, kaddr, qf, s, st);
+      widen(1, Unstaged{});
+      softmax_step(0);
+      step_end(Staged{});
+    } else if constexpr (kTail) {
+      qk_phase<false>(sm.k, kaddr, qf, s, st);
+      widen(1, Staged{});
+      softmax_step(0);
+      step_end(Unstaged{});
     }
+    int j = 1;
+    for (; j < n_stage; ++j) trail_step(j, Staged{});
+    if constexpr (kTail)
+      for (; j < n_tiles; ++j) trail_step(j, Unstaged{});
     rescale();
     pv_phase<false>(sm.v + (last % kVS) * kVStage, vaddr, acc, pt, st);
   }
-  // The last steps staged stand-in tiles nobody reads; they must land (and
-  // every wave must be done with the stages) before the stage memory holds
-  // the output rows.
+  // Every wave must be done with the stages before the stage memory holds
+  // the output rows (the prologue's stand-in tile of a one-tile item has
+  // landed by the last step's wait).
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
 
