@@ -159,7 +159,7 @@ def bench_extend(torch, workloads, SlotAttentionCall, args, seed=13, kv_fp8=Fals
             "kernel_ms_p10_p50_p90": k_spread,
             "roofline": {"bound": "mfma", "achieved": tf / 1e12, "peak": MFMA_BF16_PEAK / 1e12,
                          "unit": "TFLOP/s", "frac": tf / MFMA_BF16_PEAK,
-                         "kernel": "extend_kernel<fp8>" if kv_fp8 else "extend_bf16_kernel"}}
+                         "kernel": "extend_mfma_kernel<true>" if kv_fp8 else "extend_mfma_kernel<false>"}}
 
 
 def bench_mixed(torch, workloads, SlotAttentionCall, args):
