@@ -21,6 +21,10 @@
  *    (token_to_kv_pool.py:20-23); req_to_token holds -1 for empty positions
  *    (req_to_token_pool.py:13-16).  Slot ids read from req_to_token are clamped
  *    into [0, pool_slots) so a bad id cannot fault the GPU.
+ *  - head_dim: 256 runs the tuned kernels (the 27B model); any other multiple
+ *    of 8 up to 256 runs one-wave-per-row kernels with the same semantics (the
+ *    reference's test configurations use 32); others are TF_ERR_UNSUPPORTED.
+ *    Decode at head_dim != 256 needs no workspace (the size query returns 0).
  *  - q / out are [T, num_q_heads, head_dim] bf16 with a free token stride
  *    (q_row_stride / out_row_stride, in elements); heads and dims are dense.
  *  - q head h reads kv head h / (num_q_heads / num_kv_heads)
@@ -317,7 +321,10 @@ int32_t tf_kv_write(const void* k, const void* v, int64_t src_row_stride,
  * q_out: bf16 [n_tokens, num_q_heads, head_dim] (token stride q_out_token_stride).
  * K / V rows go to the pool like tf_kv_write (bf16, or fp8-e4m3 with
  * k_scale / v_scale); slots outside [0, pool_slots) are skipped.
- * head_dim 256 only; rotary_dim a multiple of 16.
+ * head_dim a multiple of 8 up to 256; rotary_dim even (a multiple of 16 for
+ * head_dim 256).  With 3-row positions the sections must sum to rotary_dim / 2
+ * for the sectioned layout (the reference splits by them); the interleaved
+ * layout takes any sections (rotary_embedding.py:58-70).
  */
 int32_t tf_qk_norm_rope_kv_write(const void* q, int64_t q_token_stride, int64_t q_head_stride,
                                  const void* k, int64_t k_token_stride,

@@ -40,8 +40,13 @@ def test_decode_workspace_size_and_unsupported_arguments():
     # One partial slot per (unit) + one per workgroup: index b + u is unique.
     n = _native.decode_workspace_bytes(64, 24, 4, 256, 8192, 512)
     assert n >= (64 * 4 + 512) * 16 * 256 * 4
+    # other head dims run the one-wave-per-row kernel, which needs no workspace
+    assert _native.decode_workspace_bytes(4, 16, 2, 128, 512, 0) == 0
+    assert _native.decode_workspace_bytes(4, 16, 2, 32, 512, 0) == 0
     with pytest.raises(NotImplementedError):
-        _native.decode_workspace_bytes(4, 16, 2, 128, 512, 0)       # head_dim 128 not built
+        _native.decode_workspace_bytes(4, 16, 2, 36, 512, 0)        # not a multiple of 8
+    with pytest.raises(NotImplementedError):
+        _native.decode_workspace_bytes(4, 16, 2, 264, 512, 0)       # above 256
     with pytest.raises(NotImplementedError):
         _native.decode_workspace_bytes(4096, 16, 2, 256, 512, 0)    # > 2048 requests
     with pytest.raises(ValueError):

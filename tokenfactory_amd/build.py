@@ -18,7 +18,7 @@ REPO_DIR = PKG_DIR.parent
 CSRC = PKG_DIR / "csrc"
 LIB_DIR = PKG_DIR / "_lib"
 LIB_PATH = LIB_DIR / "libtf_attn.so"
-SOURCES = ["abi.hip", "decode.hip", "extend.hip", "fp8_linear.hip",
+SOURCES = ["abi.hip", "attn_generic.hip", "decode.hip", "extend.hip", "fp8_linear.hip",
            "gdn.hip", "kv_ops.hip", "plan.hip", "qk_prep.hip"]
 ARCH = "gfx950"
 

@@ -639,14 +639,23 @@ int make_decode_plan(int32_t n_items, int32_t num_q_heads, int32_t num_kv_heads,
   if (num_kv_heads <= 0 || num_q_heads <= 0 || num_q_heads % num_kv_heads)
     return fail(TF_ERR_INVALID, "decode: num_q_heads=%d not a multiple of num_kv_heads=%d",
                 num_q_heads, num_kv_heads);
-  if (head_dim != kD)
-    return fail(TF_ERR_UNSUPPORTED, "decode: head_dim=%d (only %d is built)", head_dim, kD);
   if (num_workgroups < 0) return fail(TF_ERR_INVALID, "decode: num_workgroups=%d", num_workgroups);
+  if (head_dim != kD) {
+    // Other head dims run the one-wave-per-row kernel (attn_generic.hip),
+    // which needs no workspace.
+    if (!generic_head_dim(head_dim))
+      return fail(TF_ERR_UNSUPPORTED,
+                  "decode: head_dim=%d (a multiple of 8 between 8 and %d)", head_dim, kD);
+    *p = DecodePlan{};
+    p->generic = true;
+    return TF_OK;
+  }
   const int32_t group = num_q_heads / num_kv_heads;
   p->n_hgroups = (group + 15) / 16;
   p->gmax = group < 16 ? group : 16;
   p->n_units = (int64_t)n_items * num_kv_heads * p->n_hgroups;
   // One persistent workgroup (4 waves) per CU measured fastest on MI355X.
+  p->generic = false;
   p->n_blocks = num_workgroups > 0 ? num_workgroups : device_cu_count();
   const int64_t parts = p->n_units + p->n_blocks;
   p->ml_bytes = (parts * 16 * 2 * 4 + 255) / 256 * 256;
@@ -704,6 +713,39 @@ int decode_launch(const void* q, int64_t q_row_stride, const void* k_pool, const
     return fail(TF_ERR_INVALID, "decode: workspace needs %lld bytes, got %lld",
                 (long long)p.total_bytes, (long long)workspace_bytes);
   if (p.n_units > INT32_MAX) return fail(TF_ERR_INVALID, "decode: too many units");
+  if (p.generic) {   // head_dim != 256: everything happens in the "partial" phase
+    if (!(phases & kPhasePartial)) return TF_OK;
+    GenericAttnArgs g{};
+    g.q = static_cast<const __bf16*>(q);
+    g.q_stride = q_row_stride;
+    g.k_pool = static_cast<const uint8_t*>(k_pool);
+    g.v_pool = static_cast<const uint8_t*>(v_pool);
+    g.pool_slots = pool_slots;
+    g.fp8 = kv_dtype == TF_DTYPE_FP8_E4M3;
+    g.k_scale = k_scale;
+    g.v_scale = v_scale;
+    g.rtt = req_to_token;
+    g.rtt_rows = rtt_rows;
+    g.rtt_stride = rtt_row_stride;
+    g.rtt_cols = rtt_cols;
+    g.rpi = req_pool_indices;
+    g.seq_lens = seq_lens;
+    g.seq_override = seq_len_override;
+    g.items = items;
+    g.q_rows = q_rows;
+    g.work = nullptr;
+    g.n_rows = n_items;
+    g.hq = num_q_heads;
+    g.hkv = num_kv_heads;
+    g.head_dim = head_dim;
+    g.scale_log2 = scale * kLog2e;
+    g.out = static_cast<__bf16*>(out);
+    g.out_stride = out_row_stride;
+    g.gate = static_cast<const __bf16*>(gate);
+    g.gate_stride = gate_row_stride;
+    g.gate_hstride = gate_head_stride;
+    return launch_generic_attn(g, reinterpret_cast<hipStream_t>(stream));
+  }
 
   DecodeArgs a;
   a.q = static_cast<const __bf16*>(q);

@@ -719,8 +719,10 @@ extern "C" int32_t tf_attn_extend(const void* q, int64_t q_row_stride, const voi
   if (num_kv_heads <= 0 || num_q_heads <= 0 || num_q_heads % num_kv_heads)
     return fail(TF_ERR_INVALID, "extend: num_q_heads=%d not a multiple of num_kv_heads=%d",
                 num_q_heads, num_kv_heads);
-  if (head_dim != kD)
-    return fail(TF_ERR_UNSUPPORTED, "extend: head_dim=%d (only %d is built)", head_dim, kD);
+  const bool generic = head_dim != kD;
+  if (generic && !generic_head_dim(head_dim))
+    return fail(TF_ERR_UNSUPPORTED, "extend: head_dim=%d (a multiple of 8 between 8 and %d)",
+                head_dim, kD);
   if (kv_dtype != TF_DTYPE_BF16 && kv_dtype != TF_DTYPE_FP8_E4M3)
     return fail(TF_ERR_UNSUPPORTED, "extend: kv_dtype=%d", kv_dtype);
   if (n_work == 0) return TF_OK;
@@ -771,6 +773,36 @@ extern "C" int32_t tf_attn_extend(const void* q, int64_t q_row_stride, const voi
   a.gate_hstride = gate_head_stride;
 
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  if (generic) {   // head_dim != 256: one wave per row of every work entry
+    GenericAttnArgs g{};
+    g.q = a.q;
+    g.q_stride = a.q_stride;
+    g.k_pool = a.k_pool;
+    g.v_pool = a.v_pool;
+    g.pool_slots = a.pool_slots;
+    g.fp8 = kv_dtype == TF_DTYPE_FP8_E4M3;
+    g.k_scale = a.k_scale;
+    g.v_scale = a.v_scale;
+    g.rtt = a.rtt;
+    g.rtt_rows = a.rtt_rows;
+    g.rtt_stride = a.rtt_stride;
+    g.rtt_cols = a.rtt_cols;
+    g.rpi = a.rpi;
+    g.seq_lens = a.seq_lens;
+    g.seq_override = a.seq_override;
+    g.work = work;
+    g.n_rows = n_work;
+    g.hq = num_q_heads;
+    g.hkv = num_kv_heads;
+    g.head_dim = head_dim;
+    g.scale_log2 = a.scale_log2;
+    g.out = a.out;
+    g.out_stride = a.out_stride;
+    g.gate = a.gate;
+    g.gate_stride = a.gate_stride;
+    g.gate_hstride = a.gate_hstride;
+    return launch_generic_attn(g, s);
+  }
   if (kv_dtype == TF_DTYPE_FP8_E4M3)
     hipLaunchKernelGGL(extend_mfma_kernel<true>, dim3((unsigned)n_work), dim3(kThreads), 0, s, a);
   else

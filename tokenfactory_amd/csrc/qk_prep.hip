@@ -285,6 +285,95 @@ qk_prep_kernel(PrepArgs a) {
   }
 }
 
+// head_dim other than 256 (a multiple of 8, at most 256): one wave per (token,
+// row), lane l holding elements l, l + 64, ...; the rotate-half partner comes
+// from a wave-private LDS copy of the normalised row and each rotary element's
+// cos / sin is evaluated where it is used.  Same rounding steps as above.
+constexpr int kGenRowMax = 256;
+
+__global__ void __launch_bounds__(kThreads)
+qk_prep_generic_kernel(PrepArgs a, int D) {
+#pragma clang fp contract(off)
+  __shared__ float rowbuf[kWaves][kGenRowMax];
+  const int lane = threadIdx.x & 63;
+  const int w = threadIdx.x / kWave;
+  const int rows = a.hq + 2 * a.hkv;
+  const int64_t wid = (int64_t)blockIdx.x * kWaves + w;
+  if (wid >= a.n_tokens * rows) return;
+  const int64_t t = wid / rows;
+  const int r = (int)(wid - t * rows);
+  const int kind = r < a.hq ? 0 : (r < a.hq + a.hkv ? 1 : 2);
+  const int head = kind == 0 ? r : (kind == 1 ? r - a.hq : r - a.hq - a.hkv);
+  const __bf16* src = kind == 0 ? a.q + t * a.q_tok + (int64_t)head * a.q_head
+                                : (kind == 1 ? a.k + t * a.k_tok : a.v + t * a.v_tok) +
+                                      (int64_t)head * D;
+  const int h = a.rotary_dim >> 1;
+  float y[kGenRowMax / kWave];
+#pragma unroll
+  for (int i = 0; i < kGenRowMax / kWave; ++i) {
+    const int e = lane + kWave * i;
+    y[i] = e < D ? (float)src[e] : 0.f;
+  }
+  if (kind != 2) {
+    float ss = 0.f;
+#pragma unroll
+    for (int i = 0; i < kGenRowMax / kWave; ++i) ss += y[i] * y[i];
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) ss += __shfl_xor(ss, m, kWave);
+    const float rs = rsqrtf(ss / (float)D + a.eps);
+    const float* wt = kind == 0 ? a.qw : a.kw;
+#pragma unroll
+    for (int i = 0; i < kGenRowMax / kWave; ++i) {
+      const int e = lane + kWave * i;
+      if (e < D) y[i] = bf16r(wt[e] * (y[i] * rs));
+    }
+    if (h > 0) {
+#pragma unroll
+      for (int i = 0; i < kGenRowMax / kWave; ++i) {
+        const int e = lane + kWave * i;
+        if (e < D) rowbuf[w][e] = y[i];
+      }
+#pragma unroll
+      for (int i = 0; i < kGenRowMax / kWave; ++i) {
+        const int e = lane + kWave * i;
+        if (e < 2 * h) {
+          const int f = e < h ? e : e - h;
+          const float pf = (float)a.pos[(int64_t)mrope_row(a, f) * a.pos_stride + t];
+          float sn, cs;
+          sincosf(pf * a.inv_freq[f], &sn, &cs);
+          const float rot = e < h ? -rowbuf[w][e + h] : rowbuf[w][e - h];
+          y[i] = bf16r(bf16r(y[i] * bf16r(cs)) + bf16r(rot * bf16r(sn)));
+        }
+      }
+    }
+  }
+  if (kind == 0) {
+    __bf16* dst = a.q_out + t * a.q_out_tok + (int64_t)head * D;
+#pragma unroll
+    for (int i = 0; i < kGenRowMax / kWave; ++i) {
+      const int e = lane + kWave * i;
+      if (e < D) dst[e] = (__bf16)y[i];
+    }
+    return;
+  }
+  const int64_t slot = a.loc[t];
+  if (slot < 0 || slot >= a.pool_slots) return;
+  const int64_t base = (slot * a.hkv + head) * D;   // element index
+  uint8_t* pool = kind == 1 ? a.k_pool : a.v_pool;
+  const float sc = a.fp8 ? (kind == 1 ? a.k_scale[0] : a.v_scale[0]) : 1.f;
+#pragma unroll
+  for (int i = 0; i < kGenRowMax / kWave; ++i) {
+    const int e = lane + kWave * i;
+    if (e >= D) continue;
+    if (a.fp8) {
+      pool[base + e] = (uint8_t)(__builtin_amdgcn_cvt_pk_fp8_f32(sat448(y[i] / sc), 0.f, 0u,
+                                                                 false) & 0xffu);
+    } else {
+      reinterpret_cast<__bf16*>(pool)[base + e] = (__bf16)y[i];
+    }
+  }
+}
+
 }  // namespace
 }  // namespace tfa
 
@@ -302,17 +391,25 @@ extern "C" int32_t tf_qk_norm_rope_kv_write(
   using namespace tfa;
   clear_error();
   if (n_tokens < 0) return fail(TF_ERR_INVALID, "qk_prep: n_tokens=%lld", (long long)n_tokens);
-  if (head_dim != kD)
-    return fail(TF_ERR_UNSUPPORTED, "qk_prep: head_dim=%d (only %d is built)", head_dim, kD);
+  if (head_dim < 8 || head_dim > kD || head_dim % 8)
+    return fail(TF_ERR_UNSUPPORTED, "qk_prep: head_dim=%d (a multiple of 8 up to %d)", head_dim,
+                kD);
   if (num_q_heads <= 0 || num_kv_heads <= 0)
     return fail(TF_ERR_INVALID, "qk_prep: heads %d/%d", num_q_heads, num_kv_heads);
-  if (rotary_dim < 0 || rotary_dim > head_dim || rotary_dim % 16)
-    return fail(TF_ERR_UNSUPPORTED, "qk_prep: rotary_dim=%d (multiple of 16, <= head_dim)",
-                rotary_dim);
+  if (rotary_dim < 0 || rotary_dim > head_dim || rotary_dim % 2 ||
+      (head_dim == kD && rotary_dim % 16))
+    return fail(TF_ERR_UNSUPPORTED,
+                "qk_prep: rotary_dim=%d (even, <= head_dim; a multiple of 16 for head_dim %d)",
+                rotary_dim, kD);
   if (position_rows != 1 && position_rows != 3)
     return fail(TF_ERR_INVALID, "qk_prep: position_rows=%d (1 or 3)", position_rows);
-  if (position_rows == 3 && (mrope_section0 < 0 || mrope_section1 < 0 || mrope_section2 < 0 ||
-                             2 * (mrope_section0 + mrope_section1 + mrope_section2) != rotary_dim))
+  // Sectioned M-RoPE splits the frequencies into the three sections
+  // (rotary_embedding.py:64-70 splits them, so they must add up); the
+  // interleaved layout takes any sections (:58-63).
+  if (position_rows == 3 &&
+      (mrope_section0 < 0 || mrope_section1 < 0 || mrope_section2 < 0 ||
+       (!mrope_interleaved &&
+        2 * (mrope_section0 + mrope_section1 + mrope_section2) != rotary_dim)))
     return fail(TF_ERR_INVALID, "qk_prep: mrope sections %d+%d+%d must sum to rotary_dim/2",
                 mrope_section0, mrope_section1, mrope_section2);
   if (kv_dtype != TF_DTYPE_BF16 && kv_dtype != TF_DTYPE_FP8_E4M3)
@@ -368,6 +465,14 @@ extern "C" int32_t tf_qk_norm_rope_kv_write(
   a.k_scale = k_scale;
   a.v_scale = v_scale;
 
+  if (head_dim != kD) {   // one wave per (token, row)
+    const int64_t waves = n_tokens * (num_q_heads + 2 * num_kv_heads);
+    const int64_t gblocks = (waves + kWaves - 1) / kWaves;
+    if (gblocks > INT32_MAX) return fail(TF_ERR_INVALID, "qk_prep: too many tokens");
+    hipLaunchKernelGGL(qk_prep_generic_kernel, dim3((unsigned)gblocks), dim3(kThreads), 0,
+                       reinterpret_cast<hipStream_t>(stream), a, (int)head_dim);
+    return launch_status("tf_qk_norm_rope_kv_write launch");
+  }
   // One token per wave, four per workgroup.
   const int64_t blocks = (n_tokens + kWaves - 1) / kWaves;
   if (blocks > INT32_MAX) return fail(TF_ERR_INVALID, "qk_prep: too many tokens");
