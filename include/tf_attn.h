@@ -443,13 +443,21 @@ int32_t tf_gdn_decode(const void* qkv, int64_t qkv_row_stride, const void* a, co
  * each request's conv runs over [conv_state, its tokens] and its state is
  * carried through its tokens in order.  The state update is the reference's
  * chunk-wise WY form (:194-242) with 32-token chunks (the same recurrence as
- * token by token, equal up to fp32 rounding).  Seven launches: the request
+ * token by token, equal up to fp32 rounding).  Eight launches: the request
  * of every token row, the conv for every (token, channel) in parallel, the
  * conv-state shift, normalised q / k and the gates for every token in
  * parallel, the state-independent part of every chunk in parallel, the
- * chunked recurrence (one workgroup per request and value head, its state in
- * registers from first chunk to last) and the gated norm for every (token,
- * value head) in parallel.  qkv, z, out and core_out must be 8-byte aligned
+ * one-token requests' update (as in tf_gdn_decode), the chunked recurrence
+ * with the gated norm of its rows (one workgroup per request of two or more
+ * tokens and value head, its state in registers from first chunk to last),
+ * and zeros for the rows of no request or of an out-of-pool slot.  When the
+ * batch can hold both kinds of request (batch_size > 1, max_extend_len > 1),
+ * the one-token update runs on a second stream of the library's (one per
+ * device, made on the first call that is not under graph capture) that forks
+ * from `stream` after the chunk preparation and joins it before the call
+ * returns; under capture the fork and join become graph dependencies.
+ * Concurrent calls on one device serialise their launch sequences on a
+ * lock.  qkv, z, out and core_out must be 8-byte aligned
  * with row strides that are multiples of 4; norm_weight 16-byte aligned.  Other arguments
  * as for tf_gdn_decode, with rows = tokens; workspace:
  * tf_gdn_extend_workspace_bytes(n_tokens, batch_size, Hk, Hv) bytes, 16-byte

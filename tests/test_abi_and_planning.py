@@ -57,12 +57,12 @@ def test_decode_workspace_size_and_unsupported_arguments():
 
 def test_gdn_extend_workspace_covers_rows_and_chunk_records():
     # Per token row: conv outputs (bf16), split q / k (4 x 128 bf16 per key
-    # head), gates (2 fp32 per value head), recurrence output (bf16), the row's
-    # request (int32); then one 9 KB record per (32-token chunk slot, value
-    # head), with n_tokens / 32 + batch + 1 slots.
+    # head), gates (2 fp32 per value head), the row's request (int32); then
+    # one 9 KB record per (32-token chunk slot, value head), with
+    # n_tokens / 32 + batch + 1 slots.
     lib = _native.load()
     hk, hv = 16, 48
-    row = (2 * hk * 128 + hv * 128) * 2 + hk * 4 * 128 * 2 + hv * 8 + hv * 128 * 2 + 4
+    row = (2 * hk * 128 + hv * 128) * 2 + hk * 4 * 128 * 2 + hv * 8 + 4
     for n_tok, bsz in [(1, 1), (8320, 132), (70, 3)]:
         got = lib.tf_gdn_extend_workspace_bytes(n_tok, bsz, hk, hv)
         assert got >= n_tok * row + (n_tok // 32 + bsz + 1) * hv * 2304 * 4

@@ -208,6 +208,91 @@ def test_extend_out_of_pool_slots_are_skipped(gpu, lens):
     check_outputs(got[t0:t1].cpu(), want_out, "valid request: normed output")
 
 
+def _extend_native(qkv, b, a, z, params, cs, ss, req, lens, hk, hv, out, core, tok, ws, stream):
+    """tf_gdn_extend on caller-made tensors (views, preallocated workspace)."""
+    from tokenfactory_amd import _native
+    from tokenfactory_amd.linear_attention import CONV_KERNEL, HEAD_DIM
+    conv_w, a_log, dt_bias, norm_w = params
+    p = lambda t: 0 if t is None else t.data_ptr()
+    _native.call("tf_gdn_extend", p(qkv), qkv.stride(0), p(a), p(b), a.stride(0), p(z),
+                 z.stride(0), p(conv_w), p(a_log), p(dt_bias), p(norm_w), 1e-6, p(cs),
+                 cs.stride(0), p(ss), ss.stride(0), p(req), p(tok), len(lens), qkv.shape[0],
+                 max(lens), cs.shape[0], hk, hv, HEAD_DIM, HEAD_DIM, CONV_KERNEL, p(out),
+                 out.stride(0), p(core), core.stride(0), p(ws), ws.numel(), stream)
+
+
+def test_extend_strided_views_and_graph_replay(gpu):
+    """z, out and core_out as column views of wider tensors at an 8-byte (not
+    16-byte) offset, on a batch that mixes one-token and multi-token requests
+    (the one-token recurrence then runs on the library's second stream beside
+    the chunked pass): the outputs equal gdn_extend_step's on contiguous
+    tensors bit for bit, the columns around the views keep their contents,
+    and the call captured in a HIP graph replays to the same bits three times,
+    with eager work between the replays."""
+    from tokenfactory_amd import _native
+    hk, hv, lens = 4, 12, [1, 70, 1, 33, 1, 2]
+    n_tok, vd = sum(lens), hv * 128
+    n_slots = len(lens) + 2
+    g = torch.Generator().manual_seed(123)
+    conv_state = torch.randn((n_slots, 2 * hk * 128 + vd, 3), generator=g).to(torch.bfloat16)
+    ssm_state = torch.randn((n_slots, hv, 128, 128), generator=g) * 0.2
+    req = torch.randperm(n_slots, generator=g)[:len(lens)].to(gpu)
+    params = [p.to(gpu) for p in make_params(hk, hv, 9)]
+    qkv, a, b, z = (x.to(gpu) for x in make_step(n_tok, hk, hv, 55))
+    cs, ss = conv_state.to(gpu), ssm_state.to(gpu)
+    want_out, want_core = gdn_extend_step(qkv, b, a, z, *params, 1e-6, cs, ss, req, lens, hk, hv,
+                                          return_core=True)
+    want_cs, want_ss = cs.clone(), ss.clone()
+
+    zbig = torch.full((n_tok, vd + 8), 7.0, dtype=torch.bfloat16, device=gpu)
+    zbig[:, 4:4 + vd] = z
+    zv = zbig[:, 4:4 + vd]
+    outbig = torch.full((n_tok, vd + 8), -3.0, dtype=torch.bfloat16, device=gpu)
+    corebig = torch.full((n_tok, vd + 12), 5.0, dtype=torch.bfloat16, device=gpu)
+    out, core = outbig[:, 4:4 + vd], corebig[:, 8:8 + vd]
+    assert out.data_ptr() % 16 == 8 and zv.data_ptr() % 16 == 8
+    offs = [0]
+    for e in lens:
+        offs.append(offs[-1] + e)
+    tok = torch.tensor(offs, dtype=torch.int32, device=gpu)
+    nbytes = _native.load().tf_gdn_extend_workspace_bytes(n_tok, len(lens), hk, hv)
+    ws = torch.empty((nbytes,), dtype=torch.uint8, device=gpu)
+
+    def run(stream):
+        cs.copy_(conv_state.to(gpu))
+        ss.copy_(ssm_state.to(gpu))
+        _extend_native(qkv, b, a, zv, params, cs, ss, req, lens, hk, hv, out, core, tok, ws,
+                       stream)
+
+    def check(what):
+        assert torch.equal(out, want_out), f"{what}: out"
+        assert torch.equal(core, want_core), f"{what}: core_out"
+        assert torch.equal(ss, want_ss) and torch.equal(cs, want_cs), f"{what}: states"
+        assert (outbig[:, :4] == -3).all() and (outbig[:, 4 + vd:] == -3).all(), what
+        assert (corebig[:, :8] == 5).all() and (corebig[:, 8 + vd:] == 5).all(), what
+
+    run(torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    check("eager")
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=side):
+        _extend_native(qkv, b, a, zv, params, cs, ss, req, lens, hk, hv, out, core, tok, ws,
+                       side.cuda_stream)
+    torch.cuda.synchronize()
+    for r in range(3):
+        cs.copy_(conv_state.to(gpu))
+        ss.copy_(ssm_state.to(gpu))
+        out.fill_(0)
+        core.fill_(0)
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        check(f"replay {r}")
+        float(torch.randn(1 << 16, device=gpu).sum())   # eager work between replays
+
+
 def test_decode_out_of_pool_rows_are_zero(gpu):
     hk, hv, n_slots = 4, 12, 6
     conv_dim = 2 * hk * 128 + hv * 128

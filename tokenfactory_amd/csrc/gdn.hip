@@ -25,6 +25,8 @@
 // value head and request.
 #include <math.h>
 
+#include <mutex>
+
 #include "tf_common.h"
 #include "tf_internal.h"
 
@@ -61,7 +63,6 @@ struct GdnArgs {
   float* wg;             // extend: fp32 [rows, Hv, 2] g = log alpha, beta
   int32_t* owner;        // extend: int32 [rows] request of each token row (-1: none / skipped)
   float* wrec;           // extend: fp32 [chunk slots, Hv, 2304] chunk records
-  uint16_t* wcore;       // extend: bf16 [rows, Hv * Dv] recurrence output
   const int32_t* tok;    // extend: request b owns token rows tok[b] .. tok[b + 1] - 1
   int32_t rows;          // token rows of qkv / a / b / z / out (offsets are clamped to it)
   uint16_t* ws;          // bf16 [rows, conv_dim]: conv + SiLU outputs
@@ -217,9 +218,11 @@ __global__ void __launch_bounds__(kThreads) gdn_recur_kernel(GdnArgs a) {
 // by its own kernel); per 32-token chunk the WY quantities are prepared for all
 // chunks at once; then one workgroup per (request, value head) carries the
 // head's state in MFMA accumulators from the first chunk to the last (one state
-// read and one write per request and head).  This is the reference's chunked
-// WY update (:194-242) with 32-token chunks; the chunk length does not change
-// the result.
+// read and one write per request and head) and applies the gated norm to the
+// rows as they come out.  This is the reference's chunked WY update (:194-242)
+// with 32-token chunks; the chunk length does not change the result.  The
+// one-token requests of the batch take gdn_recur_kernel, on a second stream
+// beside the chunked pass (tf_gdn_extend).
 
 constexpr int kConvTokens = 8;    // tokens per thread in the extend conv
 
@@ -404,7 +407,8 @@ __device__ __forceinline__ void dma16(const void* sbase, uint32_t voff, uint32_t
 // depend on S - T, Bm, e^gamma, e^(gamma_C - gamma), beta - for every chunk
 // of every request in parallel into a 9 KB record per (chunk, value head).
 // gdn_chunk_ext_kernel then carries S through a request's chunks, one
-// 256-thread workgroup per (request, value head): wave w owns state columns
+// 512-thread workgroup per (request, value head) whose state wave w (0-3) owns
+// state columns
 // 32 w .. + 31 as four 32 x 32 MFMA accumulator tiles (lane (g, n) = (lane /
 // 32, lane % 32): rows 32 ti + 8 (r / 4) + 4 g + r % 4 of column 32 w + n), so
 // the state update is an MFMA into S and the products with S read it as an
@@ -413,7 +417,10 @@ __device__ __forceinline__ void dma16(const void* sbase, uint32_t voff, uint32_t
 // lo*hi, about 2^-17 relative error, fp32 accumulation); q and k arrive
 // already split (gdn_qk_ext_kernel).  Chunk records are numbered
 // floor(t0_b / 32) + b + ci for chunk ci of request b (first token row t0_b),
-// which is unique and below n_tokens / 32 + B.
+// which is unique and below n_tokens / 32 + B.  Four helper waves of the same
+// workgroup load the chunks, transpose k and apply the gated norm to the
+// output rows (gdn_chunk_ext_kernel), so the state waves' time per chunk is
+// the recurrence's alone.
 constexpr int kChunk = 32;
 constexpr int kRec = 2304;     // floats per chunk record: T, Bm, e^gamma, e^(gC - gamma), beta
 constexpr int kRecT = 0, kRecB = 1024, kRecC = 2048, kRecD = 2080, kRecBeta = 2112;
@@ -579,15 +586,29 @@ __device__ __forceinline__ uint32_t row_half(const uint32_t (*rows)[128], int t,
 }
 
 constexpr int kKtStride = 40;   // bf16 per row of the transposed k copy (80 B: 8-B reads, few conflicts)
+constexpr int kChunkThreads = 2 * kThreads;   // 4 recurrence waves + 4 helper waves
 
-__global__ void __launch_bounds__(kThreads) gdn_chunk_ext_kernel(GdnArgs a) {
+// Waves 0-3 carry the state through the chunks (the MFMA work above, nothing
+// else); waves 4-7, the helpers, share their SIMDs and keep the inputs ahead
+// of them: while the state waves work on chunk ci, the helpers move chunk
+// ci + 1 into LDS, transpose its k, and apply the gated norm to the rows of
+// chunk ci - 1.  One barrier per chunk hands the buffers over (chunk inputs,
+// the transposed k and the output tile are double-buffered by chunk parity).
+__global__ void __launch_bounds__(kChunkThreads) gdn_chunk_ext_kernel(GdnArgs a) {
   __shared__ __attribute__((aligned(16))) ChunkIn sm[2];
-  // k of the current chunk transposed, [part][dim][token], rebuilt per chunk:
-  // the state update reads 4 tokens of one dim per 8-byte load.
-  __shared__ __attribute__((aligned(16))) uint16_t kt[2][kDk][kKtStride];
+  // k of a chunk transposed, [part][dim][token]: the state update reads 4
+  // tokens of one dim per 8-byte load.
+  __shared__ __attribute__((aligned(16))) uint16_t kt[2][2][kDk][kKtStride];
+  // A chunk's recurrence output (o rounded to bf16), token-major, and the
+  // head's norm weights.
+  __shared__ __attribute__((aligned(16))) uint16_t otile[2][kChunk][kDv];
+  __shared__ float nw[kDv];
   const int bi = blockIdx.x / a.hv, h = blockIdx.x % a.hv;
   const int hk = h / a.vpk;
-  const int lane = threadIdx.x & (kWave - 1), w = wave_id();
+  const int lane = threadIdx.x & (kWave - 1), wv = wave_id();
+  const bool helper = wv >= 4;
+  const int w = wv & 3;                            // wave within its group
+  const int ht = threadIdx.x & (kThreads - 1);     // thread within its group
   const int g = lane >> 5, n = lane & 31;
   const int64_t r = a.req[bi];
   if (r < 0 || r >= a.n_slots) return;
@@ -595,8 +616,6 @@ __global__ void __launch_bounds__(kThreads) gdn_chunk_ext_kernel(GdnArgs a) {
   if (t1 - t0 < 2) return;   // one-token requests: gdn_recur_kernel
   const int last = t1 - 1;
   const int nchunks = (t1 - t0 + kChunk - 1) / kChunk;
-  const int key0 = chunk_key(a, bi);
-  const int j = 32 * w + n;   // this lane's state column
 
   // The 64 KB state goes through LDS (the chunk buffers, not yet in use) so
   // that the global accesses are coalesced 16-byte ones and each lane reads
@@ -605,214 +624,244 @@ __global__ void __launch_bounds__(kThreads) gdn_chunk_ext_kernel(GdnArgs a) {
   float* stage = reinterpret_cast<float*>(&sm[0]);
   static_assert(sizeof(sm) >= kDk * kDv * 4, "state staging");
 #pragma unroll
-  for (int i = 0; i < kDk * kDv / 4 / kThreads; ++i) {
-    const int q = i * kThreads + threadIdx.x;
+  for (int i = 0; i < kDk * kDv / 4 / kChunkThreads; ++i) {
+    const int q = i * kChunkThreads + threadIdx.x;
     reinterpret_cast<f32x4*>(stage)[q] = reinterpret_cast<const f32x4*>(S)[q];
   }
-  __syncthreads();
-  f32x16 st[4];
-  {
-    const float* my = stage + 4 * g * kDv + j;
-#pragma unroll
-    for (int ti = 0; ti < 4; ++ti)
-#pragma unroll
-      for (int rr = 0; rr < 16; ++rr)
-        st[ti][rr] = my[(32 * ti + 8 * (rr >> 2) + (rr & 3)) * kDv];
-  }
+  nw[threadIdx.x & (kDv - 1)] = a.norm_w[h * kDv + (threadIdx.x & (kDv - 1))];   // 4 writers each
   __syncthreads();
 
-  // Chunk ci into buffer bf (tokens past the last one re-read the last token;
-  // the record gives them beta = 0 and g = 0).  Wave w moves q and k rows
-  // 8 w .. 8 w + 7 (4 + 4 instructions, two rows each), V rows 8 w .. + 7 (2)
-  // and 3 KB of the record (waves 0-2).
-  const uint8_t* qk_base = reinterpret_cast<const uint8_t*>(a.wqk) + (int64_t)hk * 1024;
-  const uint8_t* v_base =
-      reinterpret_cast<const uint8_t*>(a.ws) + ((int64_t)2 * a.key_dim + h * kDv) * 2;
-  const uint8_t* rec_base = reinterpret_cast<const uint8_t*>(a.wrec) + (int64_t)h * kRec * 4;
-  auto issue = [&](int ci, int bf) {
-    const int tb = t0 + kChunk * ci;
-    ChunkIn& I = sm[bf];
+  if (!helper) {
+    const int j = 32 * w + n;   // this lane's state column
+    f32x16 st[4];
+    {
+      const float* my = stage + 4 * g * kDv + j;
 #pragma unroll
-    for (int p = 0; p < 4; ++p) {
-      const int t = 8 * w + 2 * p + g;
-      const uint32_t row = (uint32_t)min(tb + t, last) * (uint32_t)a.hk * 1024u;
-      const uint32_t cpos = (uint32_t)((n & 16) | ((n & 15) ^ (t & 15))) * 16u;
-      dma16(qk_base, row + cpos, lds_addr(&I.q[8 * w + 2 * p][0]));
-      dma16(qk_base, row + 512u + cpos, lds_addr(&I.k[8 * w + 2 * p][0]));
-    }
+      for (int ti = 0; ti < 4; ++ti)
 #pragma unroll
-    for (int p = 0; p < 2; ++p) {
-      const int t = 8 * w + 4 * p + (lane >> 4);
-      dma16(v_base, (uint32_t)min(tb + t, last) * (uint32_t)a.conv_dim * 2u + 16u * (lane & 15),
-            lds_addr(&I.v[8 * w + 4 * p][0]));
+        for (int rr = 0; rr < 16; ++rr)
+          st[ti][rr] = my[(32 * ti + 8 * (rr >> 2) + (rr & 3)) * kDv];
     }
-    if (w < 3) {
-      const uint32_t rec = (uint32_t)(key0 + ci) * (uint32_t)a.hv * (uint32_t)(kRec * 4);
-#pragma unroll
-      for (int p = 0; p < 3; ++p)
-        dma16(rec_base, rec + 1024u * (3 * w + p) + 16u * lane,
-              lds_addr(&I.rec[256 * (3 * w + p)]));
-    }
-  };
-  issue(0, 0);
+    __syncthreads();   // the staging area is free for chunk 0
 
-  for (int ci = 0; ci < nchunks; ++ci) {
-    const ChunkIn& I = sm[ci & 1];
-    const int tb = t0 + kChunk * ci;
-    const int ntok = min(kChunk, t1 - tb);
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    __syncthreads();   // chunk ci has landed; every wave is done with chunk ci - 1
-    if (ci + 1 < nchunks) issue(ci + 1, (ci + 1) & 1);
-    {   // thread (part, dim) = (tid / 128, tid % 128) transposes its 32 tokens
-      const int i = threadIdx.x & (kDk - 1), part = threadIdx.x >> 7;
-#pragma unroll
-      for (int s2 = 0; s2 < kChunk; s2 += 2)
-        *reinterpret_cast<uint32_t*>(&kt[part][i][s2]) =
-            row_half(I.k, s2, i, part) | (row_half(I.k, s2 + 1, i, part) << 16);
-    }
-    __syncthreads();
+    for (int ci = 0; ci < nchunks; ++ci) {
+      const ChunkIn& I = sm[ci & 1];
+      const uint16_t(*kT)[kDk][kKtStride] = kt[ci & 1];
+      __syncthreads();   // chunk ci and its transposed k are in; its output tile is free
 
-    // P = K S0 and R = Q S0 over the state rows (k index 8 g + jj <-> state
-    // row 32 ti + 16 hh + 8 (jj / 4) + 4 g + jj % 4)
-    // (two accumulators each for P and R, one per half of the state rows:
-    // four independent MFMA chains)
-    f32x16 Pp[2] = {{}, {}}, Rp[2] = {{}, {}};
+      // P = K S0 and R = Q S0 over the state rows (k index 8 g + jj <-> state
+      // row 32 ti + 16 hh + 8 (jj / 4) + 4 g + jj % 4)
+      // (two accumulators each for P and R, one per half of the state rows:
+      // four independent MFMA chains)
+      f32x16 Pp[2] = {{}, {}}, Rp[2] = {{}, {}};
 #pragma unroll
-    for (int ti = 0; ti < 4; ++ti) {
+      for (int ti = 0; ti < 4; ++ti) {
+#pragma unroll
+        for (int hh = 0; hh < 2; ++hh) {
+          u32x4 sh, sl, kh, kl, qh, ql;
+          split16(st[ti], 8 * hh, sh, sl);
+          const int d0 = 32 * ti + 16 * hh + 4 * g;
+          row8(I.k, n, d0, kh, kl);
+          row8(I.q, n, d0, qh, ql);
+          Pp[ti >> 1] = mma3(Pp[ti >> 1], kh, kl, sh, sl);
+          Rp[ti >> 1] = mma3(Rp[ti >> 1], qh, ql, sh, sl);
+        }
+      }
+      const f32x16 P = Pp[0] + Pp[1], R = Rp[0] + Rp[1];
+      // X = beta (v - e^gamma P); Delta = T X (k index 8 g + jj <-> token
+      // 16 hh + 8 (jj / 4) + 4 g + jj % 4)
+      f32x16 X;
+#pragma unroll
+      for (int rr = 0; rr < 16; ++rr) {
+        const int t = c_row(rr, g);
+        X[rr] = I.rec[kRecBeta + t] * (bf(I.v[t][j]) - I.rec[kRecC + t] * P[rr]);
+      }
+      f32x16 Dp[2];
 #pragma unroll
       for (int hh = 0; hh < 2; ++hh) {
-        u32x4 sh, sl, kh, kl, qh, ql;
-        split16(st[ti], 8 * hh, sh, sl);
-        const int d0 = 32 * ti + 16 * hh + 4 * g;
-        row8(I.k, n, d0, kh, kl);
-        row8(I.q, n, d0, qh, ql);
-        Pp[ti >> 1] = mma3(Pp[ti >> 1], kh, kl, sh, sl);
-        Rp[ti >> 1] = mma3(Rp[ti >> 1], qh, ql, sh, sl);
+        u32x4 xh, xl, th, tl;
+        split16(X, 8 * hh, xh, xl);
+        const float* trow = &I.rec[kRecT + n * kChunk + 16 * hh + 4 * g];
+        split8(*reinterpret_cast<const f32x4*>(trow), *reinterpret_cast<const f32x4*>(trow + 8),
+               th, tl);
+        Dp[hh] = mma3(f32x16{}, th, tl, xh, xl);
       }
-    }
-    const f32x16 P = Pp[0] + Pp[1], R = Rp[0] + Rp[1];
-    // X = beta (v - e^gamma P); Delta = T X (k index 8 g + jj <-> token
-    // 16 hh + 8 (jj / 4) + 4 g + jj % 4)
-    f32x16 X;
-#pragma unroll
-    for (int rr = 0; rr < 16; ++rr) {
-      const int t = c_row(rr, g);
-      X[rr] = I.rec[kRecBeta + t] * (bf(I.v[t][j]) - I.rec[kRecC + t] * P[rr]);
-    }
-    f32x16 Dp[2];
-#pragma unroll
-    for (int hh = 0; hh < 2; ++hh) {
-      u32x4 xh, xl, th, tl;
-      split16(X, 8 * hh, xh, xl);
-      const float* trow = &I.rec[kRecT + n * kChunk + 16 * hh + 4 * g];
-      split8(*reinterpret_cast<const f32x4*>(trow), *reinterpret_cast<const f32x4*>(trow + 8), th,
-             tl);
-      Dp[hh] = mma3(f32x16{}, th, tl, xh, xl);
-    }
-    f32x16 D = Dp[0] + Dp[1];
-    // O = e^gamma R + Bm Delta -> the recurrence output rows of this chunk
-    u32x4 dh[2], dl[2];
-    split16(D, 0, dh[0], dl[0]);
-    split16(D, 8, dh[1], dl[1]);
-    f32x16 Op[2];
-#pragma unroll
-    for (int hh = 0; hh < 2; ++hh) {
-      u32x4 bh, bl;
-      const float* brow = &I.rec[kRecB + n * kChunk + 16 * hh + 4 * g];
-      split8(*reinterpret_cast<const f32x4*>(brow), *reinterpret_cast<const f32x4*>(brow + 8), bh,
-             bl);
-      Op[hh] = mma3(f32x16{}, bh, bl, dh[hh], dl[hh]);
-    }
-    const f32x16 O = Op[0] + Op[1];
-#pragma unroll
-    for (int rr = 0; rr < 16; ++rr) {
-      const int t = c_row(rr, g);
-      if (t < ntok)
-        a.wcore[(int64_t)(tb + t) * (a.hv * kDv) + h * kDv + j] =
-            to_bf(fmaf(I.rec[kRecC + t], R[rr], O[rr]));   // .to(orig_dtype)
-    }
-    // S = e^(gamma_C) S0 + K^T (diag(e^(gamma_C - gamma)) Delta)
-#pragma unroll
-    for (int rr = 0; rr < 16; ++rr) D[rr] *= I.rec[kRecD + c_row(rr, g)];
-    split16(D, 0, dh[0], dl[0]);
-    split16(D, 8, dh[1], dl[1]);
-    const float cC = I.rec[kRecC + kChunk - 1];
-#pragma unroll
-    for (int ti = 0; ti < 4; ++ti) {
-      st[ti] *= cC;
+      f32x16 D = Dp[0] + Dp[1];
+      // O = e^gamma R + Bm Delta -> the recurrence output rows of this chunk
+      u32x4 dh[2], dl[2];
+      split16(D, 0, dh[0], dl[0]);
+      split16(D, 8, dh[1], dl[1]);
+      f32x16 Op[2];
 #pragma unroll
       for (int hh = 0; hh < 2; ++hh) {
-        // A operand: K^T row i = 32 ti + n at tokens s(jj) as for Delta
-        const int i = 32 * ti + n, s0 = 16 * hh + 4 * g;
-        const u32x2 h0 = *reinterpret_cast<const u32x2*>(&kt[0][i][s0]);
-        const u32x2 h1 = *reinterpret_cast<const u32x2*>(&kt[0][i][s0 + 8]);
-        const u32x2 l0 = *reinterpret_cast<const u32x2*>(&kt[1][i][s0]);
-        const u32x2 l1 = *reinterpret_cast<const u32x2*>(&kt[1][i][s0 + 8]);
-        const u32x4 ah = {h0[0], h0[1], h1[0], h1[1]}, al = {l0[0], l0[1], l1[0], l1[1]};
-        st[ti] = mma3(st[ti], ah, al, dh[hh], dl[hh]);
+        u32x4 bh, bl;
+        const float* brow = &I.rec[kRecB + n * kChunk + 16 * hh + 4 * g];
+        split8(*reinterpret_cast<const f32x4*>(brow), *reinterpret_cast<const f32x4*>(brow + 8),
+               bh, bl);
+        Op[hh] = mma3(f32x16{}, bh, bl, dh[hh], dl[hh]);
+      }
+      const f32x16 O = Op[0] + Op[1];
+#pragma unroll
+      for (int rr = 0; rr < 16; ++rr) {
+        const int t = c_row(rr, g);
+        otile[ci & 1][t][j] = to_bf(fmaf(I.rec[kRecC + t], R[rr], O[rr]));   // .to(orig_dtype)
+      }
+      // S = e^(gamma_C) S0 + K^T (diag(e^(gamma_C - gamma)) Delta)
+#pragma unroll
+      for (int rr = 0; rr < 16; ++rr) D[rr] *= I.rec[kRecD + c_row(rr, g)];
+      split16(D, 0, dh[0], dl[0]);
+      split16(D, 8, dh[1], dl[1]);
+      const float cC = I.rec[kRecC + kChunk - 1];
+#pragma unroll
+      for (int ti = 0; ti < 4; ++ti) {
+        st[ti] *= cC;
+#pragma unroll
+        for (int hh = 0; hh < 2; ++hh) {
+          // A operand: K^T row i = 32 ti + n at tokens s(jj) as for Delta
+          const int i = 32 * ti + n, s0 = 16 * hh + 4 * g;
+          const u32x2 h0 = *reinterpret_cast<const u32x2*>(&kT[0][i][s0]);
+          const u32x2 h1 = *reinterpret_cast<const u32x2*>(&kT[0][i][s0 + 8]);
+          const u32x2 l0 = *reinterpret_cast<const u32x2*>(&kT[1][i][s0]);
+          const u32x2 l1 = *reinterpret_cast<const u32x2*>(&kT[1][i][s0 + 8]);
+          const u32x4 ah = {h0[0], h0[1], h1[0], h1[1]}, al = {l0[0], l0[1], l1[0], l1[1]};
+          st[ti] = mma3(st[ti], ah, al, dh[hh], dl[hh]);
+        }
       }
     }
-  }
-  __syncthreads();   // every wave is done with the chunk buffers
-  {
-    float* mine = stage + 4 * g * kDv + j;
+    __syncthreads();   // the last chunk's output tile is complete
+    float* mine = stage + 4 * g * kDv + j;   // the chunk buffers are no longer read
 #pragma unroll
     for (int ti = 0; ti < 4; ++ti)
 #pragma unroll
       for (int rr = 0; rr < 16; ++rr)
         mine[(32 * ti + 8 * (rr >> 2) + (rr & 3)) * kDv] = st[ti][rr];
-  }
-  __syncthreads();
+  } else {
+    const int key0 = chunk_key(a, bi);
+    // Chunk ci into buffer bf (tokens past the last one re-read the last
+    // token; the record gives them beta = 0 and g = 0).  Helper wave w moves q
+    // and k rows 8 w .. 8 w + 7 (4 + 4 instructions, two rows each), V rows
+    // 8 w .. + 7 (2) and 3 KB of the record (waves 0-2 of the helpers).
+    const uint8_t* qk_base = reinterpret_cast<const uint8_t*>(a.wqk) + (int64_t)hk * 1024;
+    const uint8_t* v_base =
+        reinterpret_cast<const uint8_t*>(a.ws) + ((int64_t)2 * a.key_dim + h * kDv) * 2;
+    const uint8_t* rec_base = reinterpret_cast<const uint8_t*>(a.wrec) + (int64_t)h * kRec * 4;
+    auto issue = [&](int ci) __attribute__((always_inline)) {
+      const int tb = t0 + kChunk * ci;
+      ChunkIn& I = sm[ci & 1];
 #pragma unroll
-  for (int i = 0; i < kDk * kDv / 4 / kThreads; ++i) {
-    const int q = i * kThreads + threadIdx.x;
+      for (int p = 0; p < 4; ++p) {
+        const int t = 8 * w + 2 * p + g;
+        const uint32_t row = (uint32_t)min(tb + t, last) * (uint32_t)a.hk * 1024u;
+        const uint32_t cpos = (uint32_t)((n & 16) | ((n & 15) ^ (t & 15))) * 16u;
+        dma16(qk_base, row + cpos, lds_addr(&I.q[8 * w + 2 * p][0]));
+        dma16(qk_base, row + 512u + cpos, lds_addr(&I.k[8 * w + 2 * p][0]));
+      }
+#pragma unroll
+      for (int p = 0; p < 2; ++p) {
+        const int t = 8 * w + 4 * p + (lane >> 4);
+        dma16(v_base,
+              (uint32_t)min(tb + t, last) * (uint32_t)a.conv_dim * 2u + 16u * (lane & 15),
+              lds_addr(&I.v[8 * w + 4 * p][0]));
+      }
+      if (w < 3) {
+        const uint32_t rec = (uint32_t)(key0 + ci) * (uint32_t)a.hv * (uint32_t)(kRec * 4);
+#pragma unroll
+        for (int p = 0; p < 3; ++p)
+          dma16(rec_base, rec + 1024u * (3 * w + p) + 16u * lane,
+                lds_addr(&I.rec[256 * (3 * w + p)]));
+      }
+    };
+    // Helper thread (part, dim) = (ht / 128, ht % 128) transposes its 32
+    // tokens of chunk ci's k, once the chunk has landed.
+    auto transpose = [&](int ci) __attribute__((always_inline)) {
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      const ChunkIn& I = sm[ci & 1];
+      const int i = ht & (kDk - 1), part = ht >> 7;
+#pragma unroll
+      for (int s2 = 0; s2 < kChunk; s2 += 2)
+        *reinterpret_cast<uint32_t*>(&kt[ci & 1][part][i][s2]) =
+            row_half(I.k, s2, i, part) | (row_half(I.k, s2 + 1, i, part) << 16);
+    };
+    // Gated RMSNorm (rms_norm_gated.py:26-40) of chunk cj's rows: helper
+    // thread (token, part) = (ht / 8, ht % 8) takes dims 16 part .. + 15 of
+    // one row (the row's sum of squares is an 8-lane sum) with its z values
+    // in zr, loaded a chunk ahead; out = bf16(norm_w * (o / rms(o)) *
+    // silu(z)), and core_out gets o.
+    const int te = ht >> 3, c0 = 16 * (ht & 7);
+    u32x2 zr[4];
+    auto load_z = [&](int cj) __attribute__((always_inline)) {
+      const int row = min(t0 + kChunk * cj + te, last);
+      const uint16_t* zrow = a.z + (int64_t)row * a.z_rs + h * kDv + c0;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) zr[e] = *reinterpret_cast<const u32x2*>(zrow + 4 * e);
+    };
+    auto norm_rows = [&](int cj) __attribute__((always_inline)) {
+      const int row = t0 + kChunk * cj + te;
+      const u32x4 ob[2] = {*reinterpret_cast<const u32x4*>(&otile[cj & 1][te][c0]),
+                           *reinterpret_cast<const u32x4*>(&otile[cj & 1][te][c0 + 8])};
+      float ss = 0.f;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const uint32_t wd = ob[e >> 2][e & 3];
+        ss = fmaf(bf16_lo(wd), bf16_lo(wd), ss);
+        ss = fmaf(bf16_hi(wd), bf16_hi(wd), ss);
+      }
+      ss = row_sum8(ss);
+      if (row > last) return;   // padding of the request's last chunk
+      const float inv = rsqrtf(ss / (float)kDv + a.eps);
+      uint16_t* orow = a.out + (int64_t)row * a.out_rs + h * kDv + c0;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const uint32_t o01 = ob[e >> 1][2 * (e & 1)], o23 = ob[e >> 1][2 * (e & 1) + 1];
+        const float o[4] = {bf16_lo(o01), bf16_hi(o01), bf16_lo(o23), bf16_hi(o23)};
+        const float z[4] = {bf16_lo(zr[e][0]), bf16_hi(zr[e][0]), bf16_lo(zr[e][1]),
+                            bf16_hi(zr[e][1])};
+        float y[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+          y[k] = nw[c0 + 4 * e + k] * (o[k] * inv) * (z[k] / (1.f + expf(-z[k])));
+        *reinterpret_cast<u32x2*>(orow + 4 * e) =
+            u32x2{pack_bf16(y[0], y[1]), pack_bf16(y[2], y[3])};
+        if (a.core)
+          *reinterpret_cast<u32x2*>(a.core + (int64_t)row * a.core_rs + h * kDv + c0 + 4 * e) =
+              u32x2{o01, o23};
+      }
+    };
+
+    __syncthreads();   // the state waves have read the staging area
+    issue(0);
+    transpose(0);
+    for (int ci = 0; ci < nchunks; ++ci) {
+      __syncthreads();   // the state waves start chunk ci and are done with chunk ci - 1
+      if (ci + 1 < nchunks) issue(ci + 1);
+      if (ci > 0) norm_rows(ci - 1);
+      load_z(ci);
+      if (ci + 1 < nchunks) transpose(ci + 1);
+    }
+    __syncthreads();   // the last chunk's output tile is complete
+    norm_rows(nchunks - 1);
+  }
+  __syncthreads();   // the final state is staged
+#pragma unroll
+  for (int i = 0; i < kDk * kDv / 4 / kChunkThreads; ++i) {
+    const int q = i * kChunkThreads + threadIdx.x;
     reinterpret_cast<f32x4*>(S)[q] = reinterpret_cast<const f32x4*>(stage)[q];
   }
 }
 
-// Gated RMSNorm (rms_norm_gated.py:26-40) of two (token, value head) rows per
-// wave from the bf16 recurrence output: each half-wave takes one head, lane l
-// of it dims 4 l .. 4 l + 3, and the sum of squares is a 32-lane reduction
-// (grid: token rows x blocks of 8 value heads).  Also copies the recurrence
-// output to core_out when asked.  Rows of requests whose slot is outside the
-// pool are written as zeros (in out and core_out); rows of other one-token
-// requests were written by gdn_recur_kernel.
-constexpr int kNormHeads = 2 * kThreads / kWave;   // value heads per workgroup
+// Rows that no request owns, or whose request's slot is outside the pool,
+// read as zeros in out and core_out; gdn_recur_kernel and gdn_chunk_ext_kernel
+// write every other row.  One wave per row.
+constexpr int kZeroRows = kThreads / kWave;   // rows per workgroup
 
-__global__ void __launch_bounds__(kThreads) gdn_norm_ext_kernel(GdnArgs a) {
-  const int tok = blockIdx.x;
+__global__ void __launch_bounds__(kThreads) gdn_zero_ext_kernel(GdnArgs a) {
+  const int64_t tok = (int64_t)blockIdx.x * kZeroRows + wave_id();
+  if (tok >= a.rows || a.owner[tok] >= 0) return;
   const int lane = threadIdx.x & (kWave - 1);
-  const int h = blockIdx.y * kNormHeads + 2 * wave_id() + (lane >> 5);
-  const bool act = h < a.hv;
-  const int d = 4 * (lane & 31);
-  const int bo = a.owner[tok];
-  if (bo < 0) {
-    if (act) {
-      *reinterpret_cast<u32x2*>(a.out + tok * a.out_rs + h * kDv + d) = u32x2{0u, 0u};
-      if (a.core) *reinterpret_cast<u32x2*>(a.core + tok * a.core_rs + h * kDv + d) = u32x2{0u, 0u};
-    }
-    return;
+  for (int d = 4 * lane; d < a.hv * kDv; d += 4 * kWave) {
+    *reinterpret_cast<u32x2*>(a.out + tok * a.out_rs + d) = u32x2{0u, 0u};
+    if (a.core) *reinterpret_cast<u32x2*>(a.core + tok * a.core_rs + d) = u32x2{0u, 0u};
   }
-  if (min(max(a.tok[bo + 1], 0), a.rows) - min(max(a.tok[bo], 0), a.rows) == 1)
-    return;   // a one-token request: gdn_recur_kernel wrote its row
-  const int hc = act ? h : 0;
-  const u32x2 ob =
-      *reinterpret_cast<const u32x2*>(a.wcore + (int64_t)tok * (a.hv * kDv) + hc * kDv + d);
-  const float o[4] = {bf16_lo(ob[0]), bf16_hi(ob[0]), bf16_lo(ob[1]), bf16_hi(ob[1])};
-  float v2 = act ? o[0] * o[0] + o[1] * o[1] + o[2] * o[2] + o[3] * o[3] : 0.f;
-#pragma unroll
-  for (int s2 = 16; s2 >= 1; s2 >>= 1) v2 += __shfl_xor(v2, s2, kWave);
-  if (!act) return;
-  if (a.core) *reinterpret_cast<u32x2*>(a.core + tok * a.core_rs + h * kDv + d) = ob;
-  const float inv = rsqrtf(v2 / (float)kDv + a.eps);
-  const u32x2 zz = *reinterpret_cast<const u32x2*>(a.z + tok * a.z_rs + h * kDv + d);
-  const float z[4] = {bf16_lo(zz[0]), bf16_hi(zz[0]), bf16_lo(zz[1]), bf16_hi(zz[1])};
-  const f32x4 nw = *reinterpret_cast<const f32x4*>(a.norm_w + h * kDv + d);
-  float y[4];
-#pragma unroll
-  for (int e = 0; e < 4; ++e) y[e] = nw[e] * (o[e] * inv) * (z[e] / (1.f + expf(-z[e])));
-  *reinterpret_cast<u32x2*>(a.out + tok * a.out_rs + h * kDv + d) =
-      u32x2{pack_bf16(y[0], y[1]), pack_bf16(y[2], y[3])};
 }
 
 }  // namespace
@@ -831,11 +880,10 @@ int64_t tf_gdn_decode_workspace_bytes(int32_t batch_size, int32_t num_k_heads,
 
 namespace tfa {
 // Extend workspace bytes per token row: conv outputs (bf16), normalised q / k
-// (bf16 high and low parts), gates (fp32), the recurrence output (bf16) and
-// the row's request (int32).
+// (bf16 high and low parts), gates (fp32) and the row's request (int32).
 int64_t gdn_ext_row_bytes(int32_t hk, int32_t hv) {
   const int64_t conv_dim = 2LL * hk * kDk + (int64_t)hv * kDv;
-  return conv_dim * 2 + (int64_t)hk * 4 * kDk * 2 + (int64_t)hv * 2 * 4 + (int64_t)hv * kDv * 2 + 4;
+  return conv_dim * 2 + (int64_t)hk * 4 * kDk * 2 + (int64_t)hv * 2 * 4 + 4;
 }
 // Chunk-record slots: chunk ci of request b is slot floor(t0_b / 32) + b + ci.
 int64_t gdn_chunk_slots(int64_t n_tokens, int32_t batch) { return n_tokens / kChunk + batch + 1; }
@@ -917,13 +965,78 @@ int32_t gdn_setup(const char* fn, const void* qkv, int64_t qkv_row_stride, const
   g->wg = nullptr;
   g->owner = nullptr;
   g->wrec = nullptr;
-  g->wcore = nullptr;
   g->ws = static_cast<uint16_t*>(workspace);
   g->out = static_cast<uint16_t*>(out);
   g->out_rs = out_row_stride;
   g->core = static_cast<uint16_t*>(core_out);
   g->core_rs = core_row_stride;
   return TF_OK;
+}
+
+// A second stream per device for tf_gdn_extend: the one-token requests'
+// recurrence runs there beside the chunked pass.  That pass holds one
+// workgroup per (multi-token request, value head) for the whole extend at a
+// small share of the HBM bandwidth, so the HBM-bound one-token updates fit
+// beside it (they touch other state slots and output rows, so the two need
+// no order between them).  The stream and its fork / join events are made on
+// the first call that is not under graph capture; `mu` keeps the fork .. join
+// sequences of concurrent callers apart.
+struct SideLane {
+  std::mutex mu;
+  hipStream_t stream = nullptr;
+  hipEvent_t fork = nullptr, join = nullptr;
+  bool ready = false;
+};
+constexpr int kLaneDevices = 64;
+SideLane g_lanes[kLaneDevices];
+
+// The lane of the stream's device, or nullptr when there is none to use (a
+// first call under capture, an unknown device or a creation error: the caller
+// then launches everything on its own stream).  Clears the HIP error of a
+// failed query, so the caller checks its own launches before calling this.
+SideLane* side_lane(hipStream_t s) {
+  int dev = -1;
+  if (s) {
+    hipDevice_t d = -1;
+    if (hipStreamGetDevice(s, &d) != hipSuccess) {
+      (void)hipGetLastError();
+      return nullptr;
+    }
+    dev = d;
+  } else if (hipGetDevice(&dev) != hipSuccess) {
+    (void)hipGetLastError();
+    return nullptr;
+  }
+  if (dev < 0 || dev >= kLaneDevices) return nullptr;
+  SideLane& L = g_lanes[dev];
+  std::lock_guard<std::mutex> lock(L.mu);
+  if (L.ready) return &L;
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  int cur = -1;
+  if (hipStreamIsCapturing(s, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone ||
+      hipGetDevice(&cur) != hipSuccess || (cur != dev && hipSetDevice(dev) != hipSuccess)) {
+    (void)hipGetLastError();
+    return nullptr;
+  }
+  const bool ok = hipStreamCreateWithFlags(&L.stream, hipStreamNonBlocking) == hipSuccess &&
+                  hipEventCreateWithFlags(&L.fork, hipEventDisableTiming) == hipSuccess &&
+                  hipEventCreateWithFlags(&L.join, hipEventDisableTiming) == hipSuccess;
+  if (!ok) {
+    if (L.join) (void)hipEventDestroy(L.join);
+    if (L.fork) (void)hipEventDestroy(L.fork);
+    if (L.stream) (void)hipStreamDestroy(L.stream);
+    L.stream = nullptr;
+    L.fork = L.join = nullptr;
+  }
+  if (cur != dev) (void)hipSetDevice(cur);
+  (void)hipGetLastError();
+  L.ready = ok;
+  return ok ? &L : nullptr;
+}
+
+int32_t side_failure(const char* what, hipError_t e) {
+  (void)hipGetLastError();
+  return tfa::fail(TF_ERR_HIP, "tf_gdn_extend: %s: %s", what, hipGetErrorString(e));
 }
 
 }  // namespace
@@ -1000,7 +1113,7 @@ int32_t tf_gdn_extend(const void* qkv, int64_t qkv_row_stride, const void* a, co
   const int64_t n_slots_rec = gdn_chunk_slots(n_tokens, batch_size);
   if (n_tokens > 65535LL * kConvTokens || n_tokens * num_k_heads * 4 * kDk * 2 > UINT32_MAX ||
       n_tokens * g.conv_dim * 2 > UINT32_MAX || n_tokens * num_v_heads * 8 > UINT32_MAX ||
-      n_slots_rec * num_v_heads * kRec * 4 > UINT32_MAX)
+      n_slots_rec * num_v_heads * kRec * 4 > UINT32_MAX || z_row_stride * 2 * kChunk > UINT32_MAX)
     return fail(TF_ERR_UNSUPPORTED, "gdn_extend: too many tokens (32-bit staging offsets)");
   if ((reinterpret_cast<uintptr_t>(qkv) & 7u) || qkv_row_stride % 4 ||
       (reinterpret_cast<uintptr_t>(z) & 7u) || z_row_stride % 4 ||
@@ -1015,11 +1128,9 @@ int32_t tf_gdn_extend(const void* qkv, int64_t qkv_row_stride, const void* a, co
   const int64_t conv_bytes = n_tokens * g.conv_dim * 2;
   const int64_t qk_bytes = n_tokens * num_k_heads * 4 * kDk * 2;
   const int64_t gate_bytes = n_tokens * num_v_heads * 2 * 4;
-  const int64_t core_bytes = n_tokens * num_v_heads * kDv * 2;
   g.wqk = reinterpret_cast<uint16_t*>(w + ((conv_bytes + 15) & ~15LL));
   g.wg = reinterpret_cast<float*>(reinterpret_cast<uint8_t*>(g.wqk) + qk_bytes);
-  g.wcore = reinterpret_cast<uint16_t*>(reinterpret_cast<uint8_t*>(g.wg) + gate_bytes);
-  g.owner = reinterpret_cast<int32_t*>(reinterpret_cast<uint8_t*>(g.wcore) + core_bytes);
+  g.owner = reinterpret_cast<int32_t*>(reinterpret_cast<uint8_t*>(g.wg) + gate_bytes);
   g.wrec = reinterpret_cast<float*>(w + ((n_tokens * gdn_ext_row_bytes(num_k_heads, num_v_heads) +
                                           64) & ~15LL));
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
@@ -1037,13 +1148,35 @@ int32_t tf_gdn_extend(const void* qkv, int64_t qkv_row_stride, const void* a, co
                      dim3(kThreads), 0, s, g);
   hipLaunchKernelGGL(gdn_chunk_prep_kernel, dim3((uint32_t)n_slots_rec, num_k_heads),
                      dim3(kThreads), 0, s, g);
+  const int32_t pre = launch_status("tf_gdn_extend launch");
+  if (pre != TF_OK) return pre;
+  // The one-token recurrence on the side stream, beside the chunked pass,
+  // when the batch can hold both kinds of request; it needs only the conv
+  // outputs, and the caller's stream waits for it before the call's end.
+  SideLane* lane = (max_extend_len > 1 && batch_size > 1) ? side_lane(s) : nullptr;
+  std::unique_lock<std::mutex> held;
+  hipStream_t rs = s;
+  if (lane) {
+    held = std::unique_lock<std::mutex>(lane->mu);
+    hipError_t e = hipEventRecord(lane->fork, s);
+    if (e == hipSuccess) e = hipStreamWaitEvent(lane->stream, lane->fork, 0);
+    if (e != hipSuccess) return side_failure("fork to the side stream", e);
+    rs = lane->stream;
+  }
   hipLaunchKernelGGL(gdn_recur_kernel, dim3((int64_t)batch_size * num_v_heads), dim3(kThreads), 0,
-                     s, g);
+                     rs, g);
+  if (lane) {
+    const hipError_t e = hipEventRecord(lane->join, rs);
+    if (e != hipSuccess) return side_failure("join event", e);
+  }
   hipLaunchKernelGGL(gdn_chunk_ext_kernel, dim3((int64_t)batch_size * num_v_heads),
+                     dim3(kChunkThreads), 0, s, g);
+  hipLaunchKernelGGL(gdn_zero_ext_kernel, dim3((uint32_t)((n_tokens + kZeroRows - 1) / kZeroRows)),
                      dim3(kThreads), 0, s, g);
-  hipLaunchKernelGGL(gdn_norm_ext_kernel,
-                     dim3((uint32_t)n_tokens, (num_v_heads + kNormHeads - 1) / kNormHeads),
-                     dim3(kThreads), 0, s, g);
+  if (lane) {
+    const hipError_t e = hipStreamWaitEvent(s, lane->join, 0);
+    if (e != hipSuccess) return side_failure("join with the side stream", e);
+  }
   return launch_status("tf_gdn_extend launch");
 }
 

@@ -111,18 +111,6 @@ __device__ __forceinline__ const __bf16* row_ptr(const PrepArgs& a, int64_t t, i
   return a.v + t * a.v_tok + (int64_t)(r - a.hq - a.hkv) * kD;
 }
 
-// Sum over the 8 lanes of a row; every lane gets the same bits (each step adds
-// the same two operands in every lane of a pair).
-__device__ __forceinline__ float row_sum8(float v) {
-  v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(
-                                     0, __builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, false));
-  v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(
-                                     0, __builtin_bit_cast(int, v), 0x4E, 0xF, 0xF, false));
-  v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(
-                                     0, __builtin_bit_cast(int, v), 0x141, 0xF, 0xF, false));
-  return v;
-}
-
 __device__ __forceinline__ void unpack8(const u32x4& r, float (&x)[8]) {
 #pragma unroll
   for (int k = 0; k < 4; ++k) {

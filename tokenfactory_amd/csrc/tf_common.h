@@ -122,6 +122,18 @@ __device__ __forceinline__ int wave_id() {
 }
 
 // ---------------------------------------------------------------- math
+// Sum over the 8 lanes of a row; every lane gets the same bits (each step adds
+// the same two operands in every lane of a pair).
+__device__ __forceinline__ float row_sum8(float v) {
+  v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(
+                                     0, __builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, false));
+  v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(
+                                     0, __builtin_bit_cast(int, v), 0x4E, 0xF, 0xF, false));
+  v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(
+                                     0, __builtin_bit_cast(int, v), 0x141, 0xF, 0xF, false));
+  return v;
+}
+
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
 __device__ __forceinline__ float wave_max_xor(float v, int mask) {
