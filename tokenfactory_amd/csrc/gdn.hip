@@ -590,15 +590,19 @@ constexpr int kChunkThreads = 2 * kThreads;   // 4 recurrence waves + 4 helper w
 
 // Waves 0-3 carry the state through the chunks (the MFMA work above, nothing
 // else); waves 4-7, the helpers, share their SIMDs and keep the inputs ahead
-// of them: while the state waves work on chunk ci, the helpers move chunk
-// ci + 1 into LDS, transpose its k, and apply the gated norm to the rows of
-// chunk ci - 1.  One barrier per chunk hands the buffers over (chunk inputs,
-// the transposed k and the output tile are double-buffered by chunk parity).
+// of them: while the state waves work on chunk ci, the helpers transpose its
+// k (needed only by the state update at the end of the chunk; a workgroup
+// counter in LDS says when it is written), move chunk ci + 1 into LDS and
+// apply the gated norm to the rows of chunk ci - 1.  One barrier per chunk
+// hands the buffers over (chunk inputs and the output tile are
+// double-buffered by chunk parity).
 __global__ void __launch_bounds__(kChunkThreads) gdn_chunk_ext_kernel(GdnArgs a) {
   __shared__ __attribute__((aligned(16))) ChunkIn sm[2];
-  // k of a chunk transposed, [part][dim][token]: the state update reads 4
-  // tokens of one dim per 8-byte load.
-  __shared__ __attribute__((aligned(16))) uint16_t kt[2][2][kDk][kKtStride];
+  // k of the current chunk transposed, [part][dim][token]: the state update
+  // reads 4 tokens of one dim per 8-byte load.  kt_count: helper waves done
+  // with it so far (4 per chunk).
+  __shared__ __attribute__((aligned(16))) uint16_t kt[2][kDk][kKtStride];
+  __shared__ int kt_count;
   // A chunk's recurrence output (o rounded to bf16), token-major, and the
   // head's norm weights.
   __shared__ __attribute__((aligned(16))) uint16_t otile[2][kChunk][kDv];
@@ -629,6 +633,7 @@ __global__ void __launch_bounds__(kChunkThreads) gdn_chunk_ext_kernel(GdnArgs a)
     reinterpret_cast<f32x4*>(stage)[q] = reinterpret_cast<const f32x4*>(S)[q];
   }
   nw[threadIdx.x & (kDv - 1)] = a.norm_w[h * kDv + (threadIdx.x & (kDv - 1))];   // 4 writers each
+  if (threadIdx.x == 0) kt_count = 0;
   __syncthreads();
 
   if (!helper) {
@@ -646,8 +651,7 @@ __global__ void __launch_bounds__(kChunkThreads) gdn_chunk_ext_kernel(GdnArgs a)
 
     for (int ci = 0; ci < nchunks; ++ci) {
       const ChunkIn& I = sm[ci & 1];
-      const uint16_t(*kT)[kDk][kKtStride] = kt[ci & 1];
-      __syncthreads();   // chunk ci and its transposed k are in; its output tile is free
+      __syncthreads();   // chunk ci is in; its output tile is free
 
       // P = K S0 and R = Q S0 over the state rows (k index 8 g + jj <-> state
       // row 32 ti + 16 hh + 8 (jj / 4) + 4 g + jj % 4)
@@ -706,7 +710,16 @@ __global__ void __launch_bounds__(kChunkThreads) gdn_chunk_ext_kernel(GdnArgs a)
         const int t = c_row(rr, g);
         otile[ci & 1][t][j] = to_bf(fmaf(I.rec[kRecC + t], R[rr], O[rr]));   // .to(orig_dtype)
       }
-      // S = e^(gamma_C) S0 + K^T (diag(e^(gamma_C - gamma)) Delta)
+      // S = e^(gamma_C) S0 + K^T (diag(e^(gamma_C - gamma)) Delta), once the
+      // helpers have written kt (a bounded wait: after 2^22 polls the state
+      // waves go on, so a lost count cannot hang the kernel)
+      for (int spin = 0; spin < (1 << 22); ++spin) {
+        if (__hip_atomic_load(&kt_count, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) >=
+            4 * (ci + 1))
+          break;
+        __builtin_amdgcn_s_sleep(1);
+      }
+      asm volatile("" ::: "memory");
 #pragma unroll
       for (int rr = 0; rr < 16; ++rr) D[rr] *= I.rec[kRecD + c_row(rr, g)];
       split16(D, 0, dh[0], dl[0]);
@@ -719,10 +732,10 @@ __global__ void __launch_bounds__(kChunkThreads) gdn_chunk_ext_kernel(GdnArgs a)
         for (int hh = 0; hh < 2; ++hh) {
           // A operand: K^T row i = 32 ti + n at tokens s(jj) as for Delta
           const int i = 32 * ti + n, s0 = 16 * hh + 4 * g;
-          const u32x2 h0 = *reinterpret_cast<const u32x2*>(&kT[0][i][s0]);
-          const u32x2 h1 = *reinterpret_cast<const u32x2*>(&kT[0][i][s0 + 8]);
-          const u32x2 l0 = *reinterpret_cast<const u32x2*>(&kT[1][i][s0]);
-          const u32x2 l1 = *reinterpret_cast<const u32x2*>(&kT[1][i][s0 + 8]);
+          const u32x2 h0 = *reinterpret_cast<const u32x2*>(&kt[0][i][s0]);
+          const u32x2 h1 = *reinterpret_cast<const u32x2*>(&kt[0][i][s0 + 8]);
+          const u32x2 l0 = *reinterpret_cast<const u32x2*>(&kt[1][i][s0]);
+          const u32x2 l1 = *reinterpret_cast<const u32x2*>(&kt[1][i][s0 + 8]);
           const u32x4 ah = {h0[0], h0[1], h1[0], h1[1]}, al = {l0[0], l0[1], l1[0], l1[1]};
           st[ti] = mma3(st[ti], ah, al, dh[hh], dl[hh]);
         }
@@ -772,15 +785,18 @@ __global__ void __launch_bounds__(kChunkThreads) gdn_chunk_ext_kernel(GdnArgs a)
       }
     };
     // Helper thread (part, dim) = (ht / 128, ht % 128) transposes its 32
-    // tokens of chunk ci's k, once the chunk has landed.
+    // tokens of chunk ci's k; each helper wave then adds one to kt_count
+    // (its LDS writes complete first).
     auto transpose = [&](int ci) __attribute__((always_inline)) {
-      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
       const ChunkIn& I = sm[ci & 1];
       const int i = ht & (kDk - 1), part = ht >> 7;
 #pragma unroll
       for (int s2 = 0; s2 < kChunk; s2 += 2)
-        *reinterpret_cast<uint32_t*>(&kt[ci & 1][part][i][s2]) =
+        *reinterpret_cast<uint32_t*>(&kt[part][i][s2]) =
             row_half(I.k, s2, i, part) | (row_half(I.k, s2 + 1, i, part) << 16);
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+      if (lane == 0)
+        __hip_atomic_fetch_add(&kt_count, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
     };
     // Gated RMSNorm (rms_norm_gated.py:26-40) of chunk cj's rows: helper
     // thread (token, part) = (ht / 8, ht % 8) takes dims 16 part .. + 15 of
@@ -830,13 +846,14 @@ __global__ void __launch_bounds__(kChunkThreads) gdn_chunk_ext_kernel(GdnArgs a)
 
     __syncthreads();   // the state waves have read the staging area
     issue(0);
-    transpose(0);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     for (int ci = 0; ci < nchunks; ++ci) {
       __syncthreads();   // the state waves start chunk ci and are done with chunk ci - 1
       if (ci + 1 < nchunks) issue(ci + 1);
+      transpose(ci);
       if (ci > 0) norm_rows(ci - 1);
       load_z(ci);
-      if (ci + 1 < nchunks) transpose(ci + 1);
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   // chunk ci + 1 has landed
     }
     __syncthreads();   // the last chunk's output tile is complete
     norm_rows(nchunks - 1);
