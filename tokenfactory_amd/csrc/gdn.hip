@@ -606,7 +606,7 @@ __global__ void __launch_bounds__(kChunkThreads) gdn_chunk_ext_kernel(GdnArgs a)
   // A chunk's recurrence output (o rounded to bf16), token-major, and the
   // head's norm weights.
   __shared__ __attribute__((aligned(16))) uint16_t otile[2][kChunk][kDv];
-  __shared__ float nw[kDv];
+  __shared__ __attribute__((aligned(16))) float nw[kDv];
   const int bi = blockIdx.x / a.hv, h = blockIdx.x % a.hv;
   const int hk = h / a.vpk;
   const int lane = threadIdx.x & (kWave - 1), wv = wave_id();
@@ -680,15 +680,15 @@ __global__ void __launch_bounds__(kChunkThreads) gdn_chunk_ext_kernel(GdnArgs a)
         const int t = c_row(rr, g);
         X[rr] = I.rec[kRecBeta + t] * (bf(I.v[t][j]) - I.rec[kRecC + t] * P[rr]);
       }
+      // (T and Bm arrive split into bf16 high / low operand halves: split_tb)
       f32x16 Dp[2];
 #pragma unroll
       for (int hh = 0; hh < 2; ++hh) {
-        u32x4 xh, xl, th, tl;
+        u32x4 xh, xl;
         split16(X, 8 * hh, xh, xl);
-        const float* trow = &I.rec[kRecT + n * kChunk + 16 * hh + 4 * g];
-        split8(*reinterpret_cast<const f32x4*>(trow), *reinterpret_cast<const f32x4*>(trow + 8),
-               th, tl);
-        Dp[hh] = mma3(f32x16{}, th, tl, xh, xl);
+        const u32x4* tp =
+            reinterpret_cast<const u32x4*>(&I.rec[kRecT + n * kChunk + 16 * hh + 8 * g]);
+        Dp[hh] = mma3(f32x16{}, tp[0], tp[1], xh, xl);
       }
       f32x16 D = Dp[0] + Dp[1];
       // O = e^gamma R + Bm Delta -> the recurrence output rows of this chunk
@@ -698,11 +698,9 @@ __global__ void __launch_bounds__(kChunkThreads) gdn_chunk_ext_kernel(GdnArgs a)
       f32x16 Op[2];
 #pragma unroll
       for (int hh = 0; hh < 2; ++hh) {
-        u32x4 bh, bl;
-        const float* brow = &I.rec[kRecB + n * kChunk + 16 * hh + 4 * g];
-        split8(*reinterpret_cast<const f32x4*>(brow), *reinterpret_cast<const f32x4*>(brow + 8),
-               bh, bl);
-        Op[hh] = mma3(f32x16{}, bh, bl, dh[hh], dl[hh]);
+        const u32x4* bp =
+            reinterpret_cast<const u32x4*>(&I.rec[kRecB + n * kChunk + 16 * hh + 8 * g]);
+        Op[hh] = mma3(f32x16{}, bp[0], bp[1], dh[hh], dl[hh]);
       }
       const f32x16 O = Op[0] + Op[1];
 #pragma unroll
@@ -798,18 +796,45 @@ __global__ void __launch_bounds__(kChunkThreads) gdn_chunk_ext_kernel(GdnArgs a)
       if (lane == 0)
         __hip_atomic_fetch_add(&kt_count, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
     };
+    // T and Bm of chunk ci (fp32 rows of 32) split in place into the state
+    // waves' MFMA operand halves: block b of 16 floats (row n, half hh of T
+    // for b < 64, of Bm after) becomes, for g = 0 and 1, the bf16 high parts
+    // of columns 16 hh + 4 g + {0..3, 8..11} (16 bytes) and then the bf16
+    // roundings of their remainders (16 bytes).  Lane l of helper wave w < 3
+    // takes block 48 w + l: the record floats 768 w .. 768 w + 767 that this
+    // wave's own DMA brought in, so its vmcnt wait covers them.
+    auto split_tb = [&](int ci) __attribute__((always_inline)) {
+      const int b = 48 * w + lane;
+      if (w >= 3 || lane >= 48 || b >= 2 * 2 * kChunk) return;
+      static_assert(kRecT == 0 && kRecB == 2 * kChunk * 16, "record layout");
+      float* blk = &sm[ci & 1].rec[16 * b];
+      const f32x4 x0 = *reinterpret_cast<const f32x4*>(blk);
+      const f32x4 x1 = *reinterpret_cast<const f32x4*>(blk + 4);
+      const f32x4 x2 = *reinterpret_cast<const f32x4*>(blk + 8);
+      const f32x4 x3 = *reinterpret_cast<const f32x4*>(blk + 12);
+      u32x4 h0, l0, h1, l1;
+      split8(x0, x2, h0, l0);
+      split8(x1, x3, h1, l1);
+      u32x4* out = reinterpret_cast<u32x4*>(blk);
+      out[0] = h0;
+      out[1] = l0;
+      out[2] = h1;
+      out[3] = l1;
+    };
     // Gated RMSNorm (rms_norm_gated.py:26-40) of chunk cj's rows: helper
     // thread (token, part) = (ht / 8, ht % 8) takes dims 16 part .. + 15 of
     // one row (the row's sum of squares is an 8-lane sum) with its z values
     // in zr, loaded a chunk ahead; out = bf16(norm_w * (o / rms(o)) *
-    // silu(z)), and core_out gets o.
+    // silu(z)) with silu(z) = z / (1 + e^-z) from the hardware exp2 and
+    // reciprocal (about 1 ulp each in fp32, below the bf16 rounding of the
+    // output), and core_out gets o.
     const int te = ht >> 3, c0 = 16 * (ht & 7);
-    u32x2 zr[4];
+    u32x2 zr[4], zn[4];
     auto load_z = [&](int cj) __attribute__((always_inline)) {
       const int row = min(t0 + kChunk * cj + te, last);
       const uint16_t* zrow = a.z + (int64_t)row * a.z_rs + h * kDv + c0;
 #pragma unroll
-      for (int e = 0; e < 4; ++e) zr[e] = *reinterpret_cast<const u32x2*>(zrow + 4 * e);
+      for (int e = 0; e < 4; ++e) zn[e] = *reinterpret_cast<const u32x2*>(zrow + 4 * e);
     };
     auto norm_rows = [&](int cj) __attribute__((always_inline)) {
       const int row = t0 + kChunk * cj + te;
@@ -832,10 +857,12 @@ __global__ void __launch_bounds__(kChunkThreads) gdn_chunk_ext_kernel(GdnArgs a)
         const float o[4] = {bf16_lo(o01), bf16_hi(o01), bf16_lo(o23), bf16_hi(o23)};
         const float z[4] = {bf16_lo(zr[e][0]), bf16_hi(zr[e][0]), bf16_lo(zr[e][1]),
                             bf16_hi(zr[e][1])};
+        const f32x4 wn = *reinterpret_cast<const f32x4*>(&nw[c0 + 4 * e]);
         float y[4];
 #pragma unroll
         for (int k = 0; k < 4; ++k)
-          y[k] = nw[c0 + 4 * e + k] * (o[k] * inv) * (z[k] / (1.f + expf(-z[k])));
+          y[k] = wn[k] * (o[k] * inv) *
+                 (z[k] * __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(-z[k] * kLog2e)));
         *reinterpret_cast<u32x2*>(orow + 4 * e) =
             u32x2{pack_bf16(y[0], y[1]), pack_bf16(y[2], y[3])};
         if (a.core)
@@ -847,13 +874,17 @@ __global__ void __launch_bounds__(kChunkThreads) gdn_chunk_ext_kernel(GdnArgs a)
     __syncthreads();   // the state waves have read the staging area
     issue(0);
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    split_tb(0);
     for (int ci = 0; ci < nchunks; ++ci) {
       __syncthreads();   // the state waves start chunk ci and are done with chunk ci - 1
+      load_z(ci);
       if (ci + 1 < nchunks) issue(ci + 1);
       transpose(ci);
       if (ci > 0) norm_rows(ci - 1);
-      load_z(ci);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) zr[e] = zn[e];
       asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   // chunk ci + 1 has landed
+      if (ci + 1 < nchunks) split_tb(ci + 1);
     }
     __syncthreads();   // the last chunk's output tile is complete
     norm_rows(nchunks - 1);
