@@ -264,6 +264,31 @@ __global__ void __launch_bounds__(kThreads) gdn_conv_ext_kernel(GdnArgs a) {
 #pragma unroll
   for (int e = 0; e < kConvCh; ++e)
     w[e] = *reinterpret_cast<const f32x4*>(a.conv_w + 4 * (int64_t)(c + e));
+  // Most row blocks lie inside one in-pool request, at least 3 rows past its
+  // first: then every input is a qkv row (workgroup-uniform test).
+  const int tl = min(tb + kConvTokens, a.rows) - 1;
+  const int ob = a.owner[tb];
+  if (ob >= 0 && a.owner[tl] == ob && tb - 3 >= min(max(a.tok[ob], 0), a.rows)) {
+#pragma unroll
+    for (int i = 0; i < kConvTokens; ++i) {
+      if (tb + i > tl) break;
+      float y[kConvCh];
+#pragma unroll
+      for (int e = 0; e < kConvCh; ++e) {
+        float in[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          const uint32_t pr = x[i + k][e >> 1];
+          in[k] = (e & 1) ? bf16_hi(pr) : bf16_lo(pr);
+        }
+        y[e] = round_bf(w[e][0] * in[0] + w[e][1] * in[1] + w[e][2] * in[2] + w[e][3] * in[3]);
+        y[e] = y[e] / (1.f + expf(-y[e]));
+      }
+      *reinterpret_cast<u32x2*>(a.ws + (int64_t)(tb + i) * a.conv_dim + c) =
+          u32x2{pack_bf16(y[0], y[1]), pack_bf16(y[2], y[3])};
+    }
+    return;
+  }
 #pragma unroll
   for (int i = 0; i < kConvTokens; ++i) {
     const int tt = tb + i;
