@@ -299,14 +299,19 @@ def bench_oproj(torch, args):
         out = torch.empty((m, n_out), dtype=torch.bfloat16, device="cuda")
         gemm = lambda _: fl.block_fp8_gemm(xq, sx, wq, ws, None, out=out)
         quant = lambda _: fl.quantize_activations(x)
-        for fn in (gemm, quant):
+        # the module's path: the attention output write leaves amax|x| (out_amax)
+        amax = (x.view(torch.int16).to(torch.int32) & 0x7fff).max().reshape(1)
+        quant_amax = lambda _: fl.quantize_activations(x, amax=amax)
+        for fn in (gemm, quant, quant_amax):
             time_kernel(torch, [None], max(2, args.warmup), fn)
         t_gemm = time_kernel(torch, [None], steps, gemm)
         t_quant = time_kernel(torch, [None], steps, quant)
+        t_quant_amax = time_kernel(torch, [None], steps, quant_amax)
         flops = 2.0 * m * n_out * k_in
         tf = flops / (t_gemm * 1e-3) / 1e12
         wbytes = n_out * k_in + ws.numel() * 4 + m * k_in + m * n_out * 2
-        res[f"m{m}"] = {"gemm_ms": t_gemm, "quant_ms": t_quant, "gemm_tflops": tf,
+        res[f"m{m}"] = {"gemm_ms": t_gemm, "quant_ms": t_quant,
+                        "quant_from_attention_amax_ms": t_quant_amax, "gemm_tflops": tf,
                         "gemm_frac_of_fp8_peak": tf / FP8_PEAK_TFLOPS,
                         "gemm_gbps": wbytes / (t_gemm * 1e-3) / 1e9}
         if m <= 512:
@@ -331,7 +336,8 @@ def bench_oproj(torch, args):
                 f"of HBM)")
         log(f"o_proj fp8 m={m}: gemm {t_gemm*1e3:.1f} us = {tf:.0f} TFLOP/s "
             f"({tf / FP8_PEAK_TFLOPS * 100:.1f}% of fp8 peak, {wbytes / t_gemm / 1e6:.0f} GB/s), "
-            f"activation quant {t_quant*1e3:.1f} us")
+            f"activation quant {t_quant*1e3:.1f} us ({t_quant_amax*1e3:.1f} us from the "
+            f"attention's amax)")
         del x, xq, out
     res["workload"] = ("block-FP8 o_proj: bf16 [m, 6144] -> dynamic e4m3 -> x e4m3 [5120, 6144] "
                        "with 128x128 fp32 block scales -> bf16 [m, 5120]; m = tokens of the "

@@ -98,6 +98,15 @@ const char* tf_attn_last_error(void);
  * output write; the gate of the reference is the second half of each head's
  * q projection, so a strided view of it is passed as is.
  *
+ * out_amax (optional, NULL = none): a device uint32 that each call raises to
+ * the largest bf16 bit pattern of |o| over the outputs it writes (sign bit
+ * cleared, so the integer order is the float order and NaN sorts above inf),
+ * with device-scope atomics: the per-tensor amax that the dynamic FP8
+ * quantisation of the following o_proj needs (fp8_triton.py:128), folded into
+ * the output write.  The caller sets it (normally to 0) before the step; calls
+ * that write parts of one output tensor (decode and extend of a mixed step,
+ * on one stream or two) may share it.  tf_fp8_act_quant_amax consumes it.
+ *
  * tf_attn_decode runs both phases.  tf_attn_decode_partial runs the
  * HBM-streaming split kernel only (requests that fit one split get their final
  * output, the others leave partials in the workspace); tf_attn_decode_merge then
@@ -122,7 +131,7 @@ int32_t tf_attn_decode(const void* q, int64_t q_row_stride,
                        void* workspace, int64_t workspace_bytes,
                        int32_t max_seq_len, int32_t num_workgroups,
                        const void* gate, int64_t gate_row_stride, int64_t gate_head_stride,
-                       tf_stream_t stream);
+                       uint32_t* out_amax, tf_stream_t stream);
 
 int32_t tf_attn_decode_partial(const void* q, int64_t q_row_stride,
                                const void* k_pool, const void* v_pool, int64_t pool_slots,
@@ -137,7 +146,7 @@ int32_t tf_attn_decode_partial(const void* q, int64_t q_row_stride,
                                void* workspace, int64_t workspace_bytes,
                                int32_t max_seq_len, int32_t num_workgroups,
                                const void* gate, int64_t gate_row_stride, int64_t gate_head_stride,
-                               tf_stream_t stream);
+                               uint32_t* out_amax, tf_stream_t stream);
 
 int32_t tf_attn_decode_merge(const void* q, int64_t q_row_stride,
                              const void* k_pool, const void* v_pool, int64_t pool_slots,
@@ -152,7 +161,7 @@ int32_t tf_attn_decode_merge(const void* q, int64_t q_row_stride,
                              void* workspace, int64_t workspace_bytes,
                              int32_t max_seq_len, int32_t num_workgroups,
                              const void* gate, int64_t gate_row_stride, int64_t gate_head_stride,
-                             tf_stream_t stream);
+                             uint32_t* out_amax, tf_stream_t stream);
 
 /* tf_attn_decode_noalloc: no counterpart in the reference.  For callers that
  * cannot allocate device memory (code under HIP graph capture, tight serving
@@ -179,7 +188,8 @@ int32_t tf_attn_decode_noalloc(const void* q, int64_t q_row_stride,
                                float scale, void* out, int64_t out_row_stride,
                                int32_t max_seq_len, int32_t num_workgroups,
                                const void* gate, int64_t gate_row_stride,
-                               int64_t gate_head_stride, tf_stream_t stream);
+                               int64_t gate_head_stride, uint32_t* out_amax,
+                               tf_stream_t stream);
 
 /* ------------------------------------------------------------------ extend
  * Causal prefill / extend attention over cached prefix + new tokens, bf16
@@ -189,7 +199,7 @@ int32_t tf_attn_decode_noalloc(const void* q, int64_t q_row_stride,
  *
  * work: device int32 [n_work][8] from tf_attn_plan_extend(); one entry per
  * (request, kv head, tile of 256 (token, q-head) rows).
- * gate: optional output gate, as for tf_attn_decode.
+ * gate, out_amax: optional output gate and output amax, as for tf_attn_decode.
  */
 int32_t tf_attn_extend(const void* q, int64_t q_row_stride,
                        const void* k_pool, const void* v_pool, int64_t pool_slots,
@@ -202,7 +212,7 @@ int32_t tf_attn_extend(const void* q, int64_t q_row_stride,
                        int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
                        float scale, void* out, int64_t out_row_stride,
                        const void* gate, int64_t gate_row_stride, int64_t gate_head_stride,
-                       tf_stream_t stream);
+                       uint32_t* out_amax, tf_stream_t stream);
 
 /* ------------------------------------------------------------------ planning
  * Host-side work planning (all pointers are HOST pointers; no GPU needed).
@@ -383,6 +393,18 @@ int32_t tf_fp8_act_quant(const void* x, int32_t x_dtype, int64_t rows, int64_t c
                          int64_t x_row_stride, void* xq, int64_t xq_row_stride,
                          float* x_scale, void* workspace, int64_t workspace_bytes,
                          tf_stream_t stream);
+
+/* tf_fp8_act_quant_amax: tf_fp8_act_quant with max|x| already known, as the
+ * attention entry points accumulate it in their out_amax argument over the
+ * output they write (the bf16 bit pattern of |x|, sign cleared): the same
+ * x_scale and xq bit for bit, one launch (the quantisation pass) instead of
+ * two, no workspace.  amax_bits: device uint32, 4-byte aligned.  Replaces
+ * the same lines of fp8_triton.py (127-130) for a caller whose producer
+ * computed the amax (the gated attention output in front of o_proj).
+ */
+int32_t tf_fp8_act_quant_amax(const void* x, int32_t x_dtype, int64_t rows, int64_t cols,
+                              int64_t x_row_stride, void* xq, int64_t xq_row_stride,
+                              float* x_scale, const uint32_t* amax_bits, tf_stream_t stream);
 
 int32_t tf_fp8_block_gemm(const void* xq, int64_t xq_row_stride, const float* x_scale,
                           const void* w, int64_t w_row_stride, const float* w_scale,

@@ -77,17 +77,17 @@ def test_entry_points_reject_bad_arguments_before_launching():
     lib = _native.load()
     rc = lib.tf_attn_decode(None, 0, None, None, 16, 0, None, None, None, 1, 16, 16,
                             None, None, 0, None, None, 1, 16, 2, 256, 0.0625, None, 0,
-                            None, 0, 16, 0, None, 0, 0, None)
+                            None, 0, 16, 0, None, 0, 0, None, None)
     assert rc == _native.TF_ERR_INVALID
     assert b"null" in lib.tf_attn_last_error()
     rc = lib.tf_attn_extend(None, 0, None, None, 16, 5, None, None, None, 1, 16, 16,
                             None, None, 0, None, 3, 16, 2, 256, 0.0625, None, 0,
-                            None, 0, 0, None)
+                            None, 0, 0, None, None)
     assert rc == _native.TF_ERR_UNSUPPORTED
     # A misaligned output gate is rejected before anything is launched.
     rc = lib.tf_attn_extend(16, 6144, 16, 16, 16, 0, None, None, 16, 1, 16, 16,
                             16, 16, 0, 16, 3, 24, 4, 256, 0.0625, 16, 6144,
-                            8, 12288, 512, None)
+                            8, 12288, 512, None, None)
     assert rc == _native.TF_ERR_INVALID and b"gate" in lib.tf_attn_last_error()
     rc = lib.tf_kv_write(None, None, 0, 0, None, 4, None, None, 16, 0, None, None, 2, 256,
                          None)

@@ -105,6 +105,11 @@ def test_full_attention_fp8_projections(gpu, monkeypatch):
         ref, _, _ = ofl.block_fp8_linear(x.cpu(), lin.weight.cpu(), lin.weight_scale_inv.cpu())
         rms = float(ref.pow(2).mean().sqrt())
         assert torch.allclose(got.cpu().float(), ref, atol=2e-2 * rms, rtol=1e-2), name
+    # forward hands o_proj the amax the attention write accumulated
+    # (out_amax); the two-pass quantisation that measures it gives the same bits
+    with torch.no_grad():
+        assert torch.equal(out, mod.o_proj(x_o)), "o_proj with the attention's amax differs"
+
 
 
 @pytest.mark.parametrize("name", mg.CASES)

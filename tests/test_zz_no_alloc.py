@@ -26,7 +26,7 @@ def noalloc(call, out, num_workgroups=0):
                         *call._pool_args, _ptr(call._items), _ptr(call._rows), call.n_dec,
                         call.n_q, call.n_kv, call.head_dim, call.scaling,
                         out.data_ptr(), out.stride(0), call.max_len, num_workgroups,
-                        *call._gate_args, call.stream.cuda_stream)
+                        *call._epilogue_args, call.stream.cuda_stream)
 
 
 def check_pair(wl, what, gate=None, workgroups=0):

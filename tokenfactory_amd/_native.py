@@ -12,7 +12,7 @@ from pathlib import Path
 from typing import Optional
 
 LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libtf_attn.so"
-ABI_VERSION = 11
+ABI_VERSION = 12
 
 TF_DTYPE_BF16 = 0
 TF_DTYPE_FP8_E4M3 = 1
@@ -45,7 +45,7 @@ SIGNATURES = {
         _p, _i64,                      # out, out_row_stride
         _p, _i64, _i32, _i32,          # workspace, workspace_bytes, max_seq_len, num_workgroups
         _p, _i64, _i64,                # gate, gate_row_stride, gate_head_stride
-        _p,                            # stream
+        _p, _p,                        # out_amax, stream
     ]),
     "tf_attn_decode_noalloc": (_i32, [
         _p, _i64,                      # q, q_row_stride
@@ -57,7 +57,7 @@ SIGNATURES = {
         _p, _i64,                      # out, out_row_stride
         _i32, _i32,                    # max_seq_len, num_workgroups
         _p, _i64, _i64,                # gate, gate_row_stride, gate_head_stride
-        _p,                            # stream
+        _p, _p,                        # out_amax, stream
     ]),
     "tf_attn_decode_partial": None,   # same signature as tf_attn_decode
     "tf_attn_decode_merge": None,
@@ -70,7 +70,7 @@ SIGNATURES = {
         _i32, _i32, _i32, _f32,
         _p, _i64,
         _p, _i64, _i64,                # gate, gate_row_stride, gate_head_stride
-        _p,
+        _p, _p,                        # out_amax, stream
     ]),
     "tf_attn_plan_extend": (_i32, [_p, _i32, _i32, _i32, _i32, _p, _i32]),
     "tf_attn_plan_device_capacity": (_i64, [_i64, _i32, _i32, _i32]),
@@ -110,6 +110,11 @@ SIGNATURES = {
         _p, _i32, _i64, _i64, _i64,    # x, x_dtype, rows, cols, x_row_stride
         _p, _i64, _p,                  # xq, xq_row_stride, x_scale
         _p, _i64, _p,                  # workspace, workspace_bytes, stream
+    ]),
+    "tf_fp8_act_quant_amax": (_i32, [
+        _p, _i32, _i64, _i64, _i64,    # x, x_dtype, rows, cols, x_row_stride
+        _p, _i64, _p,                  # xq, xq_row_stride, x_scale
+        _p, _p,                        # amax_bits, stream
     ]),
     "tf_fp8_block_gemm": (_i32, [
         _p, _i64, _p,                  # xq, xq_row_stride, x_scale

@@ -201,12 +201,19 @@ class SlotAttentionCall:
     are identical). Meant for a call that is built once and run many times:
     with a new call per step the ROCm runtime stalls the host periodically on
     the cross-stream waits, so per-step calls keep one stream.
+
+    ``out_amax`` (optional 1-element int32 tensor on q's device): every launch
+    raises it to the largest bf16 bit pattern of ``|out|`` it writes (sign
+    cleared, so it orders like the floats and NaN sorts above inf), the amax
+    of the FP8 quantisation in front of ``o_proj``
+    (``quantize_activations(..., amax=out_amax)``); the caller zeroes it before
+    ``run()``.
     """
 
     def __init__(self, q, layer_k_buffer, layer_v_buffer, batch, *, scaling=None,
                  k_scale=None, v_scale=None, decode_workgroups: int = 0, out=None,
                  stream=None, gate=None, device_plan: bool = False,
-                 overlap_decode: Optional[bool] = None):
+                 overlap_decode: Optional[bool] = None, out_amax=None):
         _check_inputs(q, layer_k_buffer, layer_v_buffer, batch)
         n_tok, n_q, head_dim = q.shape
         n_slots, n_kv, _ = layer_k_buffer.shape
@@ -237,10 +244,16 @@ class SlotAttentionCall:
                 raise ValueError("gate must be a bf16 [T, Hq, D] view on q's device with "
                                  "contiguous dims, strides in multiples of 8 and a 16-byte "
                                  "aligned start")
-            self._gate_args = (gate.data_ptr(), gate.stride(0), gate.stride(1))
+            self._epilogue_args = (gate.data_ptr(), gate.stride(0), gate.stride(1))
         else:
-            self._gate_args = (None, 0, 0)
+            self._epilogue_args = (None, 0, 0)
         self.gate = gate
+        if out_amax is not None and (out_amax.dtype != torch.int32 or out_amax.numel() != 1
+                                     or out_amax.device != q.device):
+            raise ValueError("out_amax must be a 1-element int32 tensor on q's device")
+        self.out_amax = out_amax
+        # the launches' trailing arguments: gate, its strides, out_amax
+        self._epilogue_args = self._epilogue_args + (_ptr(out_amax),)
 
         bsz = batch.batch_size
         ext_lens = [int(e) for e in batch.extend_lens]
@@ -353,14 +366,14 @@ class SlotAttentionCall:
                      self.n_q, self.n_kv, self.head_dim, self.scaling,
                      self.out.data_ptr(), self.out.stride(0),
                      _ptr(ws), 0 if ws is None else ws.numel(), self.max_len,
-                     self.decode_workgroups, *self._gate_args, stream.cuda_stream)
+                     self.decode_workgroups, *self._epilogue_args, stream.cuda_stream)
 
     def run_extend(self) -> None:
         if self.n_work:
             _native.call("tf_attn_extend", self.q.data_ptr(), self.q.stride(0),
                          *self._pool_args, self._meta.data_ptr(), self.n_work,
                          self.n_q, self.n_kv, self.head_dim, self.scaling,
-                         self.out.data_ptr(), self.out.stride(0), *self._gate_args,
+                         self.out.data_ptr(), self.out.stride(0), *self._epilogue_args,
                          self.stream.cuda_stream)
 
     def run_decode_partial(self) -> None:
@@ -401,6 +414,7 @@ def slot_based_attention(
     decode_workgroups: int = 0,
     out: Optional[torch.Tensor] = None,
     gate: Optional[torch.Tensor] = None,
+    out_amax: Optional[torch.Tensor] = None,
 ) -> torch.Tensor:
     """Attention of ``q [T, Hq, D]`` over one layer's slot pool; returns ``[T, Hq, D]``.
 
@@ -410,11 +424,13 @@ def slot_based_attention(
     decode kernel's persistent grid (0 = one workgroup per compute unit).
     ``gate`` (bf16 ``[T, Hq, D]``, any view with contiguous dims): the result is
     ``attn * F.silu(gate)`` (``full_attention.py:157-159``), computed in the
-    kernels' output write with the same bf16 roundings.
+    kernels' output write with the same bf16 roundings. ``out_amax``: see
+    ``SlotAttentionCall``.
     """
     call = SlotAttentionCall(q, layer_k_buffer, layer_v_buffer, batch, scaling=scaling,
                              k_scale=k_scale, v_scale=v_scale,
-                             decode_workgroups=decode_workgroups, out=out, gate=gate)
+                             decode_workgroups=decode_workgroups, out=out, gate=gate,
+                             out_amax=out_amax)
     return call.run()
 
 

@@ -32,7 +32,7 @@ int launch_status(const char* what) {
 
 extern "C" {
 
-int32_t tf_attn_abi_version(void) { return 11; }
+int32_t tf_attn_abi_version(void) { return 12; }
 
 const char* tf_attn_last_error(void) { return tfa::g_err; }
 

@@ -190,14 +190,17 @@ __global__ void __launch_bounds__(kGenThreads) generic_attn_kernel(GenericAttnAr
   __bf16* orow = a.out + qrow * a.out_stride + (int64_t)h * D;
   const __bf16* grow = a.gate ? a.gate + qrow * a.gate_stride + (int64_t)h * a.gate_hstride
                               : nullptr;
+  uint32_t omax = 0;
 #pragma unroll
   for (int u = 0; u < 2; ++u) {
     const int d = u ? d1 : d0;
     if (d >= D) continue;
     uint32_t o = pack_bf16(acc[2 * u] * inv, acc[2 * u + 1] * inv);
     if (grow) o = gate_pair(o, *reinterpret_cast<const uint32_t*>(grow + d));
+    omax = max(omax, max(o & 0x7fffu, (o >> 16) & 0x7fffu));
     *reinterpret_cast<uint32_t*>(orow + d) = o;
   }
+  amax_commit(a.amax, omax);
 }
 
 }  // namespace

@@ -75,6 +75,7 @@ struct DecodeArgs {
   int64_t out_stride;
   const __bf16* gate;   // optional output gate (NULL: none)
   int64_t gate_stride, gate_hstride;
+  uint32_t* amax;       // optional: raised to max |out| (bf16 bits), amax_commit
   float* ws_ml;
   float* ws_o;
   int32_t n_blocks;   // P: workgroups of the streaming kernel
@@ -164,10 +165,12 @@ __device__ __forceinline__ void block_merge(StateSlot* slots, int w, int lane, W
   if (w == 0) take_state(&slots[0], lane, st);
 }
 
+// Returns the largest |value| written (bf16 bits) for amax_commit.
 template <bool FP8>
-__device__ __forceinline__ void write_output(const DecodeArgs& a, int qrow, int hq, int g,
-                                             const WaveState& st, float vscale) {
+__device__ __forceinline__ uint32_t write_output(const DecodeArgs& a, int qrow, int hq, int g,
+                                                 const WaveState& st, float vscale) {
   const float inv = vscale / st.l;
+  uint32_t m = 0;
   __bf16* o = a.out + (int64_t)qrow * a.out_stride + (int64_t)hq * kD;
   const __bf16* gt =
       a.gate ? a.gate + (int64_t)qrow * a.gate_stride + (int64_t)hq * a.gate_hstride : nullptr;
@@ -178,6 +181,7 @@ __device__ __forceinline__ void write_output(const DecodeArgs& a, int qrow, int 
 #pragma unroll
       for (int k = 0; k < 4; ++k) v[k] = gate_pair(v[k], gv[k]);
     }
+    m = max(m, abs_max8(v));
     *reinterpret_cast<u32x4*>(o + off) = v;
   };
   if (FP8) {
@@ -205,6 +209,7 @@ __device__ __forceinline__ void write_output(const DecodeArgs& a, int qrow, int 
       }
     }
   }
+  return m;
 }
 
 // Issue the loads of tile `it` (chunk tokens it*16 .. it*16+15, clamped to the
@@ -513,7 +518,8 @@ decode_kernel(DecodeArgs a) {
 
     if (w == 0) {
       if (t0 == 0 && t1 == Ti) {
-        if (head_ok) write_output<FP8>(a, qrow, hq, g, st, vscale);
+        const uint32_t m = head_ok ? write_output<FP8>(a, qrow, hq, g, st, vscale) : 0u;
+        amax_commit(a.amax, m);
       } else if (n < min(a.group, 16)) {
         // Partial of unit u = item * units_per_item + j from this workgroup.
         const int64_t part = (int64_t)blockIdx.x + (int64_t)item * units_per_item + j;
@@ -582,10 +588,14 @@ decode_merge_kernel(DecodeArgs a) {
   if (Ti == 0) {
     // An empty context (seq_len 0) is a NaN row, as the reference's softmax
     // over no keys; padding entries write nothing.
-    if (w == 0 && head_ok && !item_is_padding(a, item)) {
-      st.m = 0.f;
-      st.l = __builtin_nanf("");
-      write_output<FP8>(a, qrow, hq, g, st, 1.f);
+    if (w == 0) {
+      uint32_t m = 0;
+      if (head_ok && !item_is_padding(a, item)) {
+        st.m = 0.f;
+        st.l = __builtin_nanf("");
+        m = write_output<FP8>(a, qrow, hq, g, st, 1.f);
+      }
+      amax_commit(a.amax, m);
     }
     return;
   }
@@ -607,7 +617,10 @@ decode_merge_kernel(DecodeArgs a) {
     }
   }
   block_merge(slots, w, lane, st);
-  if (w == 0 && head_ok) write_output<FP8>(a, qrow, hq, g, st, vscale);
+  if (w == 0) {
+    const uint32_t m = head_ok ? write_output<FP8>(a, qrow, hq, g, st, vscale) : 0u;
+    amax_commit(a.amax, m);
+  }
 }
 
 }  // namespace
@@ -680,8 +693,8 @@ int decode_launch(const void* q, int64_t q_row_stride, const void* k_pool, const
                   int32_t num_kv_heads, int32_t head_dim, float scale, void* out,
                   int64_t out_row_stride, void* workspace, int64_t workspace_bytes,
                   int32_t max_seq_len, int32_t num_workgroups, const void* gate,
-                  int64_t gate_row_stride, int64_t gate_head_stride, tf_stream_t stream,
-                  int phases) {
+                  int64_t gate_row_stride, int64_t gate_head_stride, uint32_t* out_amax,
+                  tf_stream_t stream, int phases) {
   clear_error();
   DecodePlan p;
   int rc = make_decode_plan(n_items, num_q_heads, num_kv_heads, head_dim, max_seq_len,
@@ -744,6 +757,7 @@ int decode_launch(const void* q, int64_t q_row_stride, const void* k_pool, const
     g.gate = static_cast<const __bf16*>(gate);
     g.gate_stride = gate_row_stride;
     g.gate_hstride = gate_head_stride;
+    g.amax = out_amax;
     return launch_generic_attn(g, reinterpret_cast<hipStream_t>(stream));
   }
 
@@ -774,6 +788,7 @@ int decode_launch(const void* q, int64_t q_row_stride, const void* k_pool, const
   a.gate = static_cast<const __bf16*>(gate);
   a.gate_stride = gate_row_stride;
   a.gate_hstride = gate_head_stride;
+  a.amax = out_amax;
   char* ws = static_cast<char*>(workspace);
   a.ws_ml = reinterpret_cast<float*>(ws);
   a.ws_o = reinterpret_cast<float*>(ws + p.ml_bytes);
@@ -813,13 +828,13 @@ int decode_launch(const void* q, int64_t q_row_stride, const void* k_pool, const
       float scale, void *out, int64_t out_row_stride, void *workspace,                     \
       int64_t workspace_bytes, int32_t max_seq_len, int32_t num_workgroups,                \
       const void *gate, int64_t gate_row_stride, int64_t gate_head_stride,                 \
-      tf_stream_t stream
+      uint32_t *out_amax, tf_stream_t stream
 #define TF_DECODE_ARGS                                                                      \
   q, q_row_stride, k_pool, v_pool, pool_slots, kv_dtype, k_scale, v_scale, req_to_token,   \
       rtt_rows, rtt_row_stride, rtt_cols, req_pool_indices, seq_lens, seq_len_override,    \
       items, q_rows, n_items, num_q_heads, num_kv_heads, head_dim, scale, out,             \
       out_row_stride, workspace, workspace_bytes, max_seq_len, num_workgroups, gate,       \
-      gate_row_stride, gate_head_stride, stream
+      gate_row_stride, gate_head_stride, out_amax, stream
 
 extern "C" {
 
@@ -908,7 +923,7 @@ extern "C" int32_t tf_attn_decode_noalloc(
     const int32_t* items, const int32_t* q_rows, int32_t n_items, int32_t num_q_heads,
     int32_t num_kv_heads, int32_t head_dim, float scale, void* out, int64_t out_row_stride,
     int32_t max_seq_len, int32_t num_workgroups, const void* gate, int64_t gate_row_stride,
-    int64_t gate_head_stride, tf_stream_t stream) {
+    int64_t gate_head_stride, uint32_t* out_amax, tf_stream_t stream) {
   using namespace tfa;
   clear_error();
   DecodePlan p;

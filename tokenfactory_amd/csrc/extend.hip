@@ -679,6 +679,7 @@ __global__ void __launch_bounds__(kThreads) extend_mfma_kernel(ExtendArgs a) {
     }
   }
   const int rho0 = row0 + kRowsPerWave * w + ge;
+  uint32_t omax = 0;
 #pragma unroll
   for (int i = 0; i < 16; ++i) {
     const int r = 2 * i + ge;
@@ -692,10 +693,12 @@ __global__ void __launch_bounds__(kThreads) extend_mfma_kernel(ExtendArgs a) {
 #pragma unroll
         for (int k = 0; k < 4; ++k) v[k] = gate_pair(v[k], gv[k]);
       }
+      omax = max(omax, abs_max8(v));
       *reinterpret_cast<u32x4*>(a.out + (int64_t)(q_start + t) * a.out_stride +
                                 (int64_t)(hk * G + h) * kD + 8 * ne) = v;
     }
   }
+  amax_commit(a.amax, omax);
 }
 
 }  // namespace
@@ -712,7 +715,7 @@ extern "C" int32_t tf_attn_extend(const void* q, int64_t q_row_stride, const voi
                                   int32_t head_dim, float scale, void* out,
                                   int64_t out_row_stride, const void* gate,
                                   int64_t gate_row_stride, int64_t gate_head_stride,
-                                  tf_stream_t stream) {
+                                  uint32_t* out_amax, tf_stream_t stream) {
   using namespace tfa;
   clear_error();
   if (n_work < 0) return fail(TF_ERR_INVALID, "extend: n_work=%d", n_work);
@@ -771,6 +774,7 @@ extern "C" int32_t tf_attn_extend(const void* q, int64_t q_row_stride, const voi
   a.gate = static_cast<const __bf16*>(gate);
   a.gate_stride = gate_row_stride;
   a.gate_hstride = gate_head_stride;
+  a.amax = out_amax;
 
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   if (generic) {   // head_dim != 256: one wave per row of every work entry
@@ -801,6 +805,7 @@ extern "C" int32_t tf_attn_extend(const void* q, int64_t q_row_stride, const voi
     g.gate = a.gate;
     g.gate_stride = a.gate_stride;
     g.gate_hstride = a.gate_hstride;
+    g.amax = out_amax;
     return launch_generic_attn(g, s);
   }
   if (kv_dtype == TF_DTYPE_FP8_E4M3)

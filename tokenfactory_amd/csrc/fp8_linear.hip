@@ -52,7 +52,8 @@ struct QuantArgs {
   uint32_t rows, c8;      // rows, cols / 8
   uint8_t* xq;            // e4m3 [rows, cols], row stride qs bytes
   int64_t qs;
-  uint32_t* partial;      // per-workgroup max of |x| bits
+  const uint32_t* partial;   // maxima of |x| bits to reduce (npartial of them)
+  uint32_t npartial;
   uint32_t nblocks;
   float* scale_out;
 };
@@ -68,20 +69,11 @@ __device__ __forceinline__ uint32_t block_max(uint32_t v, uint32_t* red) {
   return v;
 }
 
-// |x| as bf16 bit patterns: for non-negative values the integer order is the
-// float order and every NaN pattern sorts above +inf.
-__device__ __forceinline__ uint32_t abs_max8(u32x4 v) {
-  uint32_t m = 0;
-#pragma unroll
-  for (int j = 0; j < 4; ++j) m = max(m, max(v[j] & 0x7fffu, (v[j] >> 16) & 0x7fffu));
-  return m;
-}
-
 // Grid-stride loops over 16-byte chunks, kUnroll chunks per trip with their
 // loads issued together, so a thread keeps kUnroll loads in flight.
 constexpr int kUnroll = 4;
 
-__global__ void __launch_bounds__(kThreads) act_amax_kernel(QuantArgs a) {
+__global__ void __launch_bounds__(kThreads) act_amax_kernel(QuantArgs a, uint32_t* partial) {
   __shared__ uint32_t red[kThreads / kWave];
   const uint32_t n = a.rows * a.c8;
   const uint32_t stride = gridDim.x * kThreads;
@@ -98,7 +90,7 @@ __global__ void __launch_bounds__(kThreads) act_amax_kernel(QuantArgs a) {
     for (int u = 0; u < kUnroll; ++u) m = max(m, abs_max8(v[u]));
   }
   m = block_max(m, red);
-  if (threadIdx.x == 0) a.partial[blockIdx.x] = m;
+  if (threadIdx.x == 0) partial[blockIdx.x] = m;
 }
 
 __device__ __forceinline__ float sat448(float x) {
@@ -108,7 +100,7 @@ __device__ __forceinline__ float sat448(float x) {
 __global__ void __launch_bounds__(kThreads) act_quant_kernel(QuantArgs a) {
   __shared__ uint32_t red[kThreads / kWave];
   uint32_t m = 0;
-  for (uint32_t i = threadIdx.x; i < a.nblocks; i += kThreads) m = max(m, a.partial[i]);
+  for (uint32_t i = threadIdx.x; i < a.npartial; i += kThreads) m = max(m, a.partial[i]);
   m = block_max(m, red);
   // amax.clamp(min=1e-12) and amax / 448 on bf16 tensors (fp8_triton.py:128-129):
   // both results are rounded to bf16.  NaN stays NaN.
@@ -460,6 +452,41 @@ void launch_gemm(const GemmArgs& a, hipStream_t stream) {
   }
 }
 
+// Validates the arguments both quantisation entry points share and fills a.
+int32_t quant_setup(const char* fn, const void* x, int32_t x_dtype, int64_t rows, int64_t cols,
+                    int64_t x_row_stride, void* xq, int64_t xq_row_stride, float* x_scale,
+                    QuantArgs* a) {
+  if (x_dtype != TF_DTYPE_BF16)
+    return fail(TF_ERR_UNSUPPORTED, "%s: x must be bf16 (dtype %d)", fn, x_dtype);
+  if (rows < 0 || cols <= 0 || cols % 8 || x_row_stride < cols || xq_row_stride < cols)
+    return fail(TF_ERR_INVALID, "%s: rows=%lld cols=%lld (a multiple of 8) strides %lld/%lld",
+                fn, (long long)rows, (long long)cols, (long long)x_row_stride,
+                (long long)xq_row_stride);
+  if (x_row_stride % 8 || xq_row_stride % 8)
+    return fail(TF_ERR_INVALID, "%s: row strides must be multiples of 8", fn);
+  if (rows * (cols / 8) > (int64_t)UINT32_MAX / 2 || rows * x_row_stride > INT64_MAX / 4)
+    return fail(TF_ERR_UNSUPPORTED, "%s: %lld x %lld is too large", fn, (long long)rows,
+                (long long)cols);
+  if ((rows > 0 && (!x || !xq)) || !x_scale)
+    return fail(TF_ERR_INVALID, "%s: null pointer", fn);
+  if (!aligned16(x) || !aligned8(xq))
+    return fail(TF_ERR_INVALID, "%s: x must be 16-byte and xq 8-byte aligned", fn);
+  a->x = static_cast<const uint16_t*>(x);
+  a->xs = x_row_stride;
+  a->rows = (uint32_t)rows;
+  a->c8 = (uint32_t)(cols / 8);
+  a->xq = static_cast<uint8_t*>(xq);
+  a->qs = xq_row_stride;
+  a->scale_out = x_scale;
+  // ~2 chunks (32 B of x) per thread, at most kQuantMaxBlocks workgroups:
+  // small inputs spread over many CUs (one round of loads each), large ones
+  // loop with kUnroll loads in flight per thread
+  const int64_t chunks = rows * (cols / 8);
+  const int64_t want = (chunks + 2 * kThreads - 1) / (2 * kThreads);
+  a->nblocks = (uint32_t)std::max<int64_t>(1, std::min<int64_t>(want, kQuantMaxBlocks));
+  return TF_OK;
+}
+
 }  // namespace
 }  // namespace tfa
 
@@ -471,43 +498,41 @@ int32_t tf_fp8_act_quant(const void* x, int32_t x_dtype, int64_t rows, int64_t c
                          tf_stream_t stream) {
   using namespace tfa;
   clear_error();
-  if (x_dtype != TF_DTYPE_BF16)
-    return fail(TF_ERR_UNSUPPORTED, "fp8_act_quant: x must be bf16 (dtype %d)", x_dtype);
-  if (rows < 0 || cols <= 0 || cols % 8 || x_row_stride < cols || xq_row_stride < cols)
-    return fail(TF_ERR_INVALID, "fp8_act_quant: rows=%lld cols=%lld (a multiple of 8) strides %lld/%lld",
-                (long long)rows, (long long)cols, (long long)x_row_stride,
-                (long long)xq_row_stride);
-  if (x_row_stride % 8 || xq_row_stride % 8)
-    return fail(TF_ERR_INVALID, "fp8_act_quant: row strides must be multiples of 8");
-  if (rows * (cols / 8) > (int64_t)UINT32_MAX / 2 || rows * x_row_stride > INT64_MAX / 4)
-    return fail(TF_ERR_UNSUPPORTED, "fp8_act_quant: %lld x %lld is too large", (long long)rows,
-                (long long)cols);
-  if ((rows > 0 && (!x || !xq)) || !x_scale || !workspace)
-    return fail(TF_ERR_INVALID, "fp8_act_quant: null pointer");
-  if (!aligned16(x) || !aligned8(xq) || (reinterpret_cast<uintptr_t>(workspace) & 3u))
-    return fail(TF_ERR_INVALID, "fp8_act_quant: x must be 16-byte and xq 8-byte aligned");
+  QuantArgs a;
+  const int32_t rc = quant_setup("fp8_act_quant", x, x_dtype, rows, cols, x_row_stride, xq,
+                                 xq_row_stride, x_scale, &a);
+  if (rc != TF_OK) return rc;
+  if (!workspace || (reinterpret_cast<uintptr_t>(workspace) & 3u))
+    return fail(TF_ERR_INVALID, "fp8_act_quant: workspace must be 4-byte aligned");
   if (workspace_bytes < TF_FP8_QUANT_WORKSPACE_BYTES)
     return fail(TF_ERR_INVALID, "fp8_act_quant: workspace of %lld bytes (needs %d)",
                 (long long)workspace_bytes, TF_FP8_QUANT_WORKSPACE_BYTES);
-  QuantArgs a;
-  a.x = static_cast<const uint16_t*>(x);
-  a.xs = x_row_stride;
-  a.rows = (uint32_t)rows;
-  a.c8 = (uint32_t)(cols / 8);
-  a.xq = static_cast<uint8_t*>(xq);
-  a.qs = xq_row_stride;
-  a.partial = static_cast<uint32_t*>(workspace);
-  a.scale_out = x_scale;
-  const int64_t chunks = rows * (cols / 8);
-  // ~2 chunks (32 B of x) per thread, at most kQuantMaxBlocks workgroups:
-  // small inputs spread over many CUs (one round of loads each), large ones
-  // loop with kUnroll loads in flight per thread
-  const int64_t want = (chunks + 2 * kThreads - 1) / (2 * kThreads);
-  a.nblocks = (uint32_t)std::max<int64_t>(1, std::min<int64_t>(want, kQuantMaxBlocks));
+  uint32_t* partial = static_cast<uint32_t*>(workspace);
+  a.partial = partial;
+  a.npartial = a.nblocks;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-  hipLaunchKernelGGL(act_amax_kernel, dim3(a.nblocks), dim3(kThreads), 0, s, a);
+  hipLaunchKernelGGL(act_amax_kernel, dim3(a.nblocks), dim3(kThreads), 0, s, a, partial);
   hipLaunchKernelGGL(act_quant_kernel, dim3(a.nblocks), dim3(kThreads), 0, s, a);
   return launch_status("tf_fp8_act_quant launch");
+}
+
+int32_t tf_fp8_act_quant_amax(const void* x, int32_t x_dtype, int64_t rows, int64_t cols,
+                              int64_t x_row_stride, void* xq, int64_t xq_row_stride,
+                              float* x_scale, const uint32_t* amax_bits, tf_stream_t stream) {
+  using namespace tfa;
+  clear_error();
+  QuantArgs a;
+  const int32_t rc = quant_setup("fp8_act_quant_amax", x, x_dtype, rows, cols, x_row_stride,
+                                 xq, xq_row_stride, x_scale, &a);
+  if (rc != TF_OK) return rc;
+  if (!amax_bits || (reinterpret_cast<uintptr_t>(amax_bits) & 3u))
+    return fail(TF_ERR_INVALID, "fp8_act_quant_amax: amax_bits must be a 4-byte aligned "
+                "device pointer");
+  a.partial = amax_bits;
+  a.npartial = 1;
+  hipLaunchKernelGGL(act_quant_kernel, dim3(a.nblocks), dim3(kThreads), 0,
+                     reinterpret_cast<hipStream_t>(stream), a);
+  return launch_status("tf_fp8_act_quant_amax launch");
 }
 
 int32_t tf_fp8_block_gemm(const void* xq, int64_t xq_row_stride, const float* x_scale,

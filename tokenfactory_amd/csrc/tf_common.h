@@ -115,6 +115,28 @@ __device__ __forceinline__ uint32_t gate_pair(uint32_t o, uint32_t gp) {
                    bf16_hi(o) * silu_to_bf16(bf16_hi(gp)));
 }
 
+// |x| of eight bf16 values as bit patterns: for non-negative values the
+// integer order is the float order and every NaN pattern sorts above +inf.
+__device__ __forceinline__ uint32_t abs_max8(u32x4 v) {
+  uint32_t m = 0;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) m = max(m, max(v[j] & 0x7fffu, (v[j] >> 16) & 0x7fffu));
+  return m;
+}
+
+// Raises *amax to the largest m of the wave's lanes (bf16 bit patterns of |o|
+// from abs_max8): one wave-wide reduction and at most one no-return atomic per
+// wave, the per-tensor amax of the dynamic FP8 quantisation that follows the
+// attention output (fp8_triton.py:128).  Every lane of the wave calls it;
+// amax NULL: nothing to do.
+__device__ __forceinline__ void amax_commit(uint32_t* amax, uint32_t m) {
+  if (!amax) return;
+#pragma unroll
+  for (int d = 32; d >= 1; d >>= 1) m = max(m, (uint32_t)__shfl_xor((int)m, d, kWave));
+  if ((threadIdx.x & (kWave - 1)) == 0 && m != 0)
+    __hip_atomic_fetch_max(amax, m, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 // Wave index within the workgroup as a scalar (wave-uniform) value, so loops
 // and branches keyed on it compile to scalar control flow.
 __device__ __forceinline__ int wave_id() {

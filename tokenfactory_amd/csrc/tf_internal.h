@@ -54,6 +54,7 @@ struct ExtendArgs {
   int64_t out_stride;
   const __bf16* gate;             // optional output gate (NULL: none)
   int64_t gate_stride, gate_hstride;
+  uint32_t* amax;                 // optional: raised to max |out| (bf16 bits)
 };
 
 // Slot attention for head dims other than 256 (attn_generic.hip): one wave per
@@ -83,6 +84,7 @@ struct GenericAttnArgs {
   int64_t out_stride;
   const __bf16* gate;
   int64_t gate_stride, gate_hstride;
+  uint32_t* amax;   // optional: raised to max |out| (bf16 bits)
 };
 // head_dim handled by the generic kernel: a multiple of 8 in [8, 256], not 256.
 bool generic_head_dim(int32_t head_dim);

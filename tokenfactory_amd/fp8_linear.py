@@ -61,11 +61,16 @@ def _pad_cols(t: torch.Tensor, cols: int) -> torch.Tensor:
     return out.view(t.dtype)
 
 
-def quantize_activations(x2d: torch.Tensor, stream=None, padded_cols: Optional[int] = None):
+def quantize_activations(x2d: torch.Tensor, stream=None, padded_cols: Optional[int] = None,
+                         amax: Optional[torch.Tensor] = None):
     """Dynamic per-tensor e4m3 quantisation of a bf16 ``[rows, cols]`` matrix
     (``fp8_triton.py:127-130``). Returns ``(xq, x_scale)``: float8_e4m3fn rows
     and a 1-element fp32 tensor holding ``bf16(max(amax|x|, 1e-12) / 448)``.
-    With ``padded_cols`` the rows of ``xq`` are zero-extended to that width."""
+    With ``padded_cols`` the rows of ``xq`` are zero-extended to that width.
+    ``amax``: the max of ``|x|`` already computed by x's producer (a 1-element
+    int32 device tensor holding the bf16 bit pattern, as the attention kernels'
+    ``out_amax`` leaves it); the result is the same, with one launch
+    (``tf_fp8_act_quant_amax``) instead of two."""
     if x2d.dtype != torch.bfloat16 or x2d.dim() != 2 or not x2d.is_cuda:
         raise ValueError("quantize_activations: x must be a 2-D bf16 CUDA tensor")
     if x2d.stride(1) != 1:
@@ -79,6 +84,14 @@ def quantize_activations(x2d: torch.Tensor, stream=None, padded_cols: Optional[i
         if width > cols:
             xq.view(torch.uint8)[:, cols:].zero_()
         scale = torch.empty((1,), dtype=torch.float32, device=x2d.device)
+        if amax is not None:
+            if amax.dtype != torch.int32 or amax.numel() != 1 or amax.device != x2d.device:
+                raise ValueError("quantize_activations: amax must be a 1-element int32 tensor "
+                                 "on x's device")
+            _native.call("tf_fp8_act_quant_amax", _ptr(x2d), _native.TF_DTYPE_BF16, rows, cols,
+                         x2d.stride(0), _ptr(xq), xq.stride(0), _ptr(scale), _ptr(amax),
+                         _stream_ptr(stream, x2d.device))
+            return xq, scale
         ws = torch.empty((_native.TF_FP8_QUANT_WORKSPACE_BYTES,), dtype=torch.uint8,
                          device=x2d.device)
         _native.call("tf_fp8_act_quant", _ptr(x2d), _native.TF_DTYPE_BF16, rows, cols,
@@ -147,16 +160,19 @@ def block_fp8_gemm(xq: torch.Tensor, x_scale: torch.Tensor, weight: torch.Tensor
 
 def block_fp8_linear(x: torch.Tensor, weight: torch.Tensor,
                      weight_scale_inv: Optional[torch.Tensor], bias: Optional[torch.Tensor],
-                     block_h: int = 128, block_w: int = 128, stream=None) -> torch.Tensor:
+                     block_h: int = 128, block_w: int = 128, stream=None,
+                     x_amax: Optional[torch.Tensor] = None) -> torch.Tensor:
     """Native ``triton_block_fp8_linear`` (``fp8_triton.py:107-183``): x ``[..., in]``
-    bf16, weight float8_e4m3fn ``[out, in]`` -> bf16 ``[..., out]``."""
+    bf16, weight float8_e4m3fn ``[out, in]`` -> bf16 ``[..., out]``. ``x_amax``:
+    max ``|x|`` from x's producer, see ``quantize_activations``."""
     in_features = weight.shape[1]
     if x.shape[-1] != in_features:
         raise ValueError(f"block_fp8_linear: x [..., {x.shape[-1]}] vs weight in={in_features}")
     x2d = x.reshape(-1, in_features)
     if x2d.stride(1) != 1:
         x2d = x2d.contiguous()
-    xq, scale = quantize_activations(x2d, stream, padded_cols=_padded_k(in_features))
+    xq, scale = quantize_activations(x2d, stream, padded_cols=_padded_k(in_features),
+                                     amax=x_amax)
     out = block_fp8_gemm(xq, scale, weight, weight_scale_inv, bias, block_h, block_w,
                          stream=stream)
     return out.reshape(*x.shape[:-1], weight.shape[0])
@@ -213,9 +229,11 @@ class Fp8Linear(nn.Module):
         full = full[: self.out_features, : self.in_features]
         return (self.weight.to(torch.float32) * full).to(target_dtype)
 
-    def forward(self, x: torch.Tensor) -> torch.Tensor:
+    def forward(self, x: torch.Tensor, x_amax: Optional[torch.Tensor] = None) -> torch.Tensor:
+        """``x_amax``: optional max ``|x|`` from x's producer (see
+        ``quantize_activations``); the result does not change."""
         return block_fp8_linear(x, self.weight, self.weight_scale_inv, self.bias,
-                                self.block_h, self.block_w)
+                                self.block_h, self.block_w, x_amax=x_amax)
 
     def extra_repr(self) -> str:
         return (f"in_features={self.in_features}, out_features={self.out_features}, "

@@ -168,10 +168,16 @@ class FullAttention(nn.Module):
             k_buf, v_buf, forward_batch.out_cache_loc, *scales)
 
         # Attention with the output gate `attn * silu(gate)` (:150-159) fused
-        # into the kernels' output write.
+        # into the kernels' output write; in front of an FP8 o_proj the same
+        # write also takes the per-tensor amax of the activation quantisation
+        # (fp8_triton.py:128), which saves that pass a read of the output.
+        fp8_out = isinstance(self.o_proj, Fp8Linear)
+        amax = torch.zeros((1,), dtype=torch.int32, device=q.device) if fp8_out else None
         attn = slot_based_attention(q, k_buf, v_buf, forward_batch, scaling=self.scaling,
-                                    k_scale=scales[0], v_scale=scales[1], gate=gate)
-        return self.o_proj(attn.reshape(n_tok, self.num_heads * self.head_dim))
+                                    k_scale=scales[0], v_scale=scales[1], gate=gate,
+                                    out_amax=amax)
+        x = attn.reshape(n_tok, self.num_heads * self.head_dim)
+        return self.o_proj(x, x_amax=amax) if fp8_out else self.o_proj(x)
 
     def _slot_based_attention(self, q: torch.Tensor, layer_k_buffer: torch.Tensor,
                               layer_v_buffer: torch.Tensor, batch, k_scale=None,
