@@ -425,21 +425,25 @@ int64_t tf_fp8_block_gemm_workspace_bytes(int64_t m, int64_t n, int64_t k);
  * [0, n_slots) are skipped and their output rows left untouched):
  *   conv: y = bf16(silu(bf16(sum_i conv_weight[c][i] * [conv_state[r][c][0..2], qkv[b][c]][i])))
  *         conv_state[r][c] <- [conv_state[r][c][1..2], qkv[b][c]]
- *   q, k, v = split(y, [Hk*128, Hk*128, Hv*128]); q = normalize(q) / sqrt(128);
+ *   q, k, v = split(y, [Hk*Dk, Hk*Dk, Hv*Dv]); q = normalize(q) / sqrt(Dk);
  *   k = normalize(k); value head h uses key head h / (Hv / Hk);
  *   alpha = exp(-exp(a_log[h]) * softplus(a[b][h] + dt_bias[h])), beta = sigmoid(b[b][h]);
  *   S = alpha * ssm_state[r][h]; S += k (beta (v - S^T k))^T; ssm_state[r][h] = S;
  *   o = bf16(S^T q);  out[b] = bf16(norm_weight * o / rms_head(o) * silu(z[b])).
- * qkv: bf16 [B, 2*Hk*128 + Hv*128]; a, b: bf16 [B, Hv] (common row stride);
- * z: bf16 [B, Hv*128]; conv_weight: fp32 [conv_dim, 4] (16-byte aligned);
- * a_log, dt_bias: fp32 [Hv]; norm_weight: fp32 [Hv*128];
- * conv_state: bf16 [slots, conv_dim, 3]; ssm_state: fp32 [slots, Hv, 128, 128]
+ * qkv: bf16 [B, 2*Hk*Dk + Hv*Dv]; a, b: bf16 [B, Hv] (common row stride);
+ * z: bf16 [B, Hv*Dv]; conv_weight: fp32 [conv_dim, 4] (16-byte aligned);
+ * a_log, dt_bias: fp32 [Hv]; norm_weight: fp32 [Hv*Dv] (rms over Dv);
+ * conv_state: bf16 [slots, conv_dim, 3]; ssm_state: fp32 [slots, Hv, Dk, Dv]
  * (16-byte aligned), both updated in place, slot strides in elements;
- * out (and the optional core_out, the pre-norm o): bf16 [B, Hv*128].
+ * out (and the optional core_out, the pre-norm o): bf16 [B, Hv*Dv].
  * workspace: device scratch of tf_gdn_decode_workspace_bytes(B, Hk, Hv) bytes
- * (the bf16 conv outputs between the two launches; no initialisation needed).
- * head_k_dim = head_v_dim = 128, conv_kernel = 4.  Requests of one call must
- * use distinct slots.
+ * (the bf16 conv outputs between the two launches; no initialisation needed;
+ * sized for Dk = Dv = 128, enough for every supported head dim).
+ * Dk = head_k_dim, Dv = head_v_dim: 128 / 128 (the Qwen3.5 layers, on the
+ * MFMA-tiled kernels), or each a multiple of 4 up to 64 (the small test
+ * models, e.g. 16 / 16, on one wave per (request, value head) with the state
+ * in registers, the whole call's tokens in that wave); conv_kernel = 4.
+ * Requests of one call must use distinct slots.
  */
 int64_t tf_gdn_decode_workspace_bytes(int32_t batch_size, int32_t num_k_heads,
                                       int32_t num_v_heads);
@@ -483,7 +487,9 @@ int32_t tf_gdn_decode(const void* qkv, int64_t qkv_row_stride, const void* a, co
  * with row strides that are multiples of 4; norm_weight 16-byte aligned.  Other arguments
  * as for tf_gdn_decode, with rows = tokens; workspace:
  * tf_gdn_extend_workspace_bytes(n_tokens, batch_size, Hk, Hv) bytes, 16-byte
- * aligned.
+ * aligned.  At head dims other than 128 / 128 the call is five launches: the
+ * request of every row, the conv, the conv-state shift, every request's
+ * tokens in order in one wave per (request, value head), and the zero rows.
  */
 int64_t tf_gdn_extend_workspace_bytes(int64_t n_tokens, int32_t batch_size,
                                       int32_t num_k_heads, int32_t num_v_heads);

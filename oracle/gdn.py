@@ -65,8 +65,9 @@ def causal_conv_prefill(qkv: torch.Tensor, state: torch.Tensor, weight: torch.Te
 
 
 def normalize_qk(q: torch.Tensor, k: torch.Tensor):
-    """``F.normalize(q.float()) * dk^-0.5`` and ``F.normalize(k.float())`` (``:171-172``)."""
-    qn = F.normalize(q.float(), p=2.0, dim=-1) * (DK ** -0.5)
+    """``F.normalize(q.float()) * dk^-0.5`` and ``F.normalize(k.float())``
+    (``:171-172``), dk = ``q.shape[-1]`` (the layer's ``head_k_dim``)."""
+    qn = F.normalize(q.float(), p=2.0, dim=-1) * (q.shape[-1] ** -0.5)
     kn = F.normalize(k.float(), p=2.0, dim=-1)
     return qn, kn
 
@@ -138,15 +139,17 @@ def gdn_decode(qkv, a, b, z, conv_weight, a_log, dt_bias, norm_weight, eps, conv
                ssm_state, req_indices, num_k_heads, num_v_heads):
     """The decode step of ``tf_gdn_decode``: ``_batched_decode_step`` (``:244-298``)
     then the gated norm (``:325``). ``conv_state`` [slots, C, 3] bf16 and
-    ``ssm_state`` [slots, Hv, Dk, Dv] fp32 are updated in place (CPU tensors).
+    ``ssm_state`` [slots, Hv, Dk, Dv] fp32 are updated in place (CPU tensors); Dk
+    and Dv are its last two extents.
     Returns ``(out, core)``: the normed bf16 output and the bf16 pre-norm output."""
     req = req_indices.cpu().long()
-    key_dim = num_k_heads * DK
+    dk, dv = ssm_state.shape[-2], ssm_state.shape[-1]
+    key_dim = num_k_heads * dk
     conv_out, new_state = causal_conv_decode(qkv.cpu(), conv_state[req], conv_weight.cpu())
     conv_state[req] = new_state
     bsz = qkv.shape[0]
-    q, k, v = conv_out.split([key_dim, key_dim, num_v_heads * DV], dim=-1)
-    qn, kn = normalize_qk(q.view(bsz, num_k_heads, DK), k.view(bsz, num_k_heads, DK))
+    q, k, v = conv_out.split([key_dim, key_dim, num_v_heads * dv], dim=-1)
+    qn, kn = normalize_qk(q.view(bsz, num_k_heads, dk), k.view(bsz, num_k_heads, dk))
     vpk = num_v_heads // num_k_heads
     q_exp = torch.repeat_interleave(qn, vpk, dim=1)
     k_exp = torch.repeat_interleave(kn, vpk, dim=1)
@@ -154,12 +157,12 @@ def gdn_decode(qkv, a, b, z, conv_weight, a_log, dt_bias, norm_weight, eps, conv
     alpha = torch.exp(decay)
     outs = []
     for i in range(bsz):
-        o, s = delta_rule_decode(q_exp[i], k_exp[i], v[i].view(num_v_heads, DV), alpha[i],
+        o, s = delta_rule_decode(q_exp[i], k_exp[i], v[i].view(num_v_heads, dv), alpha[i],
                                  beta[i], ssm_state[req[i]])
         ssm_state[req[i]] = s
         outs.append(o)
-    core = torch.stack(outs).reshape(bsz, num_v_heads * DV).to(torch.bfloat16)
-    out = rms_norm_gated(core, z.cpu(), norm_weight.cpu(), eps)
+    core = torch.stack(outs).reshape(bsz, num_v_heads * dv).to(torch.bfloat16)
+    out = rms_norm_gated(core, z.cpu(), norm_weight.cpu(), eps, head_dim=dv)
     return out, core
 
 
@@ -169,8 +172,10 @@ def gdn_extend(qkv, a, b, z, conv_weight, a_log, dt_bias, norm_weight, eps, conv
     (``linear_attention.py:328-364``): ``_causal_conv1d_step`` and
     ``_gated_delta_rule_step`` (chunked WY for ``ext_len > 1``, the one-step
     formula for ``ext_len == 1``) per request, then the gated norm over all rows.
-    States are updated in place (CPU tensors). Returns ``(out, core)``."""
-    key_dim = num_k_heads * DK
+    States are updated in place (CPU tensors); head dims from ``ssm_state``'s
+    last two extents. Returns ``(out, core)``."""
+    dk, dv = ssm_state.shape[-2], ssm_state.shape[-1]
+    key_dim = num_k_heads * dk
     vpk = num_v_heads // num_k_heads
     outs, off = [], 0
     for i, e in enumerate(extend_lens):
@@ -180,10 +185,10 @@ def gdn_extend(qkv, a, b, z, conv_weight, a_log, dt_bias, norm_weight, eps, conv
         conv_out, new_state = causal_conv_prefill(qkv[rows].cpu(), conv_state[r],
                                                   conv_weight.cpu())
         conv_state[r] = new_state
-        q, k, v = conv_out.split([key_dim, key_dim, num_v_heads * DV], dim=-1)
-        q = q.view(e, num_k_heads, DK)
-        k = k.view(e, num_k_heads, DK)
-        v = v.view(e, num_v_heads, DV)
+        q, k, v = conv_out.split([key_dim, key_dim, num_v_heads * dv], dim=-1)
+        q = q.view(e, num_k_heads, dk)
+        k = k.view(e, num_k_heads, dk)
+        v = v.view(e, num_v_heads, dv)
         if e == 1:                           # :184-192
             qn, kn = normalize_qk(q[0], k[0])
             decay, beta = gates(a[rows].cpu()[0], b[rows].cpu()[0], a_log.cpu(), dt_bias.cpu())
@@ -195,7 +200,7 @@ def gdn_extend(qkv, a, b, z, conv_weight, a_log, dt_bias, norm_weight, eps, conv
         else:
             o = gated_delta_rule_chunked(q, k, v, b[rows].cpu(), a[rows].cpu(), ssm_state[r],
                                          a_log.cpu(), dt_bias.cpu(), vpk)
-        outs.append(o.reshape(e, num_v_heads * DV).to(torch.bfloat16))
+        outs.append(o.reshape(e, num_v_heads * dv).to(torch.bfloat16))
     core = torch.cat(outs, dim=0)
-    return rms_norm_gated(core, z.cpu(), norm_weight.cpu(), eps), core
+    return rms_norm_gated(core, z.cpu(), norm_weight.cpu(), eps, head_dim=dv), core
 

@@ -14,24 +14,28 @@ import torch.nn.functional as F
 from oracle import gdn as og
 
 
-def rand_inputs(t, hk, hv, seed):
+def rand_inputs(t, hk, hv, seed, dk=og.DK, dv=og.DV):
     g = torch.Generator().manual_seed(seed)
-    q = torch.randn((t, hk, og.DK), generator=g).to(torch.bfloat16)
-    k = torch.randn((t, hk, og.DK), generator=g).to(torch.bfloat16)
-    v = torch.randn((t, hv, og.DV), generator=g).to(torch.bfloat16)
+    q = torch.randn((t, hk, dk), generator=g).to(torch.bfloat16)
+    k = torch.randn((t, hk, dk), generator=g).to(torch.bfloat16)
+    v = torch.randn((t, hv, dv), generator=g).to(torch.bfloat16)
     a = torch.randn((t, hv), generator=g).to(torch.bfloat16)
     b = torch.randn((t, hv), generator=g).to(torch.bfloat16)
     a_log = torch.rand((hv,), generator=g) * 2 - 3          # decay rates ~ -exp(-2) * softplus
     dt_bias = torch.rand((hv,), generator=g)
-    state = torch.randn((hv, og.DK, og.DV), generator=g) * 0.1
+    state = torch.randn((hv, dk, dv), generator=g) * 0.1
     return q, k, v, a, b, a_log, dt_bias, state
 
 
-@pytest.mark.parametrize("t,chunk", [(5, 64), (64, 64), (70, 64), (70, 32), (33, 32)])
-def test_chunked_prefill_equals_recurrence(t, chunk):
+@pytest.mark.parametrize("t,chunk,dk,dv", [(5, 64, 128, 128), (64, 64, 128, 128),
+                                           (70, 64, 128, 128), (70, 32, 128, 128),
+                                           (33, 32, 128, 128),
+                                           # the reference's test models: head dims 16
+                                           (70, 64, 16, 16), (9, 64, 32, 16)])
+def test_chunked_prefill_equals_recurrence(t, chunk, dk, dv):
     # chunk 64: the reference's chunk length; chunk 32: the GPU kernel's
     hk, hv = 2, 6
-    q, k, v, a, b, a_log, dt_bias, s0 = rand_inputs(t, hk, hv, t)
+    q, k, v, a, b, a_log, dt_bias, s0 = rand_inputs(t, hk, hv, t, dk, dv)
     s_chunk = s0.clone()
     out_chunk = og.gated_delta_rule_chunked(q, k, v, b, a, s_chunk, a_log, dt_bias, hv // hk,
                                             chunk_size=chunk)
@@ -48,6 +52,20 @@ def test_chunked_prefill_equals_recurrence(t, chunk):
     scale = float(out_rec.abs().max())
     assert torch.allclose(out_chunk, out_rec, atol=1e-4 * scale, rtol=1e-4)
     assert torch.allclose(s_chunk, s, atol=1e-4 * float(s.abs().max()), rtol=1e-4)
+
+
+@pytest.mark.parametrize("dk", [16, 128])
+def test_normalize_qk_closed_form(dk):
+    # q is scaled by head_k_dim^-0.5 of the layer (16 in the reference's test models)
+    q = torch.zeros((3, dk))
+    q[0, 1] = 5.0
+    q[1, dk - 1] = -0.25
+    q[2] = 2.0                                   # equal entries: the unit vector dk^-0.5 * 1
+    qn, kn = og.normalize_qk(q, q.clone())
+    assert float(kn[0, 1]) == 1.0 and float(qn[0, 1]) == pytest.approx(dk ** -0.5, rel=1e-6)
+    assert float(qn[1, dk - 1]) == pytest.approx(-(dk ** -0.5), rel=1e-6)
+    assert torch.allclose(kn[2], torch.full((dk,), dk ** -0.5))
+    assert torch.allclose(qn[2], torch.full((dk,), 1.0 / dk))
 
 
 def test_delta_rule_closed_forms():

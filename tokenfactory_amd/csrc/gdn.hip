@@ -59,6 +59,8 @@ struct GdnArgs {
   int64_t n_slots;
   int32_t batch, hv, vpk, key_dim, conv_dim;
   int32_t hk;
+  int32_t dk, dv;        // head dims (128 / 128 on the tuned kernels)
+  float qscale;          // dk^-0.5 as fp32 (the other-dims kernel)
   uint16_t* wqk;         // extend: bf16 [rows, Hk, 4, 128] normalised q (hi, lo parts) then k
   float* wg;             // extend: fp32 [rows, Hv, 2] g = log alpha, beta
   int32_t* owner;        // extend: int32 [rows] request of each token row (-1: none / skipped)
@@ -922,6 +924,98 @@ __global__ void __launch_bounds__(kChunkThreads) gdn_chunk_ext_kernel(GdnArgs a)
   }
 }
 
+// ---------------------------------------------------------------- other head dims
+// Head dims other than 128 (the reference's own test models use 16): one wave
+// per (request, value head) carries the head's dk x dv state in registers,
+// lane j holding value column j (dk, dv <= 64), through the request's token
+// rows one at a time: the delta rule of linear_attention.py:278-298 (for a
+// prefill the reference's chunk-wise form, :194-242, which equals it up to
+// fp32 rounding), with q / k normalised (:171-172) and the gated norm
+// (rms_norm_gated.py:26-40) in the same wave.  Conv outputs come from
+// gdn_conv_kernel (decode: row = request) or gdn_conv_ext_kernel (extend).
+// Decode: a request whose slot is outside the pool gets zero rows here;
+// extend: gdn_zero_ext_kernel writes them.
+constexpr int kGenD = 64;
+constexpr int kGenWaves = kThreads / kWave;
+
+__device__ __forceinline__ float wave_sum_all(float v) {
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, kWave);
+  return v;
+}
+
+__global__ void __launch_bounds__(kThreads) gdn_generic_kernel(GdnArgs a) {
+  __shared__ float qk_all[kGenWaves][2][kGenD];   // this wave's normalised q, k
+  const int wv = threadIdx.x / kWave, lane = threadIdx.x & (kWave - 1);
+  const int64_t item = (int64_t)blockIdx.x * kGenWaves + wv;
+  if (item >= (int64_t)a.batch * a.hv) return;
+  const int bi = (int)(item / a.hv), h = (int)(item % a.hv);
+  const int hk = h / a.vpk;
+  const int dk = a.dk, dv = a.dv;
+  const bool col = lane < dv;
+  const int64_t r = a.req[bi];
+  if (r < 0 || r >= a.n_slots) {
+    if (!a.tok && col) {
+      a.out[(int64_t)bi * a.out_rs + h * dv + lane] = 0;
+      if (a.core) a.core[(int64_t)bi * a.core_rs + h * dv + lane] = 0;
+    }
+    return;
+  }
+  int t0 = bi, t1 = bi + 1;
+  if (a.tok) {
+    t0 = min(max(a.tok[bi], 0), a.rows);
+    t1 = max(min(max(a.tok[bi + 1], 0), a.rows), t0);
+  }
+  float (*qk)[kGenD] = qk_all[wv];
+  qk[0][lane] = 0.f;   // entries dk .. 63 stay zero: they add nothing below
+  qk[1][lane] = 0.f;
+  float* S = a.ssm + r * a.ssm_ss + (int64_t)h * dk * dv;
+  float s[kGenD];
+#pragma unroll
+  for (int k = 0; k < kGenD; ++k) s[k] = (col && k < dk) ? S[k * dv + lane] : 0.f;
+  for (int row = t0; row < t1; ++row) {
+    const uint16_t* y = a.ws + (int64_t)row * a.conv_dim;
+    const float qv = lane < dk ? bf(y[hk * dk + lane]) : 0.f;
+    const float kv = lane < dk ? bf(y[a.key_dim + hk * dk + lane]) : 0.f;
+    const float nq = sqrtf(wave_sum_all(qv * qv)), nk = sqrtf(wave_sum_all(kv * kv));
+    if (lane < dk) {   // F.normalize (eps 1e-12), q also times dk^-0.5
+      qk[0][lane] = qv / fmaxf(nq, 1e-12f) * a.qscale;
+      qk[1][lane] = kv / fmaxf(nk, 1e-12f);
+    }
+    // (one wave: its LDS writes land before its reads below)
+    const float x = bf(a.a[(int64_t)row * a.ab_rs + h]) + a.dt_bias[h];
+    const float sp = x > 20.f ? x : log1pf(expf(x));           // F.softplus
+    const float alpha = expf(-expf(a.a_log[h]) * sp);
+    const float beta = 1.f / (1.f + expf(-bf(a.b[(int64_t)row * a.ab_rs + h])));
+    const float v = col ? bf(y[2 * a.key_dim + h * dv + lane]) : 0.f;
+    float vp = 0.f;
+#pragma unroll
+    for (int k = 0; k < kGenD; ++k) {
+      s[k] *= alpha;
+      vp += s[k] * qk[1][k];
+    }
+    const float delta = beta * (v - vp);
+    float o = 0.f;
+#pragma unroll
+    for (int k = 0; k < kGenD; ++k) {
+      s[k] += qk[1][k] * delta;
+      o += s[k] * qk[0][k];
+    }
+    o = round_bf(o);                                            // .to(orig_dtype)
+    if (col && a.core) a.core[(int64_t)row * a.core_rs + h * dv + lane] = to_bf(o);
+    const float var = wave_sum_all(col ? o * o : 0.f) / (float)dv;
+    if (col) {
+      const float zz = bf(a.z[(int64_t)row * a.z_rs + h * dv + lane]);
+      const float xn = o * rsqrtf(var + a.eps);
+      a.out[(int64_t)row * a.out_rs + h * dv + lane] =
+          to_bf(a.norm_w[h * dv + lane] * xn * (zz / (1.f + expf(-zz))));
+    }
+  }
+#pragma unroll
+  for (int k = 0; k < kGenD; ++k)
+    if (col && k < dk) S[k * dv + lane] = s[k];
+}
+
 // Rows that no request owns, or whose request's slot is outside the pool,
 // read as zeros in out and core_out; gdn_recur_kernel and gdn_chunk_ext_kernel
 // write every other row.  One wave per row.
@@ -931,7 +1025,7 @@ __global__ void __launch_bounds__(kThreads) gdn_zero_ext_kernel(GdnArgs a) {
   const int64_t tok = (int64_t)blockIdx.x * kZeroRows + wave_id();
   if (tok >= a.rows || a.owner[tok] >= 0) return;
   const int lane = threadIdx.x & (kWave - 1);
-  for (int d = 4 * lane; d < a.hv * kDv; d += 4 * kWave) {
+  for (int d = 4 * lane; d < a.hv * a.dv; d += 4 * kWave) {
     *reinterpret_cast<u32x2*>(a.out + tok * a.out_rs + d) = u32x2{0u, 0u};
     if (a.core) *reinterpret_cast<u32x2*>(a.core + tok * a.core_rs + d) = u32x2{0u, 0u};
   }
@@ -982,17 +1076,21 @@ int32_t gdn_setup(const char* fn, const void* qkv, int64_t qkv_row_stride, const
                   void* core_out, int64_t core_row_stride, void* workspace,
                   int64_t workspace_bytes, tfa::GdnArgs* g) {
   using namespace tfa;
-  if (head_k_dim != kDk || head_v_dim != kDv || conv_kernel != 4)
+  const bool tuned = head_k_dim == kDk && head_v_dim == kDv;
+  const bool other = head_k_dim >= 4 && head_k_dim <= kGenD && head_k_dim % 4 == 0 &&
+                     head_v_dim >= 4 && head_v_dim <= kGenD && head_v_dim % 4 == 0;
+  if ((!tuned && !other) || conv_kernel != 4)
     return fail(TF_ERR_UNSUPPORTED,
-                "%s: head_k_dim=%d head_v_dim=%d conv_kernel=%d (128 / 128 / 4 only)", fn,
-                head_k_dim, head_v_dim, conv_kernel);
+                "%s: head_k_dim=%d head_v_dim=%d conv_kernel=%d (128 / 128, or multiples of 4 "
+                "up to %d; conv kernel 4)", fn, head_k_dim, head_v_dim, conv_kernel, kGenD);
   if (num_k_heads <= 0 || num_v_heads <= 0 || num_v_heads % num_k_heads)
     return fail(TF_ERR_INVALID, "%s: %d value heads over %d key heads", fn, num_v_heads,
                 num_k_heads);
   if (batch_size < 0 || n_slots <= 0 || rows < 0)
     return fail(TF_ERR_INVALID, "%s: batch_size=%d n_slots=%lld", fn, batch_size,
                 (long long)n_slots);
-  const int64_t key_dim = (int64_t)num_k_heads * kDk, value_dim = (int64_t)num_v_heads * kDv;
+  const int64_t key_dim = (int64_t)num_k_heads * head_k_dim;
+  const int64_t value_dim = (int64_t)num_v_heads * head_v_dim;
   const int64_t conv_dim = 2 * key_dim + value_dim;
   if (!qkv || !a || !b || !z || !conv_weight || !a_log || !dt_bias || !norm_weight ||
       !conv_state || !ssm_state || !req_indices || !out || !workspace)
@@ -1002,7 +1100,7 @@ int32_t gdn_setup(const char* fn, const void* qkv, int64_t qkv_row_stride, const
                 (long long)workspace_bytes, (long long)(rows * conv_dim * 2));
   if (qkv_row_stride < conv_dim || ab_row_stride < num_v_heads || z_row_stride < value_dim ||
       out_row_stride < value_dim || (core_out && core_row_stride < value_dim) ||
-      conv_slot_stride < 3 * conv_dim || ssm_slot_stride < value_dim * kDk)
+      conv_slot_stride < 3 * conv_dim || ssm_slot_stride < value_dim * head_k_dim)
     return fail(TF_ERR_INVALID, "%s: a row or slot stride is too small", fn);
   if (!aligned16(conv_weight) || !aligned16(ssm_state) || ssm_slot_stride % 4)
     return fail(TF_ERR_INVALID, "%s: conv_weight / ssm_state must be 16-byte aligned", fn);
@@ -1034,6 +1132,9 @@ int32_t gdn_setup(const char* fn, const void* qkv, int64_t qkv_row_stride, const
   g->tok = nullptr;
   g->rows = (int32_t)rows;
   g->hk = num_k_heads;
+  g->dk = head_k_dim;
+  g->dv = head_v_dim;
+  g->qscale = (float)(1.0 / sqrt((double)head_k_dim));
   g->wqk = nullptr;
   g->wg = nullptr;
   g->owner = nullptr;
@@ -1139,8 +1240,14 @@ int32_t tf_gdn_decode(const void* qkv, int64_t qkv_row_stride, const void* a, co
   const int64_t n_conv = (int64_t)batch_size * g.conv_dim;
   hipLaunchKernelGGL(gdn_conv_kernel, dim3((n_conv + kThreads - 1) / kThreads), dim3(kThreads),
                      0, s, g);
-  hipLaunchKernelGGL(gdn_recur_kernel, dim3((int64_t)batch_size * num_v_heads), dim3(kThreads), 0,
-                     s, g);
+  if (g.dk != kDk)
+    hipLaunchKernelGGL(gdn_generic_kernel,
+                       dim3((uint32_t)(((int64_t)batch_size * num_v_heads + kGenWaves - 1) /
+                                       kGenWaves)),
+                       dim3(kThreads), 0, s, g);
+  else
+    hipLaunchKernelGGL(gdn_recur_kernel, dim3((int64_t)batch_size * num_v_heads), dim3(kThreads),
+                       0, s, g);
   return launch_status("tf_gdn_decode launch");
 }
 
@@ -1215,6 +1322,16 @@ int32_t tf_gdn_extend(const void* qkv, int64_t qkv_row_stride, const void* a, co
                      dim3((g.conv_dim / kConvCh + kThreads - 1) / kThreads, tblocks),
                      dim3(kThreads), 0, s, g);
   hipLaunchKernelGGL(gdn_conv_state_kernel, dim3(cblocks, batch_size), dim3(kThreads), 0, s, g);
+  if (g.dk != kDk) {   // other head dims: every request's rows in one wave per value head
+    hipLaunchKernelGGL(gdn_generic_kernel,
+                       dim3((uint32_t)(((int64_t)batch_size * num_v_heads + kGenWaves - 1) /
+                                       kGenWaves)),
+                       dim3(kThreads), 0, s, g);
+    hipLaunchKernelGGL(gdn_zero_ext_kernel,
+                       dim3((uint32_t)((n_tokens + kZeroRows - 1) / kZeroRows)), dim3(kThreads),
+                       0, s, g);
+    return launch_status("tf_gdn_extend launch");
+  }
   hipLaunchKernelGGL(gdn_qk_ext_kernel,
                      dim3((uint32_t)n_tokens,
                           (num_k_heads + 2 * kThreads / kWave - 1) / (2 * kThreads / kWave)),

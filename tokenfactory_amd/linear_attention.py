@@ -26,8 +26,17 @@ import torch.nn as nn
 from . import _native
 from .fp8_linear import Fp8Linear, on_stream
 
-HEAD_DIM = 128
+HEAD_DIM = 128      # the tuned kernels' head dims (key and value)
+MAX_OTHER_HEAD_DIM = 64   # other head dims: multiples of 4 up to this (one wave per head)
 CONV_KERNEL = 4
+
+
+def head_dims_supported(dk: int, dv: int) -> bool:
+    """Head dims the kernels take: 128 / 128, or multiples of 4 up to 64 each
+    (the reference's own test models use 16)."""
+    if dk == HEAD_DIM and dv == HEAD_DIM:
+        return True
+    return all(d % 4 == 0 and 4 <= d <= MAX_OTHER_HEAD_DIM for d in (dk, dv))
 
 
 def _ptr(t: Optional[torch.Tensor]) -> int:
@@ -42,7 +51,8 @@ def _rows(t: torch.Tensor, name: str) -> int:
 
 def _check_common(qkv, b, a, z, conv_weight, a_log, dt_bias, norm_weight, layer_conv_state,
                   layer_ssm_state, req_indices, num_v_heads):
-    value_dim = num_v_heads * HEAD_DIM
+    """Checks the shared arguments; returns the head dims (dk, dv) of
+    ``layer_ssm_state`` [slots, Hv, Dk, Dv]."""
     for name, t, dt in (("qkv", qkv, torch.bfloat16), ("b", b, torch.bfloat16),
                         ("a", a, torch.bfloat16), ("z", z, torch.bfloat16),
                         ("conv_weight", conv_weight, torch.float32),
@@ -62,8 +72,13 @@ def _check_common(qkv, b, a, z, conv_weight, a_log, dt_bias, norm_weight, layer_
     cs, ss = layer_conv_state, layer_ssm_state
     if cs.dim() != 3 or cs.stride(2) != 1 or cs.stride(1) != CONV_KERNEL - 1:
         raise ValueError("gdn step: conv state must be [slots, conv_dim, 3] with dense rows")
-    if ss.dim() != 4 or ss[0].numel() != value_dim * HEAD_DIM or not ss[0].is_contiguous():
-        raise ValueError("gdn step: ssm state must be [slots, Hv, 128, 128], dense per slot")
+    if ss.dim() != 4 or ss.shape[1] != num_v_heads or not ss[0].is_contiguous():
+        raise ValueError("gdn step: ssm state must be [slots, Hv, Dk, Dv], dense per slot")
+    dk, dv = int(ss.shape[2]), int(ss.shape[3])
+    if not head_dims_supported(dk, dv):
+        raise NotImplementedError(f"gdn step: head dims {dk} / {dv} (128 / 128, or multiples "
+                                  f"of 4 up to {MAX_OTHER_HEAD_DIM})")
+    return dk, dv
 
 
 def gdn_decode_step(qkv: torch.Tensor, b: torch.Tensor, a: torch.Tensor, z: torch.Tensor,
@@ -74,27 +89,28 @@ def gdn_decode_step(qkv: torch.Tensor, b: torch.Tensor, a: torch.Tensor, z: torc
                     stream=None):
     """One decode step of a Gated DeltaNet layer for B requests (one token each).
 
-    qkv bf16 [B, 2*Hk*128 + Hv*128], b / a bf16 [B, Hv], z bf16 [B, Hv*128];
+    qkv bf16 [B, 2*Hk*Dk + Hv*Dv], b / a bf16 [B, Hv], z bf16 [B, Hv*Dv];
     conv_weight fp32 [conv_dim, 4]; a_log, dt_bias fp32 [Hv]; norm_weight fp32
-    [Hv*128]; layer_conv_state bf16 [slots, conv_dim, 3] and layer_ssm_state
-    fp32 [slots, Hv, 128, 128] (updated in place); req_indices int64 [B] (distinct).
-    Returns the normed bf16 output [B, Hv*128] (and the pre-norm output)."""
+    [Hv*Dv]; layer_conv_state bf16 [slots, conv_dim, 3] and layer_ssm_state
+    fp32 [slots, Hv, Dk, Dv] (updated in place; its shape gives the head dims);
+    req_indices int64 [B] (distinct).
+    Returns the normed bf16 output [B, Hv*Dv] (and the pre-norm output)."""
     bsz = qkv.shape[0]
-    value_dim = num_v_heads * HEAD_DIM
-    _check_common(qkv, b, a, z, conv_weight, a_log, dt_bias, norm_weight, layer_conv_state,
-                  layer_ssm_state, req_indices, num_v_heads)
+    dk, dv = _check_common(qkv, b, a, z, conv_weight, a_log, dt_bias, norm_weight,
+                           layer_conv_state, layer_ssm_state, req_indices, num_v_heads)
+    value_dim = num_v_heads * dv
     cs, ss = layer_conv_state, layer_ssm_state
     s = stream if stream is not None else torch.cuda.current_stream(qkv.device)
     with on_stream(stream):
         out = torch.empty((bsz, value_dim), dtype=torch.bfloat16, device=qkv.device)
         core = torch.empty_like(out) if return_core else None
-        ws = torch.empty((bsz, 2 * num_k_heads * HEAD_DIM + value_dim), dtype=torch.bfloat16,
+        ws = torch.empty((bsz, 2 * num_k_heads * dk + value_dim), dtype=torch.bfloat16,
                          device=qkv.device)
         _native.call("tf_gdn_decode", _ptr(qkv), _rows(qkv, "qkv"), _ptr(a), _ptr(b),
                      _rows(a, "a"), _ptr(z), _rows(z, "z"), _ptr(conv_weight), _ptr(a_log),
                      _ptr(dt_bias), _ptr(norm_weight), float(eps), _ptr(cs), cs.stride(0),
                      _ptr(ss), ss.stride(0), _ptr(req_indices), bsz, cs.shape[0], num_k_heads,
-                     num_v_heads, HEAD_DIM, HEAD_DIM, CONV_KERNEL, _ptr(out), out.stride(0),
+                     num_v_heads, dk, dv, CONV_KERNEL, _ptr(out), out.stride(0),
                      _ptr(core), 0 if core is None else core.stride(0), _ptr(ws),
                      ws.numel() * 2, s.cuda_stream)
     return (out, core) if return_core else out
@@ -109,17 +125,17 @@ def gdn_extend_step(qkv: torch.Tensor, b: torch.Tensor, a: torch.Tensor, z: torc
     """The layer for a batch with any extend lengths (the reference's per-request
     loop, ``linear_attention.py:328-364``): request i owns the next
     ``extend_lens[i]`` token rows of qkv / a / b / z. Same tensors as
-    ``gdn_decode_step`` with rows = tokens; returns ``[T, Hv*128]`` bf16."""
+    ``gdn_decode_step`` with rows = tokens; returns ``[T, Hv*Dv]`` bf16."""
     n_tok = qkv.shape[0]
     lens = [int(e) for e in extend_lens]
     if len(lens) != req_indices.numel() or sum(lens) != n_tok or min(lens, default=1) < 0:
         raise ValueError("gdn_extend_step: extend_lens must cover the token rows, one per request")
-    _check_common(qkv, b, a, z, conv_weight, a_log, dt_bias, norm_weight, layer_conv_state,
-                  layer_ssm_state, req_indices, num_v_heads)
+    dk, dv = _check_common(qkv, b, a, z, conv_weight, a_log, dt_bias, norm_weight,
+                           layer_conv_state, layer_ssm_state, req_indices, num_v_heads)
     offsets = [0]
     for e in lens:
         offsets.append(offsets[-1] + e)
-    value_dim = num_v_heads * HEAD_DIM
+    value_dim = num_v_heads * dv
     ws_bytes = _native.load().tf_gdn_extend_workspace_bytes(n_tok, len(lens), num_k_heads,
                                                            num_v_heads)
     if ws_bytes < 0:
@@ -135,7 +151,7 @@ def gdn_extend_step(qkv: torch.Tensor, b: torch.Tensor, a: torch.Tensor, z: torc
                      _rows(a, "a"), _ptr(z), _rows(z, "z"), _ptr(conv_weight), _ptr(a_log),
                      _ptr(dt_bias), _ptr(norm_weight), float(eps), _ptr(cs), cs.stride(0),
                      _ptr(ss), ss.stride(0), _ptr(req_indices), _ptr(tok), len(lens), n_tok,
-                     max(lens), cs.shape[0], num_k_heads, num_v_heads, HEAD_DIM, HEAD_DIM,
+                     max(lens), cs.shape[0], num_k_heads, num_v_heads, dk, dv,
                      CONV_KERNEL, _ptr(out), out.stride(0), _ptr(core),
                      0 if core is None else core.stride(0), _ptr(ws), ws.numel(), s.cuda_stream)
     return (out, core) if return_core else out
@@ -151,11 +167,15 @@ class LinearAttention(nn.Module):
         self.layer_idx = layer_idx
         self.num_k_heads = config.linear_num_key_heads // tp
         self.num_v_heads = config.linear_num_value_heads // tp
-        if (config.linear_key_head_dim != HEAD_DIM or config.linear_value_head_dim != HEAD_DIM
+        self.head_k_dim = config.linear_key_head_dim
+        self.head_v_dim = config.linear_value_head_dim
+        if (not head_dims_supported(self.head_k_dim, self.head_v_dim)
                 or config.linear_conv_kernel_dim != CONV_KERNEL):
-            raise NotImplementedError("LinearAttention: head dims 128 and conv kernel 4 only")
-        self.key_dim = self.num_k_heads * HEAD_DIM
-        self.value_dim = self.num_v_heads * HEAD_DIM
+            raise NotImplementedError(
+                f"LinearAttention: head dims {self.head_k_dim} / {self.head_v_dim} (128 / 128 or "
+                f"multiples of 4 up to {MAX_OTHER_HEAD_DIM}) with conv kernel {CONV_KERNEL}")
+        self.key_dim = self.num_k_heads * self.head_k_dim
+        self.value_dim = self.num_v_heads * self.head_v_dim
         self.conv_dim = 2 * self.key_dim + self.value_dim
         self.eps = getattr(config, "rms_norm_eps", 1e-6)
         hidden = config.hidden_size
