@@ -187,6 +187,38 @@ def test_gemm_rejects_bad_layouts(gpu):
         fl.block_fp8_gemm(xq, sx, wq, torch.ones((1, 4), device=gpu), None, 128, 64)
 
 
+def test_gemm_split_k_graph_replays(gpu):
+    """A split-K call (partials, then the reduce launch) captured in a graph
+    replays bit-identically to the eager call, with eager calls of another
+    shape between the replays."""
+    print("[fp8 gemm] split-K graph replays", flush=True)
+    wq, ws = make_weight(5120, 6144, 128, 128, 43, gpu)
+    x = make_x(64, 6144, 5, gpu)
+    xq, sx = fl.quantize_activations(x)
+    want = fl.block_fp8_gemm(xq, sx, wq, ws, None).clone()
+    other = make_x(100, 6144, 6, gpu)
+    oq, osx = fl.quantize_activations(other)
+    other_want = fl.block_fp8_gemm(oq, osx, wq, ws, None).clone()
+    out = torch.empty_like(want)
+    stream = torch.cuda.Stream(device=gpu)
+    stream.wait_stream(torch.cuda.current_stream(gpu))
+    with torch.cuda.stream(stream):
+        fl.block_fp8_gemm(xq, sx, wq, ws, None, out=out)    # warm-up on the capture stream
+        stream.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=stream):
+            fl.block_fp8_gemm(xq, sx, wq, ws, None, out=out)
+    torch.cuda.current_stream(gpu).wait_stream(stream)
+    for r in range(4):
+        out.zero_()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, want), f"replay {r} differs from the eager call"
+        got = fl.block_fp8_gemm(oq, osx, wq, ws, None)
+        torch.cuda.synchronize()
+        assert torch.equal(got, other_want), f"eager call after replay {r} differs"
+
+
 def test_gemm_split_k_repeats_bit_identically(gpu):
     """Split-K sums its partials in a fixed order: repeated calls (with other
     shapes, and other split counts, in between) give identical bits."""
