@@ -563,19 +563,20 @@ __global__ void __launch_bounds__(kThreads, 4) gdn_chunk_prep_kernel(GdnArgs a) 
     }
     // this wave's writes of A before its reads (one wave: no barrier needed)
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-    if (g == 0) {   // T = (I + A)^-1 by forward substitution, lane n owns column n
+    if (g == 0) {   // T = (I + A)^-1 by forward substitution, lane n owns column n;
+                    // each row's sum in four interleaved partial sums (shorter FMA chains)
       float tc[kChunk];
 #pragma unroll
       for (int t = 0; t < kChunk; ++t) {
-        float acc = t == n ? 1.f : 0.f;
+        float acc[4] = {t == n ? 1.f : 0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int s4 = 0; s4 < t; s4 += 4) {
           const f32x4 ar = *reinterpret_cast<const f32x4*>(&A[t][s4]);
 #pragma unroll
           for (int e = 0; e < 4; ++e)
-            if (s4 + e < t) acc = fmaf(-ar[e], tc[s4 + e], acc);
+            if (s4 + e < t) acc[e] = fmaf(-ar[e], tc[s4 + e], acc[e]);
         }
-        tc[t] = acc;
+        tc[t] = (acc[0] + acc[1]) + (acc[2] + acc[3]);
         __builtin_amdgcn_sched_barrier(0);
       }
 #pragma unroll
