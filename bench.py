@@ -673,9 +673,9 @@ def measured_traffic():
 def main():
     args = parse()
     if args.gpus != 1:
-        print(json.dumps({"error": "this build measures one GPU only: the full-attention "
-                                   "path needs no collective at TP=1 (see DESIGN.md for how "
-                                   "it would shard); run with --gpus 1"}))
+        print(json.dumps({"error": "one GPU only: the full-attention path at TP=1 runs on "
+                                   "one GPU and needs no collective, and no multi-GPU "
+                                   "sharding is implemented; run with --gpus 1"}))
         sys.exit(2)
     import torch
     if not torch.cuda.is_available():
