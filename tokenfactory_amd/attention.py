@@ -388,12 +388,17 @@ class SlotAttentionCall:
             # Mixed step: the HBM-bound decode launches go to a second stream and
             # run beside the MFMA-bound extend kernel (they write disjoint rows
             # of out); the caller's stream waits for both.
+            # The extend launch goes out first (the decode launch waits only
+            # for the work before it): neither kernel's workgroup fits beside
+            # the other's on a CU, so the decode workgroups take the CUs the
+            # extend kernel's last round leaves idle, rather than the extend
+            # kernel waiting for the decode kernel's persistent grid.
             main, side = self.stream, _side_stream(self.q.device)
             fork, join = _fork_join_events(self.q.device, main)
             fork.record(main)
+            self.run_extend()
             side.wait_event(fork)
             self._decode("tf_attn_decode", side)
-            self.run_extend()
             join.record(side)
             main.wait_event(join)
         else:
