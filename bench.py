@@ -282,7 +282,7 @@ def bench_gate(torch, workloads, SlotAttentionCall, args):
 
 
 def bench_oproj(torch, args):
-    """The block-FP8 o_proj after the gated attention (fp8_linear.py:196-214 ->
+    """The block-FP8 o_proj after the gated attention (fp8_linear.py:181-201 ->
     triton_block_fp8_linear): 24 x 256 -> 5120, 128 x 128 weight-scale blocks,
     at the token counts of the decode_b64, mixed and extend_prefix steps."""
     from tokenfactory_amd import fp8_linear as fl

@@ -15,7 +15,7 @@
  *    req_pool_indices, seq_lens, out_cache_loc; ForwardBatch,
  *    qwen3_8/forward_batch.py:19-31).  Work lists made by the planners are int32.
  *  - KV pools are one layer's [pool_slots, num_kv_heads, head_dim] block
- *    (qwen3_8/hybrid_cache_pool.py:96-106, 151-154), row-major, in bf16 or in
+ *    (qwen3_8/hybrid_cache_pool.py:48-61, accessor :106-109), row-major, in bf16 or in
  *    OCP fp8-e4m3 with per-tensor fp32 scales (k_scale / v_scale, device
  *    scalars; ignored for bf16).  Slot 0 is the padding slot
  *    (token_to_kv_pool.py:20-23); req_to_token holds -1 for empty positions
@@ -197,8 +197,9 @@ int32_t tf_attn_decode_noalloc(const void* q, int64_t q_row_stride,
  * full_attention.py:244-283, and the ext_len > 1 case of the bsz == 1 branch,
  * full_attention.py:179-213.
  *
- * work: device int32 [n_work][8] from tf_attn_plan_extend(); one entry per
- * (request, kv head, tile of 256 (token, q-head) rows).
+ * work: device int32 [n_work][8] from tf_attn_plan_extend() or
+ * tf_attn_plan_device(); one entry per (request, kv head, tile of 256
+ * (token, q-head) rows).
  * gate, out_amax: optional output gate and output amax, as for tf_attn_decode.
  */
 int32_t tf_attn_extend(const void* q, int64_t q_row_stride,
@@ -354,7 +355,7 @@ int32_t tf_qk_norm_rope_kv_write(const void* q, int64_t q_token_stride, int64_t 
 
 /* ------------------------------------------------------------------ FP8 linear
  * The block-FP8 o_proj that follows the gated attention output
- * (full_attention.py:161 -> RowParallelFP8Linear, fp8_linear.py:196-214 ->
+ * (full_attention.py:161 -> RowParallelFP8Linear, fp8_linear.py:181-201 ->
  * triton_block_fp8_linear, fp8_triton.py:107-183), as two calls.
  *
  * tf_fp8_act_quant replaces the dynamic activation quantisation of
@@ -478,12 +479,12 @@ int32_t tf_gdn_decode(const void* qkv, int64_t qkv_row_stride, const void* a, co
  * tokens and value head, its state in registers from first chunk to last),
  * and zeros for the rows of no request or of an out-of-pool slot.  When the
  * batch can hold both kinds of request (batch_size > 1, max_extend_len > 1),
- * the one-token update runs on a second stream of the library's (one per
- * device, made on the first call that is not under graph capture) that forks
- * from `stream` after the chunk preparation and joins it before the call
- * returns; under capture the fork and join become graph dependencies.
- * Concurrent calls on one device serialise their launch sequences on a
- * lock.  qkv, z, out and core_out must be 8-byte aligned
+ * the one-token update of a call that is not under graph capture runs on a
+ * second stream of the library's (one per device, made on the first such
+ * call) that forks from `stream` after the chunk preparation and joins it
+ * before the call returns; concurrent calls on one device serialise their
+ * fork .. join sequences on a lock.  A call under capture launches everything
+ * on `stream`, so captured and eager calls never share the second stream.  qkv, z, out and core_out must be 8-byte aligned
  * with row strides that are multiples of 4; norm_weight 16-byte aligned.  Other arguments
  * as for tf_gdn_decode, with rows = tokens; workspace:
  * tf_gdn_extend_workspace_bytes(n_tokens, batch_size, Hk, Hv) bytes, 16-byte

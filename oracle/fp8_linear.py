@@ -4,7 +4,7 @@ TEST INFRASTRUCTURE ONLY.
 
 Restates, op for op on the CPU, the reference's Triton path for a
 float8_e4m3fn weight (``Qwen3_8FP8Linear._linear_op``,
-``qwen3_8/fp8_linear.py:196-214``):
+``qwen3_8/fp8_linear.py:181-201``):
 
 * ``quantize_activations`` -- ``triton_block_fp8_linear``'s dynamic
   per-tensor activation quantisation (``qwen3_8/fp8_triton.py:127-130``):

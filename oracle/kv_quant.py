@@ -3,7 +3,7 @@
 TEST INFRASTRUCTURE ONLY.
 
 The reference keeps its KV pool in the activation dtype
-(``qwen3_8/hybrid_cache_pool.py:96-106``); the fp8 KV variant is this build's
+(``qwen3_8/hybrid_cache_pool.py:48-61``); the fp8 KV variant is this build's
 addition. Its convention, shared by the HIP write kernel:
 
 * scale ``s`` is a positive fp32 per-tensor factor (``amax / 448`` for the

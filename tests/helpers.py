@@ -58,5 +58,18 @@ def assert_attn_close(out, ref, atol=ATOL, rtol=RTOL, norm_rel=NORM_REL, what=""
     return err.max().item(), rel
 
 
+def assert_empty_context_rows(out, ref, empty, what=""):
+    """Rows of requests with no visible key: the reference's
+    scaled_dot_product_attention with an all -inf mask row
+    (full_attention.py:231-242) returns zeros for them (torch's safe softmax),
+    and ``out`` must hold exact zeros there; every row is then compared with
+    ``assert_attn_close``."""
+    out = torch.as_tensor(out).float().cpu()
+    ref = torch.as_tensor(ref).float().cpu()
+    assert (ref[empty] == 0).all(), f"{what}: oracle rows not zero"
+    assert (out[empty] == 0).all(), f"{what}: empty-context rows not zero"
+    return assert_attn_close(out, ref, what=what)
+
+
 def as_numpy(x):
     return np.asarray(torch.as_tensor(x).float().cpu().numpy(), dtype=np.float64)

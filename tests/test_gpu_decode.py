@@ -8,7 +8,8 @@ import numpy as np
 import pytest
 import torch
 
-from tests.helpers import assert_attn_close, rebatch, restatement, small_case
+from tests.helpers import (assert_attn_close, assert_empty_context_rows, rebatch, restatement,
+                           small_case)
 from tokenfactory_amd import _native, slot_based_attention, workloads
 
 pytestmark = pytest.mark.gpu
@@ -58,6 +59,20 @@ def test_empty_and_tiny_requests(gpu):
                     dtype=torch.bfloat16)
     for wg in (0, 5, 40):
         check(wl, wg, what=f"tiny wg={wg}")
+
+
+@pytest.mark.parametrize("workgroups", [0, 3])
+def test_empty_context_rows_are_zero(gpu, workgroups):
+    """A request with seq_len 0 sees no key: its row is zeros, as the
+    reference's fully masked attention returns it, and the other rows are
+    unaffected."""
+    wl = small_case([300, 40, 1000, 2], [1] * 4, hq=24, hkv=4, d=256, seed=9, device=gpu,
+                    dtype=torch.bfloat16)
+    wl.batch.seq_lens[1] = 0
+    print(f"[decode] empty context at row 1, workgroups={workgroups}", flush=True)
+    out = run(wl, workgroups)
+    torch.cuda.synchronize()
+    assert_empty_context_rows(out, restatement(wl), [1], what="seq_len 0")
 
 
 def test_workspace_reuse_across_shapes(gpu):

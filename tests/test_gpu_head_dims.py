@@ -20,7 +20,7 @@ import torch.nn.functional as F
 from oracle.kv_quant import quantize_e4m3
 from oracle.qk_prep import inv_freq_ref, qk_prep_ref
 from oracle.slot_attention import slot_based_attention_ref
-from tests.helpers import assert_attn_close, restatement, small_case
+from tests.helpers import assert_attn_close, assert_empty_context_rows, restatement, small_case
 from tests.test_gpu_gate import assert_bits_match, module_gate
 from tokenfactory_amd import qk_norm_rope_kv_write, slot_based_attention, workloads
 from tokenfactory_amd.forward_batch import ForwardBatch
@@ -49,6 +49,18 @@ def test_decode(gpu, d):
     wl = small_case([1, 5, 64, 65, 300, 1000], [1] * 6, hq=8, hkv=2, d=d, seed=d, device=gpu,
                     dtype=torch.bfloat16)
     check(wl, "decode")
+
+
+@pytest.mark.parametrize("d", DIMS)
+def test_decode_empty_context_rows_are_zero(gpu, d):
+    """seq_len 0: a row of zeros, as at head_dim 256 and in the reference."""
+    wl = small_case([7, 300, 64], [1] * 3, hq=8, hkv=2, d=d, seed=d + 7, device=gpu,
+                    dtype=torch.bfloat16)
+    wl.batch.seq_lens[0] = 0
+    print(f"[head dims] empty context D={d}", flush=True)
+    out = run(wl)
+    torch.cuda.synchronize()
+    assert_empty_context_rows(out, restatement(wl), [0], what=f"seq_len 0 D={d}")
 
 
 @pytest.mark.parametrize("d", DIMS)

@@ -90,9 +90,16 @@ def test_amax_on_two_streams_and_shared_word(gpu):
 
 def test_nan_row_sets_the_nan_pattern(gpu):
     wl = bf16_case([5, 64], [1, 1], seed=12, gpu=gpu)
-    wl.batch.seq_lens[1] = 0   # an empty context: the reference's softmax gives NaN
+    wl.q[1] = float("nan")   # NaN scores: the reference's softmax gives a NaN row
     out, amax = run_with_amax(wl)
     assert torch.isnan(out[1].float()).all() and int(amax.item()) == bits_amax(out) >= 0x7f81
+
+
+def test_empty_context_row_adds_nothing_to_amax(gpu):
+    wl = bf16_case([5, 64], [1, 1], seed=12, gpu=gpu)
+    wl.batch.seq_lens[1] = 0   # no visible key: a row of zeros
+    out, amax = run_with_amax(wl)
+    assert (out[1] == 0).all() and int(amax.item()) == bits_amax(out[:1]) == bits_amax(out)
 
 
 @pytest.mark.parametrize("name", ["decode", "mixed", "fp8 mixed"])

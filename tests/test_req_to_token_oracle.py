@@ -131,3 +131,22 @@ def test_plan_rejects_duplicate_rows_and_bad_ranges():
         dev.plan([0], [3], [9], host)
     with pytest.raises(NotImplementedError):
         dev.plan(list(range(4097)), [0] * 4097, [0] * 4097, host)
+
+
+def test_rejected_batch_moves_no_cursor():
+    """A batch rejected anywhere (a later request out of range, or an
+    out_cache_loc that does not hold one slot per new position) leaves every
+    request's sync cursor and dirty_from mark where they were, so the next
+    sync still rewrites what the rejected one would have."""
+    dev = DeviceReqToTokenTable(4, 8, device="cpu")
+    host = [[10 * r + i for i in range(8)] for r in range(4)]
+    dev.plan([2], [0], [3], host)
+    before = list(dev.synced_lens)
+    df = [1, 1, 1, 1]
+    with pytest.raises(ValueError):
+        dev.plan([0, 3], [2, 5], [4, 9], host, df)      # row 3's [5, 9) leaves the table
+    assert dev.synced_lens == before and df == [1, 1, 1, 1]
+    loc = torch.arange(4, dtype=torch.long)               # 2 + 3 new positions need 5
+    with pytest.raises(ValueError, match="out_cache_loc"):
+        dev.sync([0, 2], [2, 3], [4, 6], loc, host, df)
+    assert dev.synced_lens == before and df == [1, 1, 1, 1]

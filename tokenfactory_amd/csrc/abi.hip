@@ -4,6 +4,7 @@
 #include <string.h>
 
 #include <algorithm>
+#include <mutex>
 #include <vector>
 
 #include "tf_internal.h"
@@ -26,6 +27,22 @@ int launch_status(const char* what) {
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return fail(TF_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
   return TF_OK;
+}
+
+int device_cu_count() {
+  static int cached[64];
+  static std::mutex mu;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  std::lock_guard<std::mutex> lock(mu);
+  if (cached[dev] == 0) {
+    int cus = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        cus <= 0)
+      cus = 256;
+    cached[dev] = cus;
+  }
+  return cached[dev];
 }
 
 }  // namespace tfa

@@ -113,8 +113,10 @@ __global__ void __launch_bounds__(kGenThreads) generic_attn_kernel(GenericAttnAr
     if (L > a.rtt_cols) L = a.rtt_cols;
     limit = L - 1;
   }
+  // A row with no visible key (a decode item with seq_len 0, an extend row
+  // past a too-short context) is all zeros, as the reference's fully masked
+  // scaled_dot_product_attention returns it and as the tuned kernels write it.
   const int64_t nkeys = limit + 1;
-  if (nkeys <= 0) return;
 
   const int64_t rrow = clamp_i64(a.rpi[b], 0, a.rtt_rows - 1);
   const int64_t* rtt = a.rtt + rrow * a.rtt_stride;
@@ -125,13 +127,14 @@ __global__ void __launch_bounds__(kGenThreads) generic_attn_kernel(GenericAttnAr
   const uint8_t* vbase = a.v_pool + (int64_t)hk * D * esz;
 
   // q row, packed bf16, in this wave's LDS row (every lane reads the same
-  // word: a broadcast).  Only this wave touches it, and its LDS accesses run
-  // in order, so no barrier is needed.
+  // word: a broadcast).  Only this wave touches it; wave_lds_sync orders
+  // every lane's writes before any lane's reads.
   __shared__ uint32_t qs_all[kGenWaves][kGenMaxD / 2];
   uint32_t* q = qs_all[threadIdx.x / kWave];
   const uint32_t* qp =
       reinterpret_cast<const uint32_t*>(a.q + qrow * a.q_stride + (int64_t)h * D);
   for (int i = lane; i < D / 2; i += kWave) q[i] = qp[i];
+  wave_lds_sync();
 
   const float sl2 = a.scale_log2 * (FP8 ? a.k_scale[0] : 1.f);
   float m = -INFINITY, l = 0.f;
@@ -186,7 +189,7 @@ __global__ void __launch_bounds__(kGenThreads) generic_attn_kernel(GenericAttnAr
     }
   }
 
-  const float inv = (FP8 ? a.v_scale[0] : 1.f) / l;
+  const float inv = nkeys > 0 ? (FP8 ? a.v_scale[0] : 1.f) / l : 0.f;
   __bf16* orow = a.out + qrow * a.out_stride + (int64_t)h * D;
   const __bf16* grow = a.gate ? a.gate + qrow * a.gate_stride + (int64_t)h * a.gate_hstride
                               : nullptr;

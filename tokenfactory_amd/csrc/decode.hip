@@ -537,7 +537,8 @@ decode_kernel(DecodeArgs a) {
 
 // Merges the partials of every unit owned by more than one workgroup of the
 // streaming kernel; one workgroup per unit. Units of an empty request (L = 0)
-// get NaN, as the reference's fully masked softmax does.
+// get zeros, as the reference's fully masked scaled_dot_product_attention
+// returns them (torch's safe softmax: a row with no visible key is all zeros).
 template <bool FP8>
 __global__ void __launch_bounds__(kWaves * kWave)
 decode_merge_kernel(DecodeArgs a) {
@@ -586,13 +587,13 @@ decode_merge_kernel(DecodeArgs a) {
   WaveState st;
   reset_state(st);
   if (Ti == 0) {
-    // An empty context (seq_len 0) is a NaN row, as the reference's softmax
-    // over no keys; padding entries write nothing.
+    // An empty context (seq_len 0) is a row of zeros (the reference's fully
+    // masked attention); padding entries write nothing.
     if (w == 0) {
       uint32_t m = 0;
       if (head_ok && !item_is_padding(a, item)) {
         st.m = 0.f;
-        st.l = __builtin_nanf("");
+        st.l = 1.f;   // O = 0
         m = write_output<FP8>(a, qrow, hq, g, st, 1.f);
       }
       amax_commit(a.amax, m);
@@ -625,21 +626,6 @@ decode_merge_kernel(DecodeArgs a) {
 
 }  // namespace
 
-static int device_cu_count() {
-  static int cached[64];
-  static std::mutex mu;
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-  std::lock_guard<std::mutex> lock(mu);
-  if (cached[dev] == 0) {
-    int cus = 0;
-    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
-        cus <= 0)
-      cus = 256;
-    cached[dev] = cus;
-  }
-  return cached[dev];
-}
 
 int make_decode_plan(int32_t n_items, int32_t num_q_heads, int32_t num_kv_heads,
                      int32_t head_dim, int32_t max_seq_len, int32_t num_workgroups,

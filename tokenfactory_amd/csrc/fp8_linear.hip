@@ -2,7 +2,7 @@
 //
 // Replaces the reference's triton_block_fp8_linear (qwen3_8/fp8_triton.py:107-183)
 // and its GEMM kernel _block_fp8_gemm_kernel (fp8_triton.py:17-98), which
-// Qwen3_8FP8Linear._linear_op (qwen3_8/fp8_linear.py:196-214) uses for a
+// Qwen3_8FP8Linear._linear_op (qwen3_8/fp8_linear.py:181-201) uses for a
 // float8_e4m3fn weight:
 //   x_scale = bf16(max(amax|x|, 1e-12) / 448)            dynamic, per tensor
 //   xq      = e4m3(clamp(x / x_scale, -448, 448))          round to nearest even
@@ -421,17 +421,17 @@ Shape gemm_shape(int64_t m) {
 }
 
 // Split-K factor: when the output tiles alone leave most CUs idle (M up to 512,
-// the weight-streaming regime), K is split so that the workgroups fill the 256
-// CUs in one round (320 workgroups, one and a quarter rounds, took 1.4 times
-// as long at M = 64).
-constexpr int kCUs = 256;
+// the weight-streaming regime), K is split so that the workgroups fill the
+// device's CUs (256 on MI355X) in one round (320 workgroups, one and a quarter
+// rounds, took 1.4 times as long at M = 64).
 int gemm_splits(int64_t m, int64_t n, int64_t k) {
   const Shape sh = gemm_shape(m);
   if (m > 512 || n % 4) return 1;
+  const int64_t cus = device_cu_count();
   const int64_t tiles = ((m + 32 * sh.mt - 1) / (32 * sh.mt)) * ((n + 64 * sh.wn - 1) / (64 * sh.wn));
   const int64_t kb = k / kKSlice;
-  if (tiles >= kCUs / 2 || kb < 4) return 1;
-  return (int)std::max<int64_t>(1, std::min<int64_t>({kb / 2, kCUs / tiles, 16}));
+  if (tiles >= cus / 2 || kb < 4) return 1;
+  return (int)std::max<int64_t>(1, std::min<int64_t>({kb / 2, cus / tiles, 16}));
 }
 
 template <int MT, int WN, int STAGES>

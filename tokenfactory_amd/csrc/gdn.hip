@@ -983,7 +983,7 @@ __global__ void __launch_bounds__(kThreads) gdn_generic_kernel(GdnArgs a) {
       qk[0][lane] = qv / fmaxf(nq, 1e-12f) * a.qscale;
       qk[1][lane] = kv / fmaxf(nk, 1e-12f);
     }
-    // (one wave: its LDS writes land before its reads below)
+    wave_lds_sync();   // every lane reads every entry below
     const float x = bf(a.a[(int64_t)row * a.ab_rs + h]) + a.dt_bias[h];
     const float sp = x > 20.f ? x : log1pf(expf(x));           // F.softplus
     const float alpha = expf(-expf(a.a_log[h]) * sp);
@@ -1011,6 +1011,7 @@ __global__ void __launch_bounds__(kThreads) gdn_generic_kernel(GdnArgs a) {
       a.out[(int64_t)row * a.out_rs + h * dv + lane] =
           to_bf(a.norm_w[h * dv + lane] * xn * (zz / (1.f + expf(-zz))));
     }
+    wave_lds_sync();   // the reads above finish before the next row overwrites qk
   }
 #pragma unroll
   for (int k = 0; k < kGenD; ++k)
@@ -1154,8 +1155,9 @@ int32_t gdn_setup(const char* fn, const void* qkv, int64_t qkv_row_stride, const
 // small share of the HBM bandwidth, so the HBM-bound one-token updates fit
 // beside it (they touch other state slots and output rows, so the two need
 // no order between them).  The stream and its fork / join events are made on
-// the first call that is not under graph capture; `mu` keeps the fork .. join
-// sequences of concurrent callers apart.
+// the first call that is not under graph capture, and only calls that are not
+// under capture use them; `mu` keeps the fork .. join sequences of concurrent
+// callers apart.
 struct SideLane {
   std::mutex mu;
   hipStream_t stream = nullptr;
@@ -1344,7 +1346,16 @@ int32_t tf_gdn_extend(const void* qkv, int64_t qkv_row_stride, const void* a, co
   // The one-token recurrence on the side stream, beside the chunked pass,
   // when the batch can hold both kinds of request; it needs only the conv
   // outputs, and the caller's stream waits for it before the call's end.
-  SideLane* lane = (max_extend_len > 1 && batch_size > 1) ? side_lane(s) : nullptr;
+  // A call under graph capture keeps everything on the caller's stream: the
+  // side stream, once joined into a capture, would stay in capture mode until
+  // that capture ends, and an eager call from another thread would then
+  // launch onto it.
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  const bool capturing =
+      hipStreamIsCapturing(s, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone;
+  (void)hipGetLastError();
+  SideLane* lane =
+      (!capturing && max_extend_len > 1 && batch_size > 1) ? side_lane(s) : nullptr;
   std::unique_lock<std::mutex> held;
   hipStream_t rs = s;
   if (lane) {

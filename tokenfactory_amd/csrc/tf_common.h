@@ -24,6 +24,16 @@ constexpr int kWave = 64;
 constexpr float kLog2e = 1.4426950408889634f;
 
 // ---------------------------------------------------------------- loads
+// Orders a wave's LDS accesses across its lanes: every lane's earlier LDS
+// writes are visible to every lane's later reads (and earlier reads complete
+// before later overwrites).  A wave-scope release / acquire around a wave
+// barrier, for data passed between the lanes of one wave through LDS.
+__device__ __forceinline__ void wave_lds_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
 __device__ __forceinline__ u32x4 ld_g16(const void* p) {
   return *reinterpret_cast<const u32x4*>(p);
 }

@@ -14,6 +14,8 @@ int fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
 void clear_error();
 // Maps the most recent launch status to TF_OK / TF_ERR_HIP.
 int launch_status(const char* what);
+// Compute units of the current device (cached per device; 256 if the query fails).
+int device_cu_count();
 
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 inline bool aligned8(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 7u) == 0; }

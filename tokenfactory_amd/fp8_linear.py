@@ -6,7 +6,7 @@
 activations to e4m3 (``tf_fp8_act_quant``) followed by the block-scaled FP8
 GEMM (``tf_fp8_block_gemm``), bf16 in and out.
 
-``Fp8Linear`` mirrors ``Qwen3_8FP8Linear`` (``qwen3_8/fp8_linear.py:12-222``)
+``Fp8Linear`` mirrors ``Qwen3_8FP8Linear`` (``qwen3_8/fp8_linear.py:12-212``)
 for a float8_e4m3fn weight: the same parameter and buffer names and shapes
 (``weight`` ``[out, in]``, ``weight_scale_inv`` ``[ceil(out / block_h),
 ceil(in / block_w)]``), ``dequantize_weight`` with the reference's
@@ -179,7 +179,7 @@ def block_fp8_linear(x: torch.Tensor, weight: torch.Tensor,
 
 
 class Fp8Linear(nn.Module):
-    """``Qwen3_8FP8Linear`` with a float8_e4m3fn weight (``fp8_linear.py:12-222``).
+    """``Qwen3_8FP8Linear`` with a float8_e4m3fn weight (``fp8_linear.py:12-212``).
 
     ``weight``: float8_e4m3fn ``[out_features, in_features]``;
     ``weight_scale_inv``: fp32 ``[ceil(out / block_h), ceil(in / block_w)]``

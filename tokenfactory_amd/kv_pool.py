@@ -1,6 +1,6 @@
 """Full-attention KV pool: the token-slot half of the reference's hybrid cache pool.
 
-Layout as the reference (``qwen3_8/hybrid_cache_pool.py:92-106, 151-154``):
+Layout as the reference (``qwen3_8/hybrid_cache_pool.py:48-61``, accessor ``:106-109``):
 ``k_buffer`` / ``v_buffer`` are ``[num_full_layers, max_total_tokens,
 local_kv_heads, head_dim]``; ``get_full_kv_buffers(layer_idx)`` returns the
 contiguous ``[S, Hkv, D]`` views of one full-attention layer, indexed by model
@@ -46,7 +46,7 @@ class FullAttnKVPool:
     def from_config(cls, config, max_total_tokens: int, device="cuda",
                     dtype: torch.dtype = torch.bfloat16) -> "FullAttnKVPool":
         """Builds the pool the way ``Qwen3_8HybridCachePool`` sizes its full-attention
-        part (``hybrid_cache_pool.py:82-106``): full layers from ``layer_types``,
+        part (``hybrid_cache_pool.py:36-61``, layer list from ``config.py:83-87``): full layers from ``layer_types``,
         ``max(1, num_key_value_heads // tp_size)`` local kv heads."""
         layers = [i for i, t in enumerate(config.layer_types) if t == "full_attention"]
         local_kv = max(1, config.num_key_value_heads // getattr(config, "tp_size", 1))

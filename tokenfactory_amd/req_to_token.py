@@ -55,7 +55,15 @@ class DeviceReqToTokenTable:
         (rewritten positions start at min(synced_len, dirty_from); afterwards
         both cursors move to the request's length).  Returns the int64 staging
         array ``[rows | prefix | seq | patch_from | patch_offsets | patch_vals]``
-        and updates ``synced_lens`` and ``dirty_from`` in place."""
+        and updates ``synced_lens`` and ``dirty_from`` in place (only once the
+        whole batch has been checked: a rejected batch moves no cursor)."""
+        staged, rows, seqs = self._plan(req_pool_indices, prefix_lens, seq_lens, host_table,
+                                        dirty_from)
+        self.mark_synced(rows, seqs, dirty_from)
+        return staged
+
+    def _plan(self, req_pool_indices, prefix_lens, seq_lens, host_table, dirty_from):
+        """``plan`` without the cursor updates: (staging array, rows, lengths)."""
         b = len(req_pool_indices)
         if not (len(prefix_lens) == len(seq_lens) == b):
             raise ValueError("req_pool_indices, prefix_lens and seq_lens differ in length")
@@ -85,10 +93,8 @@ class DeviceReqToTokenTable:
                     raise ValueError(f"host row {r} is shorter than position {start}")
                 runs.append(run)
                 n_patch += run.size
-            self.synced_lens[r] = seq
-            if dirty_from is not None:
-                dirty_from[r] = seq
-        return np.concatenate([head] + runs) if runs else head
+        staged = np.concatenate([head] + runs) if runs else head
+        return staged, [int(r) for r in head[:b]], [int(v) for v in head[2 * b:3 * b]]
 
     def sync(self, req_pool_indices: Sequence[int], prefix_lens: Sequence[int],
              seq_lens: Sequence[int], out_cache_loc: torch.Tensor,
@@ -98,7 +104,16 @@ class DeviceReqToTokenTable:
         device int64 views of (req_pool_indices, prefix_lens, seq_lens), which
         the caller can hand to ``ForwardBatch`` instead of copying them again."""
         b = len(req_pool_indices)
-        staged = self.plan(req_pool_indices, prefix_lens, seq_lens, host_table, dirty_from)
+        # Everything is checked before any cursor moves: the batch, then the
+        # new tokens' slots (one per position in [prefix, seq) of each request,
+        # in batch order, as model_runner.py:148-165 consumes them).
+        staged, rows_h, seqs_h = self._plan(req_pool_indices, prefix_lens, seq_lens, host_table,
+                                            dirty_from)
+        self._check_tensor("out_cache_loc", out_cache_loc)
+        n_new = int(sum(int(sq) - int(p) for p, sq in zip(prefix_lens, seq_lens)))
+        if out_cache_loc.numel() != n_new:
+            raise ValueError(f"out_cache_loc holds {out_cache_loc.numel()} slots for {n_new} "
+                             f"new positions")
         if b == 0:
             empty = torch.empty(0, dtype=torch.long, device=self.device)
             return empty, empty, empty
@@ -109,6 +124,7 @@ class DeviceReqToTokenTable:
         n_patch = staged.size - 5 * b
         self._launch(rows, prefix, seq, out_cache_loc,
                      dev[3 * b:4 * b], dev[4 * b:5 * b], dev[5 * b:], n_patch)
+        self.mark_synced(rows_h, seqs_h, dirty_from)
         return rows, prefix, seq
 
     def sync_from_device(self, req_pool_indices: torch.Tensor, prefix_lens: torch.Tensor,
@@ -127,13 +143,16 @@ class DeviceReqToTokenTable:
             if dirty_from is not None:
                 dirty_from[r] = seq
 
+    def _check_tensor(self, name: str, t: torch.Tensor) -> None:
+        if t.dtype != torch.long or t.device != self.device or not t.is_contiguous():
+            raise ValueError(f"{name} must be a contiguous int64 tensor on {self.device}")
+
     def _launch(self, rows, prefix, seq, loc, pfrom, poff, pvals, n_patch,
                 num_workgroups: int = 0) -> None:
         b = rows.numel()
         for name, t in (("req_pool_indices", rows), ("prefix_lens", prefix),
                         ("seq_lens", seq), ("out_cache_loc", loc)):
-            if t.dtype != torch.long or t.device != self.device or not t.is_contiguous():
-                raise ValueError(f"{name} must be a contiguous int64 tensor on {self.device}")
+            self._check_tensor(name, t)
         if prefix.numel() != b or seq.numel() != b:
             raise ValueError("req_pool_indices, prefix_lens and seq_lens differ in length")
         stream = torch.cuda.current_stream(self.device).cuda_stream
