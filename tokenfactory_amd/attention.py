@@ -133,6 +133,92 @@ def _side_stream(device: torch.device) -> torch.cuda.Stream:
         return st
 
 
+_plan_events: Dict[Tuple[int, int], torch.cuda.Event] = {}
+
+
+def _plan_event(device: torch.device, stream: torch.cuda.Stream) -> torch.cuda.Event:
+    """One reusable event per (device, planning stream), recorded behind a
+    shared step plan for the other streams that read it."""
+    idx = device.index if device.index is not None else torch.cuda.current_device()
+    key = (idx, stream.cuda_stream)
+    ev = _plan_events.get(key)
+    if ev is None:
+        ev = torch.cuda.Event()
+        _plan_events[key] = ev
+    return ev
+
+
+class StepPlan:
+    """The work lists of one model step for one head layout: the extend work
+    entries and the decode items / rows of a ``ForwardBatch``, planned on the
+    device (``tf_attn_plan_device``, from ``extend_lens_tensor``) by the first
+    attention call of the step and read by every later one.
+
+    A model step runs every full-attention layer over the same batch
+    (``decoder_layer.py:68-69`` calls the attention once per layer), so the
+    lists do not change between layers; ``slot_based_attention`` keeps one
+    ``StepPlan`` per (device, T, q heads, kv heads) on the batch object itself.
+    Calls on another stream than the planning one wait for the plan (an event
+    recorded on the planning stream)."""
+
+    def __init__(self, batch, n_tok: int, n_q: int, n_kv: int, device: torch.device):
+        bsz = batch.batch_size
+        ext_t = batch.extend_lens_tensor
+        if ext_t is None or ext_t.device != device or ext_t.dtype != torch.long \
+                or ext_t.numel() != bsz or not ext_t.is_contiguous():
+            raise ValueError("a device plan needs batch.extend_lens_tensor: contiguous int64 "
+                             "[batch_size] on q's device")
+        self.batch_size, self.n_q, self.n_kv = bsz, n_q, n_kv
+        self.ext_t = ext_t
+        self.n_work = _native.plan_device_capacity(n_tok, bsz, n_q, n_kv)
+        self.n_dec = bsz
+        self.meta = torch.empty(self.n_work * 8 + 2 * bsz + 4, dtype=torch.int32, device=device)
+        base = self.meta.data_ptr() + 4 * self.n_work * 8
+        self.items = _DevPtr(base)
+        self.rows = _DevPtr(base + 4 * bsz)
+        self.status = _DevPtr(base + 8 * bsz)
+        self.device = device
+        self._lock = threading.Lock()
+        self._planned_on: Optional[torch.cuda.Stream] = None
+        self._event: Optional[torch.cuda.Event] = None
+
+    def ensure(self, stream: torch.cuda.Stream) -> None:
+        """Plan on ``stream`` if no call has yet; else order ``stream`` after
+        the plan."""
+        with self._lock:
+            if self._planned_on is None:
+                _native.call("tf_attn_plan_device", self.ext_t.data_ptr(), self.batch_size,
+                             self.n_q, self.n_kv, 1, self.meta.data_ptr(), self.n_work,
+                             self.items.data_ptr(), self.rows.data_ptr(), self.n_dec,
+                             self.status.data_ptr(), stream.cuda_stream)
+                with _ws_lock:
+                    self._event = _plan_event(self.device, stream)
+                    self._event.record(stream)
+                self._planned_on = stream
+            elif self._planned_on.cuda_stream != stream.cuda_stream:
+                # (a later step planned on the same stream may have recorded the
+                # event again: the wait then covers more than this plan)
+                stream.wait_event(self._event)
+
+
+_STEP_PLANS = "_tf_attn_step_plans"
+
+
+def step_plan(batch, n_tok: int, n_q: int, n_kv: int, device: torch.device) -> StepPlan:
+    """The ``StepPlan`` of ``batch`` for this head layout (made on first use)."""
+    key = (device.index, n_tok, n_q, n_kv)
+    with _ws_lock:
+        plans = getattr(batch, _STEP_PLANS, None)
+        if plans is None:
+            plans = {}
+            setattr(batch, _STEP_PLANS, plans)
+        plan = plans.get(key)
+        if plan is None:
+            plan = StepPlan(batch, n_tok, n_q, n_kv, device)
+            plans[key] = plan
+        return plan
+
+
 def _ptr(t) -> Optional[int]:
     return None if t is None else t.data_ptr()
 
@@ -198,9 +284,12 @@ class SlotAttentionCall:
 
     ``overlap_decode`` (default: ``device_plan``): on a mixed step, run the
     decode launches on a second stream beside the extend kernel (the results
-    are identical). Meant for a call that is built once and run many times:
-    with a new call per step the ROCm runtime stalls the host periodically on
-    the cross-stream waits, so per-step calls keep one stream.
+    are identical).  The fork / join events are cached per (device, stream),
+    so calls made per step do not create events (events destroyed while
+    their waits are still queued stall the host on ROCm).
+
+    ``step_plan``: the batch's shared ``StepPlan`` (implies the device plan);
+    ``run()`` then plans only if no earlier call of the step did.
 
     ``out_amax`` (optional 1-element int32 tensor on q's device): every launch
     raises it to the largest bf16 bit pattern of ``|out|`` it writes (sign
@@ -213,7 +302,8 @@ class SlotAttentionCall:
     def __init__(self, q, layer_k_buffer, layer_v_buffer, batch, *, scaling=None,
                  k_scale=None, v_scale=None, decode_workgroups: int = 0, out=None,
                  stream=None, gate=None, device_plan: bool = False,
-                 overlap_decode: Optional[bool] = None, out_amax=None):
+                 overlap_decode: Optional[bool] = None, out_amax=None,
+                 step_plan: Optional[StepPlan] = None):
         _check_inputs(q, layer_k_buffer, layer_v_buffer, batch)
         n_tok, n_q, head_dim = q.shape
         n_slots, n_kv, _ = layer_k_buffer.shape
@@ -265,7 +355,8 @@ class SlotAttentionCall:
         self.k_scale, self.v_scale = k_scale, v_scale
         self.batch = batch
         self._fixed_stream = stream
-        self.device_plan = bool(device_plan)
+        self._shared_plan = step_plan
+        self.device_plan = bool(device_plan) or step_plan is not None
         self.n_q, self.n_kv, self.head_dim = n_q, n_kv, head_dim
         self.scaling = float(scaling)
         self.decode_workgroups = int(decode_workgroups)
@@ -277,7 +368,8 @@ class SlotAttentionCall:
                            rtt.data_ptr(), rtt.shape[0], rtt.stride(0), rtt.shape[1],
                            batch.req_pool_indices.data_ptr(), batch.seq_lens.data_ptr(),
                            seq_override)
-        self.overlap_decode = device_plan if overlap_decode is None else bool(overlap_decode)
+        self.overlap_decode = (self.device_plan if overlap_decode is None
+                               else bool(overlap_decode))
         self.n_work = 0
         self.n_dec = 0
         self._meta = None
@@ -285,7 +377,16 @@ class SlotAttentionCall:
         self._status = None
         if n_tok == 0:
             return
-        if self.device_plan:
+        if step_plan is not None:
+            if (step_plan.batch_size, step_plan.n_q, step_plan.n_kv) != (bsz, n_q, n_kv) \
+                    or step_plan.device != q.device:
+                raise ValueError("step_plan was made for another batch layout or device")
+            self.n_work, self.n_dec = step_plan.n_work, step_plan.n_dec
+            self._ext_t = step_plan.ext_t
+            self._meta = step_plan.meta
+            self._items, self._rows, self._status = (step_plan.items, step_plan.rows,
+                                                     step_plan.status)
+        elif self.device_plan:
             # Lists built on the device at every run() from extend_lens_tensor,
             # padded to capacities fixed by T and B (graph-capturable step).
             ext_t = batch.extend_lens_tensor
@@ -340,7 +441,12 @@ class SlotAttentionCall:
 
     # -- launches
     def run_plan(self) -> None:
-        """Device-side planning (device_plan=True): the work and decode lists."""
+        """Device-side planning (device_plan=True): the work and decode lists
+        (with a shared step plan: only if no earlier call of the step planned)."""
+        if self._shared_plan is not None:
+            if self.n_work:
+                self._shared_plan.ensure(self.stream)
+            return
         if self.device_plan and self.n_work:
             base = self._meta.data_ptr()
             _native.call("tf_attn_plan_device", self._ext_t.data_ptr(), self.batch.batch_size,
@@ -423,6 +529,12 @@ def slot_based_attention(
 ) -> torch.Tensor:
     """Attention of ``q [T, Hq, D]`` over one layer's slot pool; returns ``[T, Hq, D]``.
 
+    A step with extend work is planned once: the first call made with a
+    ``ForwardBatch`` plans its work lists on the device and keeps them on the
+    batch (``StepPlan``); the calls of the step's other layers reuse them.  On
+    a mixed step the decode launches run on a second stream beside the extend
+    kernel (identical results).
+
     ``scaling`` defaults to ``head_dim ** -0.5`` (``full_attention.py:40``).
     ``k_scale`` / ``v_scale`` (fp32 device scalars) are required for a
     ``float8_e4m3fn`` pool. ``decode_workgroups`` overrides the size of the
@@ -432,11 +544,25 @@ def slot_based_attention(
     kernels' output write with the same bf16 roundings. ``out_amax``: see
     ``SlotAttentionCall``.
     """
+    plan = None
+    if q.is_cuda and q.dim() == 3 and q.shape[0] and layer_k_buffer.dim() == 3 \
+            and _plannable(batch, q.device):
+        plan = step_plan(batch, q.shape[0], q.shape[1], layer_k_buffer.shape[1], q.device)
     call = SlotAttentionCall(q, layer_k_buffer, layer_v_buffer, batch, scaling=scaling,
                              k_scale=k_scale, v_scale=v_scale,
                              decode_workgroups=decode_workgroups, out=out, gate=gate,
-                             out_amax=out_amax)
+                             out_amax=out_amax, step_plan=plan)
     return call.run()
+
+
+def _plannable(batch, device: torch.device) -> bool:
+    """Whether the step has extend work and the batch carries the device copy
+    of its extend lengths (pure decode steps need no plan at all)."""
+    if batch.max_extend_len <= 1 or (batch.batch_size == 1 and int(batch.extend_lens[0]) == 1):
+        return False
+    ext_t = batch.extend_lens_tensor
+    return (ext_t is not None and ext_t.device == device and ext_t.dtype == torch.long
+            and ext_t.numel() == batch.batch_size and ext_t.is_contiguous())
 
 
 def gather_kv(pool: torch.Tensor, req_to_token: torch.Tensor, req_pool_indices: torch.Tensor,
