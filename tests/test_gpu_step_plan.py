@@ -98,3 +98,37 @@ def test_pure_decode_steps_plan_nothing(gpu, monkeypatch):
     torch.cuda.synchronize()
     assert "tf_attn_plan_device" not in launched and "tf_attn_extend" not in launched
     assert torch.equal(out, want)
+
+
+def test_captured_layer_call_replays_beside_eager_calls(gpu):
+    """A layer call captured in a HIP graph plans inside the graph: every replay
+    equals the host-planned step, and eager calls with the same batch between
+    the replays (which share the batch's step plan) do too."""
+    wl = CASES["mixed"](gpu)
+    want = host_planned(wl)
+
+    def layer():
+        return slot_based_attention(wl.q, wl.k_pool, wl.v_pool, wl.batch, scaling=wl.scale)
+
+    first = layer().clone()
+    side = torch.cuda.Stream(device=gpu)
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        layer()                                       # warm-up outside the capture
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        captured = layer()
+    torch.cuda.synchronize()
+    assert torch.equal(first, want)
+    for r in range(3):
+        print(f"[step plan] replay {r}", flush=True)
+        captured.zero_()
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(captured, want), f"replay {r}"
+        eager = layer()
+        torch.cuda.synchronize()
+        assert torch.equal(eager, want), f"eager call after replay {r}"

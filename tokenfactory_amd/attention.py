@@ -531,9 +531,10 @@ def slot_based_attention(
 
     A step with extend work is planned once: the first call made with a
     ``ForwardBatch`` plans its work lists on the device and keeps them on the
-    batch (``StepPlan``); the calls of the step's other layers reuse them.  On
-    a mixed step the decode launches run on a second stream beside the extend
-    kernel (identical results).
+    batch (``StepPlan``); the calls of the step's other layers reuse them.  A
+    call under graph capture plans inside the graph instead.  On a mixed step
+    the decode launches run on a second stream beside the extend kernel
+    (identical results).
 
     ``scaling`` defaults to ``head_dim ** -0.5`` (``full_attention.py:40``).
     ``k_scale`` / ``v_scale`` (fp32 device scalars) are required for a
@@ -544,14 +545,19 @@ def slot_based_attention(
     kernels' output write with the same bf16 roundings. ``out_amax``: see
     ``SlotAttentionCall``.
     """
-    plan = None
+    plan, device_plan = None, False
     if q.is_cuda and q.dim() == 3 and q.shape[0] and layer_k_buffer.dim() == 3 \
             and _plannable(batch, q.device):
-        plan = step_plan(batch, q.shape[0], q.shape[1], layer_k_buffer.shape[1], q.device)
+        if torch.cuda.is_current_stream_capturing():
+            # A captured call plans inside the graph (its plan runs at every
+            # replay) and shares nothing with eager calls of the batch.
+            device_plan = True
+        else:
+            plan = step_plan(batch, q.shape[0], q.shape[1], layer_k_buffer.shape[1], q.device)
     call = SlotAttentionCall(q, layer_k_buffer, layer_v_buffer, batch, scaling=scaling,
                              k_scale=k_scale, v_scale=v_scale,
                              decode_workgroups=decode_workgroups, out=out, gate=gate,
-                             out_amax=out_amax, step_plan=plan)
+                             out_amax=out_amax, step_plan=plan, device_plan=device_plan)
     return call.run()
 
 
