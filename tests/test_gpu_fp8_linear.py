@@ -121,8 +121,17 @@ def test_gemm_oproj_shape(gpu, m):
 
 @pytest.mark.parametrize("m,n", [(1025, 640), (1500, 320), (2048, 5120)])
 def test_gemm_large_m(gpu, m, n):
-    # the 8-wave 256 x 256 tiles for large M, ragged in M and in N tiles
+    # the 8-wave tiles for large M (one round of 192-row tiles at these
+    # sizes), ragged in M and in N tiles
     gemm_case(gpu, m, n, 6144 if n < 5120 else 1536, bias=n == 320, seed=m)
+
+
+@pytest.mark.parametrize("bh", [128, 48])
+def test_gemm_256_row_tiles(gpu, bh):
+    # m = 8320 runs the 256 x 256 tiles (33 x 20 tiles, the last m-tile half
+    # full: three rounds of 256-row tiles end before four of 192-row ones),
+    # dealt to the XCDs in groups; bh = 48 gives each column its own scale
+    gemm_case(gpu, 8320, 5120, 256, bh=bh, bias=bh == 48, seed=15 + bh)
 
 
 @pytest.mark.parametrize("k", [128, 256, 384])

@@ -20,12 +20,17 @@
 // block).  A workgroup of 2 x WN waves owns 64 WN output columns x 32 MT rows,
 // a wave holding 64 columns x 16 MT rows (4 x MT 16x16 tiles): 4 waves
 // (128 columns, three K slices in LDS, one wave per SIMD) up to M = 1024,
-// 8 waves (256 x 256, two slices in LDS, two waves per SIMD) above.  Each MFMA starts from zero and its product is folded into the fp32
-// accumulator with that block's scale, acc += p * s, one FMA per accumulator
-// element per 128 of K.  Per 128-wide K slice the workgroup stages the weight
-// tile (64 WN rows), the activation tile (32 MT rows) and the column scales
-// straight from global memory into LDS (global_load_lds_dwordx4 /
-// global_load_lds_dword), STAGES - 1 slices ahead of the MFMAs.
+// 8 waves (256 columns x 256 or 192 rows, two slices in LDS, two waves per
+// SIMD) above.  Each MFMA starts from zero and its product is folded into the
+// fp32 accumulator with that block's scale, acc += p * s, one FMA per
+// accumulator element per 128 of K; a row's folds run between the next row's
+// MFMAs, and each row's operand is read from LDS two rows ahead.  Per
+// 128-wide K slice the workgroup stages the weight tile (64 WN rows), the
+// activation tile (32 MT rows) and the column scales straight from global
+// memory into LDS (global_load_lds_dwordx4 / global_load_lds_dword), STAGES - 1
+// slices ahead of the MFMAs, a few instructions per row of MFMAs.  Tiles are
+// dealt to the XCDs in compact groups (xcd_tile) so that each XCD's L2 serves
+// an X or W slice to several of its workgroups.
 // Rows are 128 bytes; a row's 16-byte chunk c is stored at chunk
 // c ^ swz(row) so the operand reads (16 rows x 16 bytes per 16 lanes) hit 16
 // distinct bank groups.  The transposed product makes each lane own four
@@ -141,6 +146,8 @@ __global__ void __launch_bounds__(kThreads) act_quant_kernel(QuantArgs a) {
 
 // ---------------------------------------------------------------- GEMM
 constexpr int kKSlice = 128;          // K per slice = one weight-scale block
+constexpr int kSpread = 3;            // staging instructions issued per row of MFMAs
+constexpr int kGroupM = 8;            // m-tiles per group of the XCD tile order
 
 // A workgroup of 2 x WN waves owns 32 MT activation rows x 64 WN output
 // columns; wave (wm, wn) holds rows 16 MT wm .. and columns 64 wn .., i.e.
@@ -226,6 +233,26 @@ __device__ __forceinline__ f32x4 mfma_fp8(const i32x8& w, const i32x8& x) {
                                                           0, 0, 0, 0, 0);
 }
 
+// Tile order.  Workgroup b of a grid runs on XCD b % 8 (workgroups are dealt to
+// the 8 XCDs round-robin), and each XCD takes its workgroups in launch order.
+// XCD x gets the contiguous range [x T / 8, (x + 1) T / 8) (rounded) of a
+// grouped order in which gm_max consecutive m-tiles share each n-tile, so the
+// workgroups one XCD runs at once cover a compact block of tiles (8 m-tiles x
+// 4 n-tiles for 32 CUs) whose X and W slices its L2 serves once to all of
+// them.  Under split-K (grid = splits x T) the same permutation is applied to
+// each split's tiles.
+__device__ __forceinline__ void xcd_tile(int b, int tiles, int tiles_m, int gm_max, int* tm,
+                                         int* tn) {
+  const int x = b & 7, i = b >> 3, q = tiles >> 3, r = tiles & 7;
+  const int lin = x * q + min(x, r) + i;
+  const int tiles_n = tiles / tiles_m;
+  const int group = gm_max * tiles_n;
+  const int gid = lin / group, in = lin - gid * group;
+  const int gm = min(tiles_m - gid * gm_max, gm_max);
+  *tm = gid * gm_max + in % gm;
+  *tn = in / gm;
+}
+
 // kUni: block_h is a multiple of 64, so the 64 columns of a wave share one
 // weight-scale row and the slice's scale is one value per wave.
 template <int MT, int WN, int STAGES, bool kUni>
@@ -233,11 +260,14 @@ __global__ void __launch_bounds__(2 * kWave * WN)
 fp8_gemm_kernel(GemmArgs a) {
   using T = Tile<MT, WN, STAGES>;
   __shared__ __attribute__((aligned(16))) uint8_t smem[STAGES * T::kStage];
+  constexpr int kXAhead = kUni ? 2 : 1;   // rows between an operand's read and its use
   const int t = threadIdx.x, w = wave_id(), l = t & 63;
   const int wm = w / WN, wn = w % WN;
-  const int tile = blockIdx.x % a.tiles, split = blockIdx.x / a.tiles;
-  const int m0 = (tile % a.tiles_m) * T::kBM;
-  const int n0 = (tile / a.tiles_m) * T::kBN;
+  const int split = blockIdx.x / a.tiles;
+  int tm_i, tn_i;
+  xcd_tile(blockIdx.x % a.tiles, a.tiles, a.tiles_m, kGroupM, &tm_i, &tn_i);
+  const int m0 = tm_i * T::kBM;
+  const int n0 = tn_i * T::kBN;
   // This workgroup's K slices [kb0, kb0 + KB) (all of them without split-K).
   const int kb0 = (int)((int64_t)a.KB * split / a.splits);
   const int KB = (int)((int64_t)a.KB * (split + 1) / a.splits) - kb0;
@@ -267,17 +297,23 @@ fp8_gemm_kernel(GemmArgs a) {
   const uint32_t so = ones ? 0u : (uint32_t)((scol / a.bh) * a.sn) * 4u;
   const uint32_t lds0 = lds_addr(smem);
 
-  auto issue = [&](int kb, int st) {
+  // Staging instruction idx of K slice kb into stage st: the X rows
+  // (idx < kXInst), the W rows, then the column scales.
+  auto issue_one = [&](int kb, int st, int idx) {
     const uint32_t sb = lds0 + st * T::kStage + w * 1024;
-    const uint8_t* xb = a.xq + (int64_t)kb * kKSlice;
-    const uint8_t* wb = a.w + (int64_t)kb * kKSlice;
+    if (idx < T::kXInst) {
+      dma16(a.xq + (int64_t)kb * kKSlice, xo[idx], sb + idx * 16 * T::kThreads);
+    } else if (idx < T::kXInst + T::kWInst) {
+      const int i = idx - T::kXInst;
+      dma16(a.w + (int64_t)kb * kKSlice, wo[i], sb + T::kXBytes + i * 16 * T::kThreads);
+    } else {
+      const float* sbase = ones ? a.x_scale : a.wsc + (int64_t)(kb / a.bw_slices) * a.sk;
+      dma4(sbase, so, lds0 + st * T::kStage + T::kXBytes + T::kWBytes + w * 256);
+    }
+  };
+  auto issue = [&](int kb, int st) {
 #pragma unroll
-    for (int i = 0; i < T::kXInst; ++i) dma16(xb, xo[i], sb + i * 16 * T::kThreads);
-#pragma unroll
-    for (int i = 0; i < T::kWInst; ++i)
-      dma16(wb, wo[i], sb + T::kXBytes + i * 16 * T::kThreads);
-    const float* sbase = ones ? a.x_scale : a.wsc + (int64_t)(kb / a.bw_slices) * a.sk;
-    dma4(sbase, so, lds0 + st * T::kStage + T::kXBytes + T::kWBytes + w * 256);
+    for (int idx = 0; idx < T::kLoads; ++idx) issue_one(kb, st, idx);
   };
 
   // Fragment reads: row l % 16 of a 16-row tile, chunks 2g and 2g + 1.
@@ -303,9 +339,15 @@ fp8_gemm_kernel(GemmArgs a) {
     vm_wait<0>();
   __syncthreads();
 
+  // With one scale per wave, the last row's products of a slice are folded in
+  // during the next slice's first row (pl, with that slice's scale in sl);
+  // with per-column scales (16 more VGPRs) at the end of the slice.
+  f32x4 pl[4], sl[4];
+#pragma unroll
+  for (int tn = 0; tn < 4; ++tn) pl[tn] = sl[tn] = f32x4{0.f, 0.f, 0.f, 0.f};
   int st = 0;
   for (int j = 0; j < KB; ++j) {
-    issue(kb0 + min(j + T::kAhead, KB - 1), st == 0 ? STAGES - 1 : st - 1);
+    const int knext = kb0 + min(j + T::kAhead, KB - 1), stn = st == 0 ? STAGES - 1 : st - 1;
     const uint8_t* sp = smem + st * T::kStage;
     const uint8_t* ssp = sp + T::kXBytes + T::kWBytes;
     f32x4 s4[4];
@@ -318,23 +360,56 @@ fp8_gemm_kernel(GemmArgs a) {
       for (int tn = 0; tn < 4; ++tn)
         s4[tn] = sfac * *reinterpret_cast<const f32x4*>(ssp + 4 * (scol4 + 16 * tn));
     }
-    i32x8 wf[4];
+    i32x8 wf[4], xf[3];
 #pragma unroll
     for (int tn = 0; tn < 4; ++tn)
       wf[tn] = frag(sp + T::kXBytes + (wrow + 16 * tn) * kKSlice, o0, o1);
-    // Row tm's products are folded in while row tm + 1's MFMAs run.
-    f32x4 p[MT][4];
+    xf[0] = frag(sp + xrow * kKSlice, o0, o1);
+    if constexpr (MT > 1 && kXAhead == 2) xf[1] = frag(sp + (xrow + 16) * kKSlice, o0, o1);
+    // Per row tm: up to kSpread staging instructions of slice j + kAhead (the
+    // stage they fill was released by the previous step's barrier), the read
+    // of row tm + kXAhead's operand, then row tm's four MFMAs, each followed
+    // by four FMAs folding row tm - 1's products.  The scheduling barriers
+    // keep that order: each MFMA's operand was read kXAhead rows earlier and
+    // each product is folded four MFMAs after its own.  (Per-column scales
+    // hold 16 more VGPRs per lane, so that variant reads one row ahead.)
+    f32x4 p[2][4];
 #pragma unroll
     for (int tm = 0; tm < MT; ++tm) {
-      const i32x8 xf = frag(sp + (xrow + 16 * tm) * kKSlice, o0, o1);
+#pragma unroll
+      for (int q = 0; q < kSpread; ++q)
+        if (tm * kSpread + q < T::kLoads) issue_one(knext, stn, tm * kSpread + q);
+      if (tm == MT - 1)
+#pragma unroll
+        for (int idx = MT * kSpread; idx < T::kLoads; ++idx) issue_one(knext, stn, idx);
+      if (tm + kXAhead < MT)
+        xf[(tm + kXAhead) % 3] = frag(sp + (xrow + 16 * (tm + kXAhead)) * kKSlice, o0, o1);
+      __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int tn = 0; tn < 4; ++tn) {
-        p[tm][tn] = mfma_fp8(wf[tn], xf);
-        if (tm > 0) acc[tm - 1][tn] += p[tm - 1][tn] * s4[tn];
+        p[tm & 1][tn] = mfma_fp8(wf[tn], xf[tm % 3]);
+        if (tm > 0)
+          acc[tm - 1][tn] += p[(tm - 1) & 1][tn] * s4[tn];
+        else if constexpr (kUni)
+          acc[MT - 1][tn] += pl[tn] * sl[tn];
       }
+      if (tm + kXAhead < MT) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);   // 2 LDS reads
+#pragma unroll
+      for (int tn = 0; tn < 4; ++tn) {
+        __builtin_amdgcn_sched_group_barrier(0x8, 1, 0);   // 1 MFMA
+        __builtin_amdgcn_sched_group_barrier(0x2, 4, 0);   // 4 VALU
+      }
+      __builtin_amdgcn_sched_barrier(0);
     }
 #pragma unroll
-    for (int tn = 0; tn < 4; ++tn) acc[MT - 1][tn] += p[MT - 1][tn] * s4[tn];
+    for (int tn = 0; tn < 4; ++tn) {
+      if constexpr (kUni) {
+        pl[tn] = p[(MT - 1) & 1][tn];
+        sl[tn] = s4[tn];
+      } else {
+        acc[MT - 1][tn] += p[(MT - 1) & 1][tn] * s4[tn];
+      }
+    }
     if constexpr (T::kAhead == 2)
       vm_wait<T::kLoads>();
     else
@@ -343,6 +418,10 @@ fp8_gemm_kernel(GemmArgs a) {
     st = st == STAGES - 1 ? 0 : st + 1;
   }
   vm_wait<0>();   // the refills of the last steps land before the workgroup ends
+  if constexpr (kUni) {
+#pragma unroll
+    for (int tn = 0; tn < 4; ++tn) acc[MT - 1][tn] += pl[tn] * sl[tn];
+  }
 
   // Epilogue: lane holds D[n0 + wn 64 + 16 tn + 4 g + r][m0 + wm 16 MT + 16 tm + rr].
   if (a.part) {   // split-K: fp32 partials, bias and rounding in splitk_reduce_kernel
@@ -412,12 +491,19 @@ __global__ void __launch_bounds__(kThreads) splitk_reduce_kernel(GemmArgs a) {
 struct Shape {
   int mt, wn;
 };
-Shape gemm_shape(int64_t m) {
+Shape gemm_shape(int64_t m, int64_t n) {
   if (m <= 32) return {1, 2};
   if (m <= 64) return {2, 2};
   if (m <= 128) return {4, 2};
   if (m <= 1024) return {8, 2};
-  return {8, 4};   // 8 waves, 256 x 256 tiles, 2 waves per SIMD
+  // 8 waves, 256 columns, 2 waves per SIMD: 256 or 192 rows, whichever ends
+  // sooner when the tiles run in rounds of one per CU; a 192-row tile takes
+  // 0.8 of a 256-row one (measured at m = 4096, 8320, 21938: 192 rows win at
+  // 4096, 256 at the other two).
+  const int64_t cus = device_cu_count(), tn = (n + 255) / 256;
+  const int64_t r256 = ((m + 255) / 256 * tn + cus - 1) / cus;
+  const int64_t r192 = ((m + 191) / 192 * tn + cus - 1) / cus;
+  return 5 * r256 <= 4 * r192 ? Shape{8, 4} : Shape{6, 4};
 }
 
 // Split-K factor: when the output tiles alone leave most CUs idle (M up to 512,
@@ -425,7 +511,7 @@ Shape gemm_shape(int64_t m) {
 // device's CUs (256 on MI355X) in one round (320 workgroups, one and a quarter
 // rounds, took 1.4 times as long at M = 64).
 int gemm_splits(int64_t m, int64_t n, int64_t k) {
-  const Shape sh = gemm_shape(m);
+  const Shape sh = gemm_shape(m, n);
   if (m > 512 || n % 4) return 1;
   const int64_t cus = device_cu_count();
   const int64_t tiles = ((m + 32 * sh.mt - 1) / (32 * sh.mt)) * ((n + 64 * sh.wn - 1) / (64 * sh.wn));
@@ -598,7 +684,7 @@ int32_t tf_fp8_block_gemm(const void* xq, int64_t xq_row_stride, const float* x_
     a.part = static_cast<float*>(workspace);
   }
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-  const Shape sh = gemm_shape(m);
+  const Shape sh = gemm_shape(m, n);
   if (sh.mt == 1)
     launch_gemm<1, 2, 3>(a, s);
   else if (sh.mt == 2)
@@ -607,6 +693,8 @@ int32_t tf_fp8_block_gemm(const void* xq, int64_t xq_row_stride, const float* x_
     launch_gemm<4, 2, 3>(a, s);
   else if (sh.wn == 2)
     launch_gemm<8, 2, 3>(a, s);
+  else if (sh.mt == 6)
+    launch_gemm<6, 4, 2>(a, s);
   else
     launch_gemm<8, 4, 2>(a, s);
   return launch_status("tf_fp8_block_gemm launch");
