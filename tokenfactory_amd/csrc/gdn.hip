@@ -685,19 +685,27 @@ __global__ void __launch_bounds__(kChunkThreads) gdn_chunk_ext_kernel(GdnArgs a)
       // row 32 ti + 16 hh + 8 (jj / 4) + 4 g + jj % 4)
       // (two accumulators each for P and R, one per half of the state rows:
       // four independent MFMA chains)
+      // (step (ti, hh) + 1's operands are read from LDS while step (ti, hh)'s
+      // MFMAs run)
       f32x16 Pp[2] = {{}, {}}, Rp[2] = {{}, {}};
+      u32x4 op[2][4];
+      auto read_ops = [&](int step, u32x4 (&o)[4]) __attribute__((always_inline)) {
+        const int d0 = 32 * (step >> 1) + 16 * (step & 1) + 4 * g;
+        row8(I.k, n, d0, o[0], o[1]);
+        row8(I.q, n, d0, o[2], o[3]);
+      };
+      read_ops(0, op[0]);
 #pragma unroll
-      for (int ti = 0; ti < 4; ++ti) {
-#pragma unroll
-        for (int hh = 0; hh < 2; ++hh) {
-          u32x4 sh, sl, kh, kl, qh, ql;
-          split16(st[ti], 8 * hh, sh, sl);
-          const int d0 = 32 * ti + 16 * hh + 4 * g;
-          row8(I.k, n, d0, kh, kl);
-          row8(I.q, n, d0, qh, ql);
-          Pp[ti >> 1] = mma3(Pp[ti >> 1], kh, kl, sh, sl);
-          Rp[ti >> 1] = mma3(Rp[ti >> 1], qh, ql, sh, sl);
-        }
+      for (int step = 0; step < 8; ++step) {
+        const int ti = step >> 1, hh = step & 1;
+        if (step + 1 < 8) read_ops(step + 1, op[(step + 1) & 1]);
+        __builtin_amdgcn_sched_barrier(0);
+        u32x4 sh, sl;
+        split16(st[ti], 8 * hh, sh, sl);
+        const u32x4(&o)[4] = op[step & 1];
+        Pp[ti >> 1] = mma3(Pp[ti >> 1], o[0], o[1], sh, sl);
+        Rp[ti >> 1] = mma3(Rp[ti >> 1], o[2], o[3], sh, sl);
+        __builtin_amdgcn_sched_barrier(0);
       }
       const f32x16 P = Pp[0] + Pp[1], R = Rp[0] + Rp[1];
       // X = beta (v - e^gamma P); Delta = T X (k index 8 g + jj <-> token
@@ -751,20 +759,27 @@ __global__ void __launch_bounds__(kChunkThreads) gdn_chunk_ext_kernel(GdnArgs a)
       split16(D, 0, dh[0], dl[0]);
       split16(D, 8, dh[1], dl[1]);
       const float cC = I.rec[kRecC + kChunk - 1];
+      // A operand: K^T row i = 32 ti + n at tokens s(jj) as for Delta (step
+      // (ti, hh) + 1's read while step (ti, hh)'s MFMAs run)
+      u32x4 ka[2][2];
+      auto read_kt = [&](int step, u32x4 (&o)[2]) __attribute__((always_inline)) {
+        const int i = 32 * (step >> 1) + n, s0 = 16 * (step & 1) + 4 * g;
+        const u32x2 h0 = *reinterpret_cast<const u32x2*>(&kt[0][i][s0]);
+        const u32x2 h1 = *reinterpret_cast<const u32x2*>(&kt[0][i][s0 + 8]);
+        const u32x2 l0 = *reinterpret_cast<const u32x2*>(&kt[1][i][s0]);
+        const u32x2 l1 = *reinterpret_cast<const u32x2*>(&kt[1][i][s0 + 8]);
+        o[0] = u32x4{h0[0], h0[1], h1[0], h1[1]};
+        o[1] = u32x4{l0[0], l0[1], l1[0], l1[1]};
+      };
+      read_kt(0, ka[0]);
 #pragma unroll
-      for (int ti = 0; ti < 4; ++ti) {
-        st[ti] *= cC;
-#pragma unroll
-        for (int hh = 0; hh < 2; ++hh) {
-          // A operand: K^T row i = 32 ti + n at tokens s(jj) as for Delta
-          const int i = 32 * ti + n, s0 = 16 * hh + 4 * g;
-          const u32x2 h0 = *reinterpret_cast<const u32x2*>(&kt[0][i][s0]);
-          const u32x2 h1 = *reinterpret_cast<const u32x2*>(&kt[0][i][s0 + 8]);
-          const u32x2 l0 = *reinterpret_cast<const u32x2*>(&kt[1][i][s0]);
-          const u32x2 l1 = *reinterpret_cast<const u32x2*>(&kt[1][i][s0 + 8]);
-          const u32x4 ah = {h0[0], h0[1], h1[0], h1[1]}, al = {l0[0], l0[1], l1[0], l1[1]};
-          st[ti] = mma3(st[ti], ah, al, dh[hh], dl[hh]);
-        }
+      for (int step = 0; step < 8; ++step) {
+        const int ti = step >> 1, hh = step & 1;
+        if (step + 1 < 8) read_kt(step + 1, ka[(step + 1) & 1]);
+        __builtin_amdgcn_sched_barrier(0);
+        if (hh == 0) st[ti] *= cC;
+        st[ti] = mma3(st[ti], ka[step & 1][0], ka[step & 1][1], dh[hh], dl[hh]);
+        __builtin_amdgcn_sched_barrier(0);
       }
     }
     __syncthreads();   // the last chunk's output tile is complete
