@@ -445,9 +445,9 @@ __device__ __forceinline__ void dma16(const void* sbase, uint32_t voff, uint32_t
 // already split (gdn_qk_ext_kernel).  Chunk records are numbered
 // floor(t0_b / 32) + b + ci for chunk ci of request b (first token row t0_b),
 // which is unique and below n_tokens / 32 + B.  Four helper waves of the same
-// workgroup load the chunks, transpose k and apply the gated norm to the
-// output rows (gdn_chunk_ext_kernel), so the state waves' time per chunk is
-// the recurrence's alone.
+// workgroup load the chunks and apply the gated norm to the output rows
+// (gdn_chunk_ext_kernel), so the state waves' time per chunk is the
+// recurrence's alone.
 constexpr int kChunk = 32;
 constexpr int kRec = 2304;     // floats per chunk record: T, Bm, e^gamma, e^(gC - gamma), beta
 constexpr int kRecT = 0, kRecB = 1024, kRecC = 2048, kRecD = 2080, kRecBeta = 2112;
@@ -607,30 +607,20 @@ __device__ __forceinline__ void row8(const uint32_t (*rows)[128], int t, int d0,
   hi = u32x4{h0[0], h0[1], h1[0], h1[1]};
   lo = u32x4{l0[0], l0[1], l1[0], l1[1]};
 }
-// The bf16 high (part 0) or low (part 1) value of dim i of swizzled row t.
-__device__ __forceinline__ uint32_t row_half(const uint32_t (*rows)[128], int t, int i, int part) {
-  const uint16_t* row = reinterpret_cast<const uint16_t*>(rows[t]);
-  return row[128 * part + 8 * ((i >> 3) ^ (t & 15)) + (i & 7)];
-}
-
-constexpr int kKtStride = 40;   // bf16 per row of the transposed k copy (80 B: 8-B reads, few conflicts)
+typedef short i16x4_t __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) i16x4_t lds_i16x4;
 constexpr int kChunkThreads = 2 * kThreads;   // 4 recurrence waves + 4 helper waves
 
 // Waves 0-3 carry the state through the chunks (the MFMA work above, nothing
 // else); waves 4-7, the helpers, share their SIMDs and keep the inputs ahead
-// of them: while the state waves work on chunk ci, the helpers transpose its
-// k (needed only by the state update at the end of the chunk; a workgroup
-// counter in LDS says when it is written), move chunk ci + 1 into LDS and
-// apply the gated norm to the rows of chunk ci - 1.  One barrier per chunk
+// of them: while the state waves work on chunk ci, the helpers move chunk
+// ci + 1 into LDS and apply the gated norm to the rows of chunk ci - 1.  The
+// state update reads k transposed straight from the token-major rows
+// (ds_read_b64_tr_b16).  One barrier per chunk
 // hands the buffers over (chunk inputs and the output tile are
 // double-buffered by chunk parity).
 __global__ void __launch_bounds__(kChunkThreads) gdn_chunk_ext_kernel(GdnArgs a) {
   __shared__ __attribute__((aligned(16))) ChunkIn sm[2];
-  // k of the current chunk transposed, [part][dim][token]: the state update
-  // reads 4 tokens of one dim per 8-byte load.  kt_count: helper waves done
-  // with it so far (4 per chunk).
-  __shared__ __attribute__((aligned(16))) uint16_t kt[2][kDk][kKtStride];
-  __shared__ int kt_count;
   // A chunk's recurrence output (o rounded to bf16), token-major, and the
   // head's norm weights.
   __shared__ __attribute__((aligned(16))) uint16_t otile[2][kChunk][kDv];
@@ -661,7 +651,6 @@ __global__ void __launch_bounds__(kChunkThreads) gdn_chunk_ext_kernel(GdnArgs a)
     reinterpret_cast<f32x4*>(stage)[q] = reinterpret_cast<const f32x4*>(S)[q];
   }
   nw[threadIdx.x & (kDv - 1)] = a.norm_w[h * kDv + (threadIdx.x & (kDv - 1))];   // 4 writers each
-  if (threadIdx.x == 0) kt_count = 0;
   __syncthreads();
 
   if (!helper) {
@@ -694,17 +683,25 @@ __global__ void __launch_bounds__(kChunkThreads) gdn_chunk_ext_kernel(GdnArgs a)
         row8(I.k, n, d0, o[0], o[1]);
         row8(I.q, n, d0, o[2], o[3]);
       };
+      // (and step + 1's state operand is split while step's MFMAs run)
+      u32x4 sh[2], sl[2];
       read_ops(0, op[0]);
+      split16(st[0], 0, sh[0], sl[0]);
 #pragma unroll
       for (int step = 0; step < 8; ++step) {
-        const int ti = step >> 1, hh = step & 1;
+        const int ti = step >> 1;
         if (step + 1 < 8) read_ops(step + 1, op[(step + 1) & 1]);
         __builtin_amdgcn_sched_barrier(0);
-        u32x4 sh, sl;
-        split16(st[ti], 8 * hh, sh, sl);
         const u32x4(&o)[4] = op[step & 1];
-        Pp[ti >> 1] = mma3(Pp[ti >> 1], o[0], o[1], sh, sl);
-        Rp[ti >> 1] = mma3(Rp[ti >> 1], o[2], o[3], sh, sl);
+        Pp[ti >> 1] = mma3(Pp[ti >> 1], o[0], o[1], sh[step & 1], sl[step & 1]);
+        Rp[ti >> 1] = mma3(Rp[ti >> 1], o[2], o[3], sh[step & 1], sl[step & 1]);
+        if (step + 1 < 8)
+          split16(st[(step + 1) >> 1], 8 * ((step + 1) & 1), sh[(step + 1) & 1], sl[(step + 1) & 1]);
+#pragma unroll
+        for (int q = 0; q < 6; ++q) {
+          __builtin_amdgcn_sched_group_barrier(0x8, 1, 0);   // 1 MFMA
+          __builtin_amdgcn_sched_group_barrier(0x2, 4, 0);   // 4 VALU
+        }
         __builtin_amdgcn_sched_barrier(0);
       }
       const f32x16 P = Pp[0] + Pp[1], R = Rp[0] + Rp[1];
@@ -744,30 +741,31 @@ __global__ void __launch_bounds__(kChunkThreads) gdn_chunk_ext_kernel(GdnArgs a)
         const int t = c_row(rr, g);
         otile[ci & 1][t][j] = to_bf(fmaf(I.rec[kRecC + t], R[rr], O[rr]));   // .to(orig_dtype)
       }
-      // S = e^(gamma_C) S0 + K^T (diag(e^(gamma_C - gamma)) Delta), once the
-      // helpers have written kt (a bounded wait: after 2^22 polls the state
-      // waves go on, so a lost count cannot hang the kernel)
-      for (int spin = 0; spin < (1 << 22); ++spin) {
-        if (__hip_atomic_load(&kt_count, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) >=
-            4 * (ci + 1))
-          break;
-        __builtin_amdgcn_s_sleep(1);
-      }
-      asm volatile("" ::: "memory");
+      // S = e^(gamma_C) S0 + K^T (diag(e^(gamma_C - gamma)) Delta)
 #pragma unroll
       for (int rr = 0; rr < 16; ++rr) D[rr] *= I.rec[kRecD + c_row(rr, g)];
       split16(D, 0, dh[0], dl[0]);
       split16(D, 8, dh[1], dl[1]);
       const float cC = I.rec[kRecC + kChunk - 1];
-      // A operand: K^T row i = 32 ti + n at tokens s(jj) as for Delta (step
-      // (ti, hh) + 1's read while step (ti, hh)'s MFMAs run)
+      // A operand: K^T row i = 32 ti + n at tokens s(jj) as for Delta, read
+      // from the token-major k rows with ds_read_b64_tr_b16, which hands lane
+      // i of each 16-lane group element i % 4 of the 8 bytes addressed by lane
+      // 4 k + (i % 16) / 4 as its element k: lane L addresses token
+      // 16 hh + 4 g + (L % 16) / 4 (+ 8), dims 32 ti + 16 ((L / 16) % 2) +
+      // 4 (L % 4) .. + 3 (step (ti, hh) + 1's read while step (ti, hh)'s
+      // MFMAs run)
       u32x4 ka[2][2];
+      const int tq = (lane & 15) >> 2, dq = 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
       auto read_kt = [&](int step, u32x4 (&o)[2]) __attribute__((always_inline)) {
-        const int i = 32 * (step >> 1) + n, s0 = 16 * (step & 1) + 4 * g;
-        const u32x2 h0 = *reinterpret_cast<const u32x2*>(&kt[0][i][s0]);
-        const u32x2 h1 = *reinterpret_cast<const u32x2*>(&kt[0][i][s0 + 8]);
-        const u32x2 l0 = *reinterpret_cast<const u32x2*>(&kt[1][i][s0]);
-        const u32x2 l1 = *reinterpret_cast<const u32x2*>(&kt[1][i][s0 + 8]);
+        const int d = 32 * (step >> 1) + dq, c = d >> 3, e = (d & 7) >> 1;
+        const int t0 = 16 * (step & 1) + 4 * g + tq, t1 = t0 + 8;
+        const uint32_t* a0 = &I.k[t0][4 * (c ^ (t0 & 15)) + e];
+        const uint32_t* a1 = &I.k[t1][4 * (c ^ (t1 & 15)) + e];
+        auto tr = [](const uint32_t* p) __attribute__((always_inline)) {
+          return __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                                               (lds_i16x4*)(const_cast<uint32_t*>(p))));
+        };
+        const u32x2 h0 = tr(a0), h1 = tr(a1), l0 = tr(a0 + 64), l1 = tr(a1 + 64);
         o[0] = u32x4{h0[0], h0[1], h1[0], h1[1]};
         o[1] = u32x4{l0[0], l0[1], l1[0], l1[1]};
       };
@@ -824,20 +822,6 @@ __global__ void __launch_bounds__(kChunkThreads) gdn_chunk_ext_kernel(GdnArgs a)
           dma16(rec_base, rec + 1024u * (3 * w + p) + 16u * lane,
                 lds_addr(&I.rec[256 * (3 * w + p)]));
       }
-    };
-    // Helper thread (part, dim) = (ht / 128, ht % 128) transposes its 32
-    // tokens of chunk ci's k; each helper wave then adds one to kt_count
-    // (its LDS writes complete first).
-    auto transpose = [&](int ci) __attribute__((always_inline)) {
-      const ChunkIn& I = sm[ci & 1];
-      const int i = ht & (kDk - 1), part = ht >> 7;
-#pragma unroll
-      for (int s2 = 0; s2 < kChunk; s2 += 2)
-        *reinterpret_cast<uint32_t*>(&kt[part][i][s2]) =
-            row_half(I.k, s2, i, part) | (row_half(I.k, s2 + 1, i, part) << 16);
-      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-      if (lane == 0)
-        __hip_atomic_fetch_add(&kt_count, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
     };
     // T and Bm of chunk ci (fp32 rows of 32) split in place into the state
     // waves' MFMA operand halves: block b of 16 floats (row n, half hh of T
@@ -922,7 +906,6 @@ __global__ void __launch_bounds__(kChunkThreads) gdn_chunk_ext_kernel(GdnArgs a)
       __syncthreads();   // the state waves start chunk ci and are done with chunk ci - 1
       load_z(ci);
       if (ci + 1 < nchunks) issue(ci + 1);
-      transpose(ci);
       if (ci > 0) norm_rows(ci - 1);
 #pragma unroll
       for (int e = 0; e < 4; ++e) zr[e] = zn[e];
