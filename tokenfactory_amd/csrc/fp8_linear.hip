@@ -148,6 +148,7 @@ __global__ void __launch_bounds__(kThreads) act_quant_kernel(QuantArgs a) {
 constexpr int kKSlice = 128;          // K per slice = one weight-scale block
 constexpr int kSpread = 3;            // staging instructions issued per row of MFMAs
 constexpr int kGroupM = 8;            // m-tiles per group of the XCD tile order
+constexpr int kMaxSplits = 16;        // split-K factor limit
 
 // A workgroup of 2 x WN waves owns 32 MT activation rows x 64 WN output
 // columns; wave (wm, wn) holds rows 16 MT wm .. and columns 64 wn .., i.e.
@@ -468,14 +469,21 @@ fp8_gemm_kernel(GemmArgs a) {
 }
 
 // out = bf16(sum over splits of the fp32 partials (in split order) + bias);
-// one thread per four consecutive columns (N % 4 == 0).
+// one thread per four consecutive columns (N % 4 == 0).  Every partial is
+// loaded before the first add, so the loads' latencies overlap.
 __global__ void __launch_bounds__(kThreads) splitk_reduce_kernel(GemmArgs a) {
   const int64_t e = 4 * ((int64_t)blockIdx.x * kThreads + threadIdx.x);
   const int64_t mn = (int64_t)a.M * a.N;
   if (e >= mn) return;
   const int m = (int)(e / a.N), n = (int)(e - (int64_t)m * a.N);
-  f32x4 v = *reinterpret_cast<const f32x4*>(a.part + e);
-  for (int sp = 1; sp < a.splits; ++sp) v += *reinterpret_cast<const f32x4*>(a.part + sp * mn + e);
+  f32x4 p[kMaxSplits];
+#pragma unroll
+  for (int sp = 0; sp < kMaxSplits; ++sp)
+    if (sp < a.splits) p[sp] = *reinterpret_cast<const f32x4*>(a.part + sp * mn + e);
+  f32x4 v = p[0];
+#pragma unroll
+  for (int sp = 1; sp < kMaxSplits; ++sp)
+    if (sp < a.splits) v += p[sp];
   float b[4] = {0.f, 0.f, 0.f, 0.f};
   if (a.bias) {
 #pragma unroll
@@ -517,7 +525,7 @@ int gemm_splits(int64_t m, int64_t n, int64_t k) {
   const int64_t tiles = ((m + 32 * sh.mt - 1) / (32 * sh.mt)) * ((n + 64 * sh.wn - 1) / (64 * sh.wn));
   const int64_t kb = k / kKSlice;
   if (tiles >= cus / 2 || kb < 4) return 1;
-  return (int)std::max<int64_t>(1, std::min<int64_t>({kb / 2, cus / tiles, 16}));
+  return (int)std::max<int64_t>(1, std::min<int64_t>({kb / 2, cus / tiles, kMaxSplits}));
 }
 
 template <int MT, int WN, int STAGES>
