@@ -134,6 +134,15 @@ def test_gemm_256_row_tiles(gpu, bh):
     gemm_case(gpu, 8320, 5120, 256, bh=bh, bias=bh == 48, seed=15 + bh)
 
 
+@pytest.mark.parametrize("m,n", [(1100, 256), (2000, 768), (1030, 2304)])
+def test_gemm_tile_order_edges(gpu, m, n):
+    # the XCD-grouped tile order (192-row tiles here) with fewer tiles than
+    # XCDs (6 x 1), with a tile count that is not a multiple of 8 and a last
+    # group of m-tiles shorter than the first (11 x 3 = 33: groups of 8 and 3
+    # m-tiles), and with fewer m-tiles than a group holds (6 x 9)
+    gemm_case(gpu, m, n, 256, bias=True, seed=m + n)
+
+
 @pytest.mark.parametrize("k", [128, 256, 384])
 def test_gemm_short_k(gpu, k):
     # one, two and three 128-wide K slices: the staging pipeline's edge cases
