@@ -118,6 +118,17 @@ def _fork_join_events(device: torch.device, main: torch.cuda.Stream):
         return ev
 
 
+_cu_counts: Dict[int, int] = {}
+
+
+def _cu_count(device: torch.device) -> int:
+    idx = device.index if device.index is not None else torch.cuda.current_device()
+    n = _cu_counts.get(idx)
+    if n is None:
+        n = _cu_counts[idx] = torch.cuda.get_device_properties(idx).multi_processor_count
+    return n
+
+
 _side_streams: Dict[int, torch.cuda.Stream] = {}
 
 
@@ -424,6 +435,14 @@ class SlotAttentionCall:
             if self.n_dec:
                 self._items = _DevPtr(base)
                 self._rows = _DevPtr(base + 4 * self.n_dec)
+        if (self.decode_workgroups == 0 and self.n_work and self.n_dec
+                and max(ext_lens) > 1 and min(ext_lens) == 1):
+            # A mixed step's decode kernel runs beside the extend kernel, whose
+            # workgroups hold whole CUs: three times as many, shorter decode
+            # workgroups fill the CUs the extend kernel frees as it drains
+            # (mixed step 1350 -> 1310 us per layer).  The rule depends on the
+            # batch alone, so a serial call gives the same bits.
+            self.decode_workgroups = 3 * _cu_count(q.device)
         self.ws = None
         if self.n_dec:
             nbytes = _native.decode_workspace_bytes(self.n_dec, n_q, n_kv, head_dim,
@@ -539,7 +558,8 @@ def slot_based_attention(
     ``scaling`` defaults to ``head_dim ** -0.5`` (``full_attention.py:40``).
     ``k_scale`` / ``v_scale`` (fp32 device scalars) are required for a
     ``float8_e4m3fn`` pool. ``decode_workgroups`` overrides the size of the
-    decode kernel's persistent grid (0 = one workgroup per compute unit).
+    decode kernel's persistent grid (0 = one workgroup per compute unit, three
+    per compute unit on a step that mixes extends and decodes).
     ``gate`` (bf16 ``[T, Hq, D]``, any view with contiguous dims): the result is
     ``attn * F.silu(gate)`` (``full_attention.py:157-159``), computed in the
     kernels' output write with the same bf16 roundings. ``out_amax``: see
