@@ -132,3 +132,27 @@ def test_captured_layer_call_replays_beside_eager_calls(gpu):
         eager = layer()
         torch.cuda.synchronize()
         assert torch.equal(eager, want), f"eager call after replay {r}"
+
+
+def test_mixed_steps_use_three_decode_workgroups_per_cu(gpu):
+    """A step with extends and decodes runs its decode kernel on three
+    workgroups per CU (they fill the CUs the extend kernel frees); serial and
+    overlapped calls use the same grid and give the same bits, and an explicit
+    ``decode_workgroups`` or a pure decode step keeps its own grid."""
+    cus = torch.cuda.get_device_properties(gpu).multi_processor_count
+    wl = CASES["mixed"](gpu)
+    ser = SlotAttentionCall(wl.q, wl.k_pool, wl.v_pool, wl.batch, scaling=wl.scale,
+                            overlap_decode=False)
+    ovl = SlotAttentionCall(wl.q, wl.k_pool, wl.v_pool, wl.batch, scaling=wl.scale,
+                            overlap_decode=True)
+    own = SlotAttentionCall(wl.q, wl.k_pool, wl.v_pool, wl.batch, scaling=wl.scale,
+                            decode_workgroups=cus)
+    assert ser.decode_workgroups == ovl.decode_workgroups == 3 * cus
+    assert own.decode_workgroups == cus
+    a, b = ser.run().clone(), ovl.run().clone()
+    torch.cuda.synchronize()
+    assert torch.equal(a, b)
+    dec = small_case([300, 2000, 47, 9], [1] * 4, hq=24, hkv=4, d=256, seed=10, device=gpu,
+                     dtype=torch.bfloat16)
+    call = SlotAttentionCall(dec.q, dec.k_pool, dec.v_pool, dec.batch, scaling=dec.scale)
+    assert call.decode_workgroups == 0
