@@ -82,7 +82,10 @@ const char* tf_attn_last_error(void);
  * The streaming kernel runs a persistent grid of num_workgroups workgroups
  * (0 = one per compute unit) that split the (request, kv head, 16-token tile)
  * work evenly, whatever the length mix; a request's kv head that spans several
- * workgroups leaves fp32 partials that the merge phase combines.
+ * workgroups leaves fp32 partials that the merge phase combines.  Beside an
+ * extend launch on another stream, three per compute unit fill the CUs the
+ * extend kernel frees sooner (the Python side's choice for mixed steps).  The
+ * grid fixes where partials are cut, so results depend on it in the last bits.
  * At most 2048 requests per call.
  * workspace: device scratch of tf_attn_decode_workspace_bytes(...) bytes (no
  * initialisation needed) holding the partials between the two phases.  Calls
