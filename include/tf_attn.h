@@ -426,7 +426,7 @@ int64_t tf_fp8_block_gemm_workspace_bytes(int64_t m, int64_t n, int64_t k);
  * gated RMSNorm (:325, rms_norm_gated.py:26-40); out_proj is left to the caller.
  *
  * Request b reads state slot r = req_indices[b] (requests with r outside
- * [0, n_slots) are skipped and their output rows left untouched):
+ * [0, n_slots) leave every state untouched and get zero out / core_out rows):
  *   conv: y = bf16(silu(bf16(sum_i conv_weight[c][i] * [conv_state[r][c][0..2], qkv[b][c]][i])))
  *         conv_state[r][c] <- [conv_state[r][c][1..2], qkv[b][c]]
  *   q, k, v = split(y, [Hk*Dk, Hk*Dk, Hv*Dv]); q = normalize(q) / sqrt(Dk);
@@ -440,9 +440,10 @@ int64_t tf_fp8_block_gemm_workspace_bytes(int64_t m, int64_t n, int64_t k);
  * conv_state: bf16 [slots, conv_dim, 3]; ssm_state: fp32 [slots, Hv, Dk, Dv]
  * (16-byte aligned), both updated in place, slot strides in elements;
  * out (and the optional core_out, the pre-norm o): bf16 [B, Hv*Dv].
- * workspace: device scratch of tf_gdn_decode_workspace_bytes(B, Hk, Hv) bytes
- * (the bf16 conv outputs between the two launches; no initialisation needed;
- * sized for Dk = Dv = 128, enough for every supported head dim).
+ * workspace: 16-byte aligned device scratch of tf_gdn_decode_workspace_bytes(B, Hk,
+ * Hv) bytes (the bf16 conv outputs and the fp32 gates between the two
+ * launches; no initialisation needed; sized for Dk = Dv = 128, enough for
+ * every supported head dim).
  * Dk = head_k_dim, Dv = head_v_dim: 128 / 128 (the Qwen3.5 layers, on the
  * MFMA-tiled kernels), or each a multiple of 4 up to 64 (the small test
  * models, e.g. 16 / 16, on one wave per (request, value head) with the state

@@ -93,6 +93,44 @@ def test_decode_steps_match_oracle(gpu, bsz, hk, hv):
         print(f"[gdn] {what}: max |dS| {float((ss - ssm_state).abs().max()):.2e}", flush=True)
 
 
+def test_decode_misaligned_rows_match_oracle(gpu):
+    """qkv rows and conv-state slots at odd element offsets: the conv runs per
+    channel where a row or slot is not 8-byte aligned, four channels at a time
+    where it is; both agree with the oracle bit for bit on the conv state."""
+    bsz, hk, hv, n_slots = 6, 4, 12, 9
+    conv_dim = 2 * hk * 128 + hv * 128
+    g = torch.Generator().manual_seed(29)
+    conv_state = torch.randn((n_slots, conv_dim, 3), generator=g).to(torch.bfloat16)
+    ssm_state = torch.randn((n_slots, hv, 128, 128), generator=g) * 0.2
+    req = torch.tensor([0, 3, 8, 1, 6, 5], dtype=torch.int64)
+    params = make_params(hk, hv, 31)
+    gp = [p.to(gpu) for p in params]
+    # slot r starts at element 1 + r * (3 conv_dim + 1): the alignment varies by slot
+    cs_big = torch.zeros(1 + n_slots * (3 * conv_dim + 1), dtype=torch.bfloat16, device=gpu)
+    cs_gpu = cs_big.as_strided((n_slots, conv_dim, 3), (3 * conv_dim + 1, 3, 1), 1)
+    cs_gpu.copy_(conv_state.to(gpu))
+    ss_gpu = ssm_state.to(gpu)
+    for step in range(2):
+        qkv, a, b, z = make_step(bsz, hk, hv, 77 + step)
+        qkv_big = torch.zeros((bsz, conv_dim + 3), dtype=torch.bfloat16)
+        qkv_big[:, 1:1 + conv_dim] = qkv
+        qkv_view = qkv_big.to(gpu)[:, 1:1 + conv_dim]     # row bi at element 1 + bi (conv_dim + 3)
+        out, core = gdn_decode_step(qkv_view, b.to(gpu), a.to(gpu), z.to(gpu), *gp, 1e-6,
+                                    cs_gpu, ss_gpu, req.to(gpu), hk, hv, return_core=True)
+        want_out, want_core = og.gdn_decode(qkv, a, b, z, *params, 1e-6, conv_state, ssm_state,
+                                            req, hk, hv)
+        torch.cuda.synchronize()
+        what = f"misaligned step {step}"
+        assert torch.equal(cs_gpu.cpu(), conv_state), f"{what}: conv state"
+        pads = cs_big[0::3 * conv_dim + 1].float()   # before slot 0 and after every slot
+        assert pads.numel() == n_slots + 1 and (pads == 0).all(), f"{what}: padding written"
+        scale = float(ssm_state.abs().max())
+        close_fraction(ss_gpu.cpu(), ssm_state, 1e-5 * scale, 1e-2 * scale, 1e-3,
+                       f"{what}: ssm state")
+        check_outputs(core.cpu(), want_core, f"{what}: pre-norm output")
+        check_outputs(out.cpu(), want_out, f"{what}: normed output")
+
+
 @pytest.mark.parametrize("lens,hk,hv", [([5], 16, 48), ([1, 70, 3, 130], 16, 48),
                                          ([200, 1, 1, 64, 2], 4, 12),
                                          # 32-token chunk edges: exact, one over, one short

@@ -15,11 +15,13 @@
 // The recurrent state S[slot][h] is a 128 x 128 fp32 matrix (key rows, value
 // columns) updated in place; the conv state is bf16 [slot][channel][3].
 //
-// Two launches.  gdn_conv_kernel: one thread per (request, channel) runs the
-// conv step, writes the bf16 SiLU output to a workspace row and shifts the conv
-// state.  gdn_recur_kernel: one 256-thread workgroup per (request, value head)
-// normalises its q / k from the workspace, streams the head's 64 KB state
-// through registers once (thread t holds columns 4 (t % 32) .. + 3 of rows
+// Two launches.  gdn_conv_kernel: one thread per (request, 4 channels) runs the
+// conv step, writes the bf16 SiLU outputs to a workspace row and shifts the
+// conv state; the first Hv threads of a request also form the value heads'
+// gates (log alpha, beta) into the workspace.  gdn_recur_kernel: one 256-thread
+// workgroup per (request, value head) normalises its q / k from the workspace,
+// streams the head's 64 KB state through registers once with nontemporal
+// loads and stores (thread t holds columns 4 (t % 32) .. + 3 of rows
 // t / 32 + 8 i), reduces S^T k and S^T q over the rows through LDS and applies
 // the gated norm to the whole head.  HBM-bound: 128 KB of state traffic per
 // value head and request.
@@ -74,6 +76,8 @@ struct GdnArgs {
   int64_t core_rs;
 };
 
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+
 __device__ __forceinline__ float bf(uint16_t u) { return __uint_as_float((uint32_t)u << 16); }
 __device__ __forceinline__ uint16_t to_bf(float x) {
   return (uint16_t)(pack_bf16(x, 0.f) & 0xffffu);
@@ -92,22 +96,80 @@ __device__ __forceinline__ float sum128(float v, float* red) {
   return s;
 }
 
+// Four channels c .. c + 3 of one request per thread (conv_dim is a multiple
+// of 4): 8-byte accesses to the conv state, qkv and the workspace when all
+// three are 8-byte aligned, per channel otherwise; the arithmetic is the same.
+__device__ __forceinline__ float conv_tap4(const f32x4& w, uint16_t x0, uint16_t x1,
+                                           uint16_t x2, uint16_t x3) {
+  const float acc = w[0] * bf(x0) + w[1] * bf(x1) + w[2] * bf(x2) + w[3] * bf(x3);
+  const float y = round_bf(acc);                               // conv1d output (bf16)
+  return y / (1.f + expf(-y));                                 // F.silu
+}
+
 __global__ void __launch_bounds__(kThreads) gdn_conv_kernel(GdnArgs a) {
   const int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x;
-  const int bi = (int)(i / a.conv_dim), c = (int)(i - (int64_t)bi * a.conv_dim);
+  const int per_req = a.conv_dim >> 2;
+  const int bi = (int)(i / per_req), c = 4 * (int)(i - (int64_t)bi * per_req);
   if (bi >= a.batch) return;
   const int64_t r = a.req[bi];
   if (r < 0 || r >= a.n_slots) return;
+  if (c / 4 < a.hv) {
+    // the gates of value head h = c / 4 for the recurrence: g = log alpha, beta
+    const int h = c / 4;
+    const float xa = bf(a.a[bi * a.ab_rs + h]) + a.dt_bias[h];
+    const float sp = xa > 20.f ? xa : log1pf(expf(xa));        // F.softplus
+    *reinterpret_cast<f32x2*>(a.wg + ((int64_t)bi * a.hv + h) * 2) =
+        f32x2{-expf(a.a_log[h]) * sp, 1.f / (1.f + expf(-bf(a.b[bi * a.ab_rs + h])))};
+  }
   uint16_t* st = a.conv_state + r * a.conv_ss + 3 * (int64_t)c;
-  const uint16_t x0 = st[0], x1 = st[1], x2 = st[2];
-  const uint16_t x3 = a.qkv[bi * a.qkv_rs + c];
-  const f32x4 w = *reinterpret_cast<const f32x4*>(a.conv_w + 4 * (int64_t)c);
-  const float acc = w[0] * bf(x0) + w[1] * bf(x1) + w[2] * bf(x2) + w[3] * bf(x3);
-  const float y = round_bf(acc);                               // conv1d output (bf16)
-  a.ws[(int64_t)bi * a.conv_dim + c] = to_bf(y / (1.f + expf(-y)));   // F.silu on bf16
-  st[0] = x1;
-  st[1] = x2;
-  st[2] = x3;
+  const uint16_t* xin = a.qkv + bi * a.qkv_rs + c;
+  uint16_t* yo = a.ws + (int64_t)bi * a.conv_dim + c;
+  f32x4 w[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) w[e] = *reinterpret_cast<const f32x4*>(a.conv_w + 4 * (int64_t)(c + e));
+  if (((reinterpret_cast<uintptr_t>(st) | reinterpret_cast<uintptr_t>(xin) |
+        reinterpret_cast<uintptr_t>(yo)) & 7u) == 0) {
+    // taps of channel e: state elements 3e .. 3e + 2, then qkv element e
+    uint16_t x[16];
+#pragma unroll
+    for (int j = 0; j < 3; ++j) {
+      const u32x2 v = reinterpret_cast<const u32x2*>(st)[j];
+      x[4 * j] = (uint16_t)v[0];
+      x[4 * j + 1] = (uint16_t)(v[0] >> 16);
+      x[4 * j + 2] = (uint16_t)v[1];
+      x[4 * j + 3] = (uint16_t)(v[1] >> 16);
+    }
+    const u32x2 q = *reinterpret_cast<const u32x2*>(xin);
+    x[12] = (uint16_t)q[0];
+    x[13] = (uint16_t)(q[0] >> 16);
+    x[14] = (uint16_t)q[1];
+    x[15] = (uint16_t)(q[1] >> 16);
+    uint16_t yv[4], ns[12];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      yv[e] = to_bf(conv_tap4(w[e], x[3 * e], x[3 * e + 1], x[3 * e + 2], x[12 + e]));
+      ns[3 * e] = x[3 * e + 1];
+      ns[3 * e + 1] = x[3 * e + 2];
+      ns[3 * e + 2] = x[12 + e];
+    }
+    *reinterpret_cast<u32x2*>(yo) =
+        u32x2{yv[0] | ((uint32_t)yv[1] << 16), yv[2] | ((uint32_t)yv[3] << 16)};
+#pragma unroll
+    for (int j = 0; j < 3; ++j)
+      reinterpret_cast<u32x2*>(st)[j] =
+          u32x2{ns[4 * j] | ((uint32_t)ns[4 * j + 1] << 16),
+                ns[4 * j + 2] | ((uint32_t)ns[4 * j + 3] << 16)};
+    return;
+  }
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    uint16_t* se = st + 3 * e;
+    const uint16_t x0 = se[0], x1 = se[1], x2 = se[2], x3 = xin[e];
+    yo[e] = to_bf(conv_tap4(w[e], x0, x1, x2, x3));
+    se[0] = x1;
+    se[1] = x2;
+    se[2] = x3;
+  }
 }
 
 __global__ void __launch_bounds__(kThreads) gdn_recur_kernel(GdnArgs a) {
@@ -138,12 +200,14 @@ __global__ void __launch_bounds__(kThreads) gdn_recur_kernel(GdnArgs a) {
   const uint16_t* y = a.ws + (int64_t)row * a.conv_dim;
 
   // The state loads go out first; q / k normalisation runs under their latency.
+  // The state is read and written once per step, so both go nontemporal.
   const int d0 = 4 * (t & 31), g = t >> 5;
   float* S = a.ssm + r * a.ssm_ss + (int64_t)h * kDk * kDv;
   f32x4 s[16];
 #pragma unroll
   for (int i = 0; i < 16; ++i)
-    s[i] = *reinterpret_cast<const f32x4*>(S + (g + kRowGroups * i) * kDv + d0);
+    s[i] = __builtin_nontemporal_load(
+        reinterpret_cast<const f32x4*>(S + (g + kRowGroups * i) * kDv + d0));
 
   // q = normalize(q) * dk^-0.5, k = normalize(k)  (F.normalize, eps 1e-12)
   {
@@ -162,10 +226,9 @@ __global__ void __launch_bounds__(kThreads) gdn_recur_kernel(GdnArgs a) {
     __syncthreads();
   }
 
-  const float x = bf(a.a[row * a.ab_rs + h]) + a.dt_bias[h];
-  const float sp = x > 20.f ? x : log1pf(expf(x));           // F.softplus
-  const float alpha = expf(-expf(a.a_log[h]) * sp);
-  const float beta = 1.f / (1.f + expf(-bf(a.b[row * a.ab_rs + h])));
+  // gates from the conv kernel (decode) or the q/k kernel (extend)
+  const f32x2 gt = *reinterpret_cast<const f32x2*>(a.wg + ((int64_t)row * a.hv + h) * 2);
+  const float alpha = expf(gt[0]), beta = gt[1];
 
   f32x4 vp = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -191,7 +254,7 @@ __global__ void __launch_bounds__(kThreads) gdn_recur_kernel(GdnArgs a) {
   for (int i = 0; i < 16; ++i) {
     const int k = g + kRowGroups * i;
     s[i] += s_k[k] * delta;
-    *reinterpret_cast<f32x4*>(S + k * kDv + d0) = s[i];
+    __builtin_nontemporal_store(s[i], reinterpret_cast<f32x4*>(S + k * kDv + d0));
     op += s[i] * s_q[k];
   }
   *reinterpret_cast<f32x4*>(&s_red[g][d0]) = op;
@@ -1032,6 +1095,12 @@ __global__ void __launch_bounds__(kThreads) gdn_zero_ext_kernel(GdnArgs a) {
 }
 
 }  // namespace
+
+// Decode workspace: bf16 conv outputs [B, conv_dim], then the fp32 gates
+// (log alpha, beta) [B, Hv, 2].
+inline int64_t gdn_dec_ws_bytes(int64_t batch, int64_t conv_dim, int32_t hv) {
+  return batch * (conv_dim * 2 + (int64_t)hv * 8);
+}
 }  // namespace tfa
 
 extern "C" {
@@ -1042,7 +1111,7 @@ int64_t tf_gdn_decode_workspace_bytes(int32_t batch_size, int32_t num_k_heads,
   if (batch_size < 0 || num_k_heads <= 0 || num_v_heads <= 0)
     return tfa::fail(TF_ERR_INVALID, "gdn_decode_workspace_bytes: bad arguments");
   const int64_t conv_dim = 2LL * num_k_heads * tfa::kDk + (int64_t)num_v_heads * tfa::kDv;
-  return (int64_t)batch_size * conv_dim * 2;
+  return tfa::gdn_dec_ws_bytes(batch_size, conv_dim, num_v_heads);
 }
 
 namespace tfa {
@@ -1237,8 +1306,14 @@ int32_t tf_gdn_decode(const void* qkv, int64_t qkv_row_stride, const void* a, co
       head_k_dim, head_v_dim, conv_kernel, out, out_row_stride, core_out, core_row_stride,
       workspace, workspace_bytes, &g);
   if (rc != TF_OK) return rc;
+  const int64_t need = gdn_dec_ws_bytes(batch_size, g.conv_dim, num_v_heads);
+  if (workspace_bytes < need || (reinterpret_cast<uintptr_t>(workspace) & 15u))
+    return fail(TF_ERR_INVALID, "gdn_decode: workspace of %lld bytes (needs %lld, 16-byte aligned)",
+                (long long)workspace_bytes, (long long)need);
+  g.wg = reinterpret_cast<float*>(static_cast<uint8_t*>(workspace) +
+                                  (int64_t)batch_size * g.conv_dim * 2);
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-  const int64_t n_conv = (int64_t)batch_size * g.conv_dim;
+  const int64_t n_conv = (int64_t)batch_size * (g.conv_dim / 4);   // 4 channels per thread
   hipLaunchKernelGGL(gdn_conv_kernel, dim3((n_conv + kThreads - 1) / kThreads), dim3(kThreads),
                      0, s, g);
   if (g.dk != kDk)

@@ -104,15 +104,16 @@ def gdn_decode_step(qkv: torch.Tensor, b: torch.Tensor, a: torch.Tensor, z: torc
     with on_stream(stream):
         out = torch.empty((bsz, value_dim), dtype=torch.bfloat16, device=qkv.device)
         core = torch.empty_like(out) if return_core else None
-        ws = torch.empty((bsz, 2 * num_k_heads * dk + value_dim), dtype=torch.bfloat16,
-                         device=qkv.device)
+        # bf16 conv outputs [B, conv_dim], then fp32 gates [B, Hv, 2]
+        ws = torch.empty(bsz * ((2 * num_k_heads * dk + value_dim) * 2 + num_v_heads * 8),
+                         dtype=torch.uint8, device=qkv.device)
         _native.call("tf_gdn_decode", _ptr(qkv), _rows(qkv, "qkv"), _ptr(a), _ptr(b),
                      _rows(a, "a"), _ptr(z), _rows(z, "z"), _ptr(conv_weight), _ptr(a_log),
                      _ptr(dt_bias), _ptr(norm_weight), float(eps), _ptr(cs), cs.stride(0),
                      _ptr(ss), ss.stride(0), _ptr(req_indices), bsz, cs.shape[0], num_k_heads,
                      num_v_heads, dk, dv, CONV_KERNEL, _ptr(out), out.stride(0),
                      _ptr(core), 0 if core is None else core.stride(0), _ptr(ws),
-                     ws.numel() * 2, s.cuda_stream)
+                     ws.numel(), s.cuda_stream)
     return (out, core) if return_core else out
 
 
