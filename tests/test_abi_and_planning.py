@@ -59,14 +59,14 @@ def test_gdn_extend_workspace_covers_rows_and_chunk_records():
     # Per token row: conv outputs (bf16), split q / k (4 x 128 bf16 per key
     # head), gates (2 fp32 per value head), the row's request (int32); then
     # one 9 KB record per (32-token chunk slot, value head), with
-    # n_tokens / 32 + batch + 1 slots.
+    # n_tokens / 32 + batch + 1 slots; then the 16 KB SiLU table.
     lib = _native.load()
     hk, hv = 16, 48
     row = (2 * hk * 128 + hv * 128) * 2 + hk * 4 * 128 * 2 + hv * 8 + 4
     for n_tok, bsz in [(1, 1), (8320, 132), (70, 3)]:
         got = lib.tf_gdn_extend_workspace_bytes(n_tok, bsz, hk, hv)
-        assert got >= n_tok * row + (n_tok // 32 + bsz + 1) * hv * 2304 * 4
-        assert got <= n_tok * row + 80 + (n_tok // 32 + bsz + 1) * hv * 2304 * 4
+        assert got >= n_tok * row + (n_tok // 32 + bsz + 1) * hv * 2304 * 4 + 16384
+        assert got <= n_tok * row + 80 + (n_tok // 32 + bsz + 1) * hv * 2304 * 4 + 16384
     assert lib.tf_gdn_extend_workspace_bytes(100, 5, hk, hv) < \
         lib.tf_gdn_extend_workspace_bytes(100, 6, hk, hv)
     assert lib.tf_gdn_extend_workspace_bytes(10, -1, hk, hv) == _native.TF_ERR_INVALID

@@ -27,6 +27,8 @@
 // value head and request.
 #include <math.h>
 
+#include <algorithm>
+
 #include <mutex>
 
 #include "tf_common.h"
@@ -66,6 +68,7 @@ struct GdnArgs {
   uint16_t* wqk;         // extend: bf16 [rows, Hk, 4, 128] normalised q (hi, lo parts) then k
   float* wg;             // extend: fp32 [rows, Hv, 2] g = log alpha, beta
   int32_t* owner;        // extend: int32 [rows] request of each token row (-1: none / skipped)
+  uint16_t* silu_tab;    // extend: bf16 SiLU of the bf16 values 2^-25 <= |y| < 2^7
   float* wrec;           // extend: fp32 [chunk slots, Hv, 2304] chunk records
   const int32_t* tok;    // extend: request b owns token rows tok[b] .. tok[b + 1] - 1
   int32_t rows;          // token rows of qkv / a / b / z / out (offsets are clamped to it)
@@ -291,10 +294,33 @@ __global__ void __launch_bounds__(kThreads) gdn_recur_kernel(GdnArgs a) {
 
 constexpr int kConvTokens = 8;    // tokens per thread in the extend conv
 
+// The conv output y is a bf16 value, so bf16(silu(y)) is a function of 16
+// bits.  The extend conv looks it up for 2^-25 <= |y| < 2^7 (biased exponents
+// kSiluELo .. kSiluELo + 31, both signs: 8192 entries) and computes it for
+// the rest; the table holds what silu_bf16 computes, so both agree bit for bit.
+constexpr int kSiluELo = 102;
+constexpr int kSiluTab = 8192;
+
+__device__ __forceinline__ uint16_t silu_bf16(float y) {
+  return to_bf(y / (1.f + expf(-y)));   // F.silu (accurate exp: q / k / v feed everything)
+}
+__device__ __forceinline__ uint32_t silu_lookup(float y, const uint16_t* tab) {
+  const uint32_t u = __float_as_uint(y) >> 16;   // y's bf16 bits
+  const uint32_t e = ((u >> 7) & 0xffu) - kSiluELo;
+  if (e < 32u) return tab[((u >> 15) << 12) | (e << 7) | (u & 127u)];
+  return silu_bf16(y);
+}
+
 // owner[tt] = the request whose rows hold tt, or -1 when none does or the
 // request's slot is outside the pool (those rows are skipped everywhere).
+// Threads 0 .. kSiluTab - 1 also fill the SiLU table.
 __global__ void __launch_bounds__(kThreads) gdn_owner_kernel(GdnArgs a) {
   const int tt = blockIdx.x * kThreads + threadIdx.x;
+  if (tt < kSiluTab) {
+    const uint32_t u = ((uint32_t)(tt >> 12) << 15) | ((uint32_t)(kSiluELo + ((tt >> 7) & 31)) << 7) |
+                       (uint32_t)(tt & 127);
+    a.silu_tab[tt] = silu_bf16(__uint_as_float(u << 16));
+  }
   if (tt >= a.rows) return;
   int lo = 0, hi = a.batch - 1;
   while (lo < hi) {
@@ -309,75 +335,83 @@ __global__ void __launch_bounds__(kThreads) gdn_owner_kernel(GdnArgs a) {
 constexpr int kConvCh = 4;   // channels per thread in the extend conv
 
 // Conv + SiLU of kConvTokens consecutive token rows for kConvCh channels per
-// thread (grid: channel blocks x token-row blocks of the flattened batch).
+// thread (grid: channel blocks x a stride of kConvTokens-row blocks over the
+// flattened batch; the SiLU table is copied to LDS once per workgroup).
 // Each token's window takes the inputs before its request's first token from
 // the request's conv state, which this kernel only reads;
 // gdn_conv_state_kernel shifts it afterwards.  Rows of requests whose slot is
 // outside the pool are skipped.
+constexpr int kConvRowWgs = 192;   // workgroups per channel block (row-block stride)
+
 __global__ void __launch_bounds__(kThreads) gdn_conv_ext_kernel(GdnArgs a) {
+  __shared__ __attribute__((aligned(16))) uint16_t tab[kSiluTab];
+  for (int i = threadIdx.x; i < kSiluTab / 8; i += kThreads)
+    reinterpret_cast<u32x4*>(tab)[i] = reinterpret_cast<const u32x4*>(a.silu_tab)[i];
+  __syncthreads();
   const int c = kConvCh * (blockIdx.x * kThreads + threadIdx.x);
-  const int tb = blockIdx.y * kConvTokens;
-  if (tb >= a.rows || c >= a.conv_dim) return;
-  u32x2 x[kConvTokens + 3];   // rows tb - 3 .. tb + kConvTokens - 1 (0 outside [0, rows))
-#pragma unroll
-  for (int i = 0; i < kConvTokens + 3; ++i) {
-    const int tt = tb - 3 + i;
-    x[i] = tt >= 0 && tt < a.rows ? *reinterpret_cast<const u32x2*>(a.qkv + tt * a.qkv_rs + c)
-                                  : u32x2{0u, 0u};
-  }
+  if (c >= a.conv_dim) return;
   f32x4 w[kConvCh];
 #pragma unroll
   for (int e = 0; e < kConvCh; ++e)
     w[e] = *reinterpret_cast<const f32x4*>(a.conv_w + 4 * (int64_t)(c + e));
-  // Most row blocks lie inside one in-pool request, at least 3 rows past its
-  // first: then every input is a qkv row (workgroup-uniform test).
-  const int tl = min(tb + kConvTokens, a.rows) - 1;
-  const int ob = a.owner[tb];
-  if (ob >= 0 && a.owner[tl] == ob && tb - 3 >= min(max(a.tok[ob], 0), a.rows)) {
+  for (int tb = blockIdx.y * kConvTokens; tb < a.rows; tb += gridDim.y * kConvTokens) {
+    u32x2 x[kConvTokens + 3];   // rows tb - 3 .. tb + kConvTokens - 1 (0 outside [0, rows))
+#pragma unroll
+    for (int i = 0; i < kConvTokens + 3; ++i) {
+      const int tt = tb - 3 + i;
+      x[i] = tt >= 0 && tt < a.rows ? *reinterpret_cast<const u32x2*>(a.qkv + tt * a.qkv_rs + c)
+                                    : u32x2{0u, 0u};
+    }
+    // Most row blocks lie inside one in-pool request, at least 3 rows past its
+    // first: then every input is a qkv row (workgroup-uniform test).
+    const int tl = min(tb + kConvTokens, a.rows) - 1;
+    const int ob = a.owner[tb];
+    if (ob >= 0 && a.owner[tl] == ob && tb - 3 >= min(max(a.tok[ob], 0), a.rows)) {
+#pragma unroll
+      for (int i = 0; i < kConvTokens; ++i) {
+        if (tb + i > tl) break;
+        uint32_t y[kConvCh];
+#pragma unroll
+        for (int e = 0; e < kConvCh; ++e) {
+          float in[4];
+#pragma unroll
+          for (int k = 0; k < 4; ++k) {
+            const uint32_t pr = x[i + k][e >> 1];
+            in[k] = (e & 1) ? bf16_hi(pr) : bf16_lo(pr);
+          }
+          y[e] = silu_lookup(
+              round_bf(w[e][0] * in[0] + w[e][1] * in[1] + w[e][2] * in[2] + w[e][3] * in[3]), tab);
+        }
+        *reinterpret_cast<u32x2*>(a.ws + (int64_t)(tb + i) * a.conv_dim + c) =
+            u32x2{y[0] | (y[1] << 16), y[2] | (y[3] << 16)};
+      }
+      continue;
+    }
 #pragma unroll
     for (int i = 0; i < kConvTokens; ++i) {
-      if (tb + i > tl) break;
-      float y[kConvCh];
+      const int tt = tb + i;
+      if (tt >= a.rows) break;
+      const int bi = a.owner[tt];
+      if (bi < 0) continue;
+      const int t0 = min(max(a.tok[bi], 0), a.rows);
+      const int64_t r = a.req[bi];
+      const uint16_t* st = a.conv_state + r * a.conv_ss + 3 * (int64_t)c;
+      uint32_t y[kConvCh];
 #pragma unroll
       for (int e = 0; e < kConvCh; ++e) {
         float in[4];
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
+          const int p = tt - 3 + k;   // input position; before t0 it is in the conv state
           const uint32_t pr = x[i + k][e >> 1];
-          in[k] = (e & 1) ? bf16_hi(pr) : bf16_lo(pr);
+          in[k] = p >= t0 ? ((e & 1) ? bf16_hi(pr) : bf16_lo(pr)) : bf(st[3 * e + p - t0 + 3]);
         }
-        y[e] = round_bf(w[e][0] * in[0] + w[e][1] * in[1] + w[e][2] * in[2] + w[e][3] * in[3]);
-        y[e] = y[e] / (1.f + expf(-y[e]));
+        y[e] = silu_lookup(
+            round_bf(w[e][0] * in[0] + w[e][1] * in[1] + w[e][2] * in[2] + w[e][3] * in[3]), tab);
       }
-      *reinterpret_cast<u32x2*>(a.ws + (int64_t)(tb + i) * a.conv_dim + c) =
-          u32x2{pack_bf16(y[0], y[1]), pack_bf16(y[2], y[3])};
+      *reinterpret_cast<u32x2*>(a.ws + (int64_t)tt * a.conv_dim + c) =
+          u32x2{y[0] | (y[1] << 16), y[2] | (y[3] << 16)};
     }
-    return;
-  }
-#pragma unroll
-  for (int i = 0; i < kConvTokens; ++i) {
-    const int tt = tb + i;
-    if (tt >= a.rows) break;
-    const int bi = a.owner[tt];
-    if (bi < 0) continue;
-    const int t0 = min(max(a.tok[bi], 0), a.rows);
-    const int64_t r = a.req[bi];
-    const uint16_t* st = a.conv_state + r * a.conv_ss + 3 * (int64_t)c;
-    float y[kConvCh];
-#pragma unroll
-    for (int e = 0; e < kConvCh; ++e) {
-      float in[4];
-#pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        const int p = tt - 3 + k;   // input position; before t0 it is in the conv state
-        const uint32_t pr = x[i + k][e >> 1];
-        in[k] = p >= t0 ? ((e & 1) ? bf16_hi(pr) : bf16_lo(pr)) : bf(st[3 * e + p - t0 + 3]);
-      }
-      y[e] = round_bf(w[e][0] * in[0] + w[e][1] * in[1] + w[e][2] * in[2] + w[e][3] * in[3]);
-      y[e] = y[e] / (1.f + expf(-y[e]));   // F.silu (accurate exp: q / k / v feed everything)
-    }
-    *reinterpret_cast<u32x2*>(a.ws + (int64_t)tt * a.conv_dim + c) =
-        u32x2{pack_bf16(y[0], y[1]), pack_bf16(y[2], y[3])};
   }
 }
 
@@ -1123,10 +1157,10 @@ int64_t gdn_ext_row_bytes(int32_t hk, int32_t hv) {
 }
 // Chunk-record slots: chunk ci of request b is slot floor(t0_b / 32) + b + ci.
 int64_t gdn_chunk_slots(int64_t n_tokens, int32_t batch) { return n_tokens / kChunk + batch + 1; }
-// Per-token rows (16-byte aligned), then the chunk records.
+// Per-token rows (16-byte aligned), then the chunk records, then the SiLU table.
 int64_t gdn_ext_ws_bytes(int64_t n_tokens, int32_t batch, int32_t hk, int32_t hv) {
   return ((n_tokens * gdn_ext_row_bytes(hk, hv) + 64) & ~15LL) +
-         gdn_chunk_slots(n_tokens, batch) * hv * kRec * 4;
+         gdn_chunk_slots(n_tokens, batch) * hv * kRec * 4 + kSiluTab * 2;
 }
 }  // namespace tfa
 
@@ -1207,6 +1241,7 @@ int32_t gdn_setup(const char* fn, const void* qkv, int64_t qkv_row_stride, const
   g->wqk = nullptr;
   g->wg = nullptr;
   g->owner = nullptr;
+  g->silu_tab = nullptr;
   g->wrec = nullptr;
   g->ws = static_cast<uint16_t*>(workspace);
   g->out = static_cast<uint16_t*>(out);
@@ -1389,13 +1424,17 @@ int32_t tf_gdn_extend(const void* qkv, int64_t qkv_row_stride, const void* a, co
   g.owner = reinterpret_cast<int32_t*>(reinterpret_cast<uint8_t*>(g.wg) + gate_bytes);
   g.wrec = reinterpret_cast<float*>(w + ((n_tokens * gdn_ext_row_bytes(num_k_heads, num_v_heads) +
                                           64) & ~15LL));
+  g.silu_tab = reinterpret_cast<uint16_t*>(g.wrec + n_slots_rec * num_v_heads * kRec);
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   const uint32_t cblocks = (g.conv_dim + kThreads - 1) / kThreads;
   const uint32_t tblocks = (uint32_t)((n_tokens + kConvTokens - 1) / kConvTokens);
-  hipLaunchKernelGGL(gdn_owner_kernel, dim3((uint32_t)((n_tokens + kThreads - 1) / kThreads)),
+  hipLaunchKernelGGL(gdn_owner_kernel,
+                     dim3((uint32_t)((std::max<int64_t>(n_tokens, kSiluTab) + kThreads - 1) /
+                                     kThreads)),
                      dim3(kThreads), 0, s, g);
   hipLaunchKernelGGL(gdn_conv_ext_kernel,
-                     dim3((g.conv_dim / kConvCh + kThreads - 1) / kThreads, tblocks),
+                     dim3((g.conv_dim / kConvCh + kThreads - 1) / kThreads,
+                          std::min<uint32_t>(tblocks, kConvRowWgs)),
                      dim3(kThreads), 0, s, g);
   hipLaunchKernelGGL(gdn_conv_state_kernel, dim3(cblocks, batch_size), dim3(kThreads), 0, s, g);
   if (g.dk != kDk) {   // other head dims: every request's rows in one wave per value head
