@@ -60,7 +60,30 @@ def check_outputs(got, want, what):
     assert bad <= max(1, g.numel() // 1000), f"{what}: {bad} elements off by more than 1 ulp"
 
 
-@pytest.mark.parametrize("bsz,hk,hv", [(1, 16, 48), (7, 16, 48), (64, 16, 48), (9, 4, 12)])
+def check_chunked_outputs(got, want, what, normed):
+    """Outputs of the chunked extend form against the oracle's sequence.  Their
+    fp32 sums differ by about 1e-6 of the largest output, which for outputs
+    below 1/256 of the largest exceeds their own bf16 ulp, so the ulp is taken
+    of max(|w|, max|w| / 256).  The pre-norm output (bf16(o)) must be within one
+    such ulp everywhere (up to 1e-4 of the elements beyond it); the normed
+    output within two, as a one-ulp flip of bf16(o) carries through the norm,
+    and at most 0.1 % beyond one."""
+    g, w = got.float(), want.float()
+    amax = float(w.abs().max())
+    ulp = torch.clamp(w.abs(), min=max(amax / 256, 2.0 ** -126)) * 2.0 ** -7
+    d = (g - w).abs()
+    worst = float((d / ulp).max())
+    one = int((d > ulp).sum())
+    if normed:
+        assert worst <= 2.0, f"{what}: an element off by {worst:.2f} floored ulps"
+        assert one <= max(1, g.numel() // 1000), f"{what}: {one} elements beyond 1 floored ulp"
+    else:
+        assert one <= max(1, g.numel() // 10000), f"{what}: {one} elements beyond 1 floored ulp"
+
+
+@pytest.mark.parametrize("bsz,hk,hv", [(1, 16, 48), (7, 16, 48), (64, 16, 48), (9, 4, 12),
+                                        # one, two and four value heads per key head
+                                        (5, 8, 8), (6, 4, 8), (3, 2, 8)])
 def test_decode_steps_match_oracle(gpu, bsz, hk, hv):
     print(f"[gdn] B={bsz} Hk={hk} Hv={hv}", flush=True)
     n_slots = bsz + 5
@@ -134,7 +157,10 @@ def test_decode_misaligned_rows_match_oracle(gpu):
 @pytest.mark.parametrize("lens,hk,hv", [([5], 16, 48), ([1, 70, 3, 130], 16, 48),
                                          ([200, 1, 1, 64, 2], 4, 12),
                                          # 32-token chunk edges: exact, one over, one short
-                                         ([32, 64, 33, 31, 1, 2], 4, 12)])
+                                         ([32, 64, 33, 31, 1, 2], 4, 12),
+                                         # one, two and four value heads per key head
+                                         ([40, 1, 7], 8, 8), ([3, 66, 1], 4, 8),
+                                         ([1, 35], 2, 8)])
 def test_extend_matches_oracle(gpu, lens, hk, hv):
     """Mixed extend lengths against the oracle's per-request loop (chunked WY
     update for ext > 1): two consecutive calls, the second with other lengths.
@@ -164,8 +190,8 @@ def test_extend_matches_oracle(gpu, lens, hk, hv):
         scale = float(ssm_state.abs().max())
         close_fraction(ss_gpu.cpu(), ssm_state, 2e-4 * scale, 1e-2 * scale, 1e-3,
                        f"{what}: ssm state")
-        check_outputs(core.cpu(), want_core, f"{what}: pre-norm output")
-        check_outputs(out.cpu(), want_out, f"{what}: normed output")
+        check_chunked_outputs(core.cpu(), want_core, f"{what}: pre-norm output", False)
+        check_chunked_outputs(out.cpu(), want_out, f"{what}: normed output", True)
 
 
 def test_extend_of_single_tokens_equals_decode(gpu):
