@@ -48,6 +48,9 @@ def test_restatement_matches_oracle_at_head_dim_256_with_shared_prefixes():
 
 
 # ----------------------------------------------------------------- closed forms
+# Each pin takes the attention under test, the head dim of its cases and an
+# absolute tolerance (None: the fp32 oracles' own); the HIP path runs the same
+# pins in bf16 (tests/test_gpu_pins.py).
 
 def _visible_slots(wl, b, t):
     """Slot ids visible to new token t of request b (positions 0 .. P + t)."""
@@ -57,20 +60,20 @@ def _visible_slots(wl, b, t):
     return [max(int(rtt[wl.rows[b], k]), 0) for k in range(P + t + 1)]
 
 
-def pin_single_key_returns_value(attn):
-    wl = small_case([1, 1, 1], [1, 1, 1], hq=4, hkv=2, d=16, seed=4)
+def pin_single_key_returns_value(attn, d=16, atol=None):
+    wl = small_case([1, 1, 1], [1, 1, 1], hq=4, hkv=2, d=d, seed=4)
     out = attn(wl)
     vp = wl.v_pool.numpy()
     for b in range(3):
         slot = _visible_slots(wl, b, 0)[0]
         for h in range(4):
-            if not np.allclose(out[b, h], vp[slot, h // 2], atol=1e-6):
+            if not np.allclose(out[b, h], vp[slot, h // 2], atol=1e-6 if atol is None else atol):
                 return False
     return True
 
 
-def pin_equal_keys_average_visible_values(attn):
-    wl = small_case([10, 7, 13], [4, 1, 6], hq=4, hkv=2, d=16, seed=5)
+def pin_equal_keys_average_visible_values(attn, d=16, atol=None):
+    wl = small_case([10, 7, 13], [4, 1, 6], hq=4, hkv=2, d=d, seed=5)
     wl.k_pool[:] = wl.k_pool[1:2].clone()          # every key row identical
     out = attn(wl)
     vp = wl.v_pool.numpy().astype(np.float64)
@@ -80,15 +83,15 @@ def pin_equal_keys_average_visible_values(attn):
             slots = _visible_slots(wl, b, t)
             for h in range(4):
                 want = vp[slots, h // 2].mean(axis=0)
-                if not np.allclose(out[row, h], want, atol=1e-5):
+                if not np.allclose(out[row, h], want, atol=1e-5 if atol is None else atol):
                     return False
             row += 1
     return True
 
 
-def pin_dominant_key_selects_its_value(attn):
+def pin_dominant_key_selects_its_value(attn, d=16, atol=None):
     """q of head h aligned with one key of kv head h // G: softmax ~ one-hot."""
-    wl = small_case([9, 12], [3, 1], hq=4, hkv=2, d=16, seed=6)
+    wl = small_case([9, 12], [3, 1], hq=4, hkv=2, d=d, seed=6)
     rng = np.random.default_rng(0)
     row = 0
     targets = []
@@ -109,11 +112,12 @@ def pin_dominant_key_selects_its_value(attn):
         wl.q[row, h] = key / key.norm() * 400.0
     out = attn(wl)
     vp = wl.v_pool.numpy()
-    return all(np.allclose(out[row, h], vp[s, h // 2], atol=1e-4) for row, h, s in targets)
+    tol = 1e-4 if atol is None else atol
+    return all(np.allclose(out[row, h], vp[s, h // 2], atol=tol) for row, h, s in targets)
 
 
-def pin_slot_permutation_invariance(attn):
-    wl = small_case([11, 6], [4, 1], hq=4, hkv=1, d=16, seed=7, pool=64)
+def pin_slot_permutation_invariance(attn, d=16, atol=None):
+    wl = small_case([11, 6], [4, 1], hq=4, hkv=1, d=d, seed=7, pool=64)
     base = attn(wl)
     perm = torch.randperm(63, generator=torch.Generator().manual_seed(3)) + 1
     new_of_old = torch.zeros(64, dtype=torch.long)
@@ -124,43 +128,43 @@ def pin_slot_permutation_invariance(attn):
     rtt = wl.batch.req_to_token
     live = rtt >= 0
     rtt[live] = new_of_old[rtt[live]]
-    return np.allclose(attn(wl), base, atol=1e-6)
+    return np.allclose(attn(wl), base, atol=1e-6 if atol is None else atol)
 
 
-def pin_prefix_extend_equals_full_prefill_rows(attn):
+def pin_prefix_extend_equals_full_prefill_rows(attn, d=16, atol=None):
     """A request whose first P positions are a cached prefix gives the same rows
     as a fresh prefill of all P + N tokens (the reference's own equivalence)."""
     P, N = 9, 5
-    full = small_case([P + N], [P + N], hq=4, hkv=2, d=16, seed=8)
+    full = small_case([P + N], [P + N], hq=4, hkv=2, d=d, seed=8)
     ref = attn(full)
     ext = rebatch(full, [P + N], [N], full.q[P:].clone())
-    return np.allclose(attn(ext), ref[P:], atol=1e-6)
+    return np.allclose(attn(ext), ref[P:], atol=1e-6 if atol is None else atol)
 
 
-def pin_chunked_extend_equals_one_shot(attn):
+def pin_chunked_extend_equals_one_shot(attn, d=16, atol=None):
     P, N1, N2 = 6, 4, 3
-    one = small_case([P + N1 + N2, 5], [N1 + N2, 1], hq=4, hkv=1, d=16, seed=9)
+    one = small_case([P + N1 + N2, 5], [N1 + N2, 1], hq=4, hkv=1, d=d, seed=9)
     ref = attn(one)
     a = rebatch(one, [P + N1, 5], [N1, 1], torch.cat([one.q[:N1], one.q[N1 + N2:]]))
     b = rebatch(one, [P + N1 + N2, 5], [N2, 1], torch.cat([one.q[N1:N1 + N2],
                                                            one.q[N1 + N2:]]))
     got = np.concatenate([attn(a)[:N1], attn(b)[:N2]])
-    return np.allclose(got, ref[:N1 + N2], atol=1e-6)
+    return np.allclose(got, ref[:N1 + N2], atol=1e-6 if atol is None else atol)
 
 
-def pin_decode_equals_last_prefill_row(attn):
+def pin_decode_equals_last_prefill_row(attn, d=16, atol=None):
     L = 10
-    pre = small_case([L, 4], [L, 1], hq=4, hkv=2, d=16, seed=10)
+    pre = small_case([L, 4], [L, 1], hq=4, hkv=2, d=d, seed=10)
     ref = attn(pre)
     dec = rebatch(pre, [L, 4], [1, 1], torch.stack([pre.q[L - 1], pre.q[L]]))
-    return np.allclose(attn(dec)[0], ref[L - 1], atol=1e-6)
+    return np.allclose(attn(dec)[0], ref[L - 1], atol=1e-6 if atol is None else atol)
 
 
-def pin_two_keys_logistic_weight(attn):
+def pin_two_keys_logistic_weight(attn, d=16, atol=None):
     """Two visible keys and a one-hot query: the weight of key 0 is the logistic
     function 1 / (1 + exp(scale * c * (x1 - x0))) of the score gap."""
     import math
-    wl = small_case([2, 2], [1, 1], hq=2, hkv=1, d=16, seed=12, scale=0.3)
+    wl = small_case([2, 2], [1, 1], hq=2, hkv=1, d=d, seed=12, scale=0.3)
     rtt = wl.batch.req_to_token.numpy()
     for b in range(2):
         s0, s1 = (int(rtt[wl.rows[b], k]) for k in range(2))
@@ -176,7 +180,7 @@ def pin_two_keys_logistic_weight(attn):
         for h, c in enumerate((2.0, -1.0)):
             w0 = 1.0 / (1.0 + math.exp(0.3 * c * (x1 - x0)))
             want = w0 * vp[s0, 0] + (1 - w0) * vp[s1, 0]
-            if not np.allclose(out[b, h], want, atol=1e-5):
+            if not np.allclose(out[b, h], want, atol=1e-5 if atol is None else atol):
                 return False
     return True
 
