@@ -113,6 +113,37 @@ def gemm_case(gpu, m, n, k, bh=128, bw=128, bias=False, no_scales=False, out_str
     print(f"[fp8 gemm] max |err| {float(err.max()):.3e}, worst/bound {worst:.3f}", flush=True)
 
 
+@pytest.mark.parametrize("m,bh", [(8, 128), (64, 128), (300, 128), (1100, 128), (64, 96),
+                                  (1100, 96)])
+def test_gemm_scale_indexing_closed_form(gpu, m, bh):
+    """Row r of xq holds 1.0 at one column of K block kb0[r] and 2.0 at one of
+    another block kb1[r]; the weights are all 1.0, x_scale is 0.25 and the block
+    scales are distinct powers of two.  Then out[r, n] = 0.25 (ws[n / bh, kb0] +
+    2 ws[n / bh, kb1]) is exact in fp32 and the kernel must return its bf16
+    rounding bit for bit; a transposed or shifted scale index, or a K slice
+    taken from the wrong place, changes the powers."""
+    print(f"[fp8 gemm] closed form m={m} bh={bh}", flush=True)
+    n, k = 640, 1024
+    nb, kb = -(-n // bh), k // 128
+    e = (torch.arange(nb)[:, None] * 3 + torch.arange(kb)[None, :] * 5) % 11 - 5
+    ws = torch.pow(2.0, e.double())
+    g = torch.Generator().manual_seed(m + bh)
+    kb0 = torch.randint(0, kb, (m,), generator=g)
+    kb1 = (kb0 + torch.randint(1, kb, (m,), generator=g)) % kb
+    x = torch.zeros((m, k))
+    rows = torch.arange(m)
+    x[rows, kb0 * 128 + torch.randint(0, 128, (m,), generator=g)] = 1.0
+    x[rows, kb1 * 128 + torch.randint(0, 128, (m,), generator=g)] = 2.0
+    xq = x.to(torch.float8_e4m3fn).to(gpu)
+    wq = torch.ones((n, k)).to(torch.float8_e4m3fn).to(gpu)
+    sx = torch.tensor([0.25], device=gpu)
+    got = fl.block_fp8_gemm(xq, sx, wq, ws.float().to(gpu), None, bh, 128)
+    torch.cuda.synchronize()
+    nblk = torch.arange(n) // bh
+    want = 0.25 * (ws[nblk[None, :], kb0[:, None]] + 2.0 * ws[nblk[None, :], kb1[:, None]])
+    assert torch.equal(got.cpu(), want.to(torch.bfloat16)), "outputs differ from the closed form"
+
+
 @pytest.mark.parametrize("m", [1, 8, 32, 33, 64, 100, 128, 129, 300])
 def test_gemm_oproj_shape(gpu, m):
     # o_proj of one GPU: in = 24 heads x 256, out = hidden 5120
