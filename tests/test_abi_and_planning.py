@@ -98,6 +98,28 @@ def test_entry_points_reject_bad_arguments_before_launching():
     assert lib.tf_gather_kv(None, 0, 16, 512, None, 1, 16, 16, None, 0, 5, None, None) == 0
 
 
+def test_gdn_decode_workspace_holds_conv_outputs_and_gates():
+    """The decode workspace is the bf16 conv outputs [B, conv_dim] followed by
+    the fp32 gates [B, Hv, 2], 16-byte aligned; a smaller or misaligned one is
+    rejected before anything is launched (the pointers below are never used)."""
+    lib = _native.load()
+    bsz, hk, hv = 4, 16, 48
+    conv_dim = 2 * hk * 128 + hv * 128
+    need = bsz * (conv_dim * 2 + hv * 8)
+    assert lib.tf_gdn_decode_workspace_bytes(bsz, hk, hv) == need
+    p = 1 << 20   # a 16-byte aligned stand-in address for every tensor
+
+    def call(ws, ws_bytes):
+        return lib.tf_gdn_decode(p, conv_dim, p, p, hv, p, hv * 128, p, p, p, p, 1e-6,
+                                 p, 3 * conv_dim, p, hv * 128 * 128, p, bsz, 8, hk, hv, 128,
+                                 128, 4, p, hv * 128, None, 0, ws, ws_bytes, None)
+
+    assert call(p, need - 1) == _native.TF_ERR_INVALID        # no room for the gates
+    assert b"workspace" in lib.tf_attn_last_error()
+    assert call(p + 8, need) == _native.TF_ERR_INVALID        # 8-byte aligned only
+    assert b"16-byte aligned" in lib.tf_attn_last_error()
+
+
 def _expected_extend_items(lens, hq, hkv, skip_decode):
     g = hq // hkv
     starts = np.concatenate([[0], np.cumsum(lens)[:-1]])
