@@ -160,7 +160,9 @@ def test_decode_misaligned_rows_match_oracle(gpu):
                                          ([32, 64, 33, 31, 1, 2], 4, 12),
                                          # one, two and four value heads per key head
                                          ([40, 1, 7], 8, 8), ([3, 66, 1], 4, 8),
-                                         ([1, 35], 2, 8)])
+                                         ([1, 35], 2, 8),
+                                         # eight: two passes of the prep's head loop
+                                         ([5, 40], 1, 8)])
 def test_extend_matches_oracle(gpu, lens, hk, hv):
     """Mixed extend lengths against the oracle's per-request loop (chunked WY
     update for ext > 1): two consecutive calls, the second with other lengths.

@@ -585,7 +585,7 @@ __device__ __forceinline__ f32x16 mma3(f32x16 c, const u32x4& ah, const u32x4& a
 struct PrepSmem {
   float kk[kChunk][kChunk + 1];    // k_t . k_s
   float qq[kChunk][kChunk + 1];    // q_t . k_s
-  float am[4][kChunk][36];         // A of the value head each wave solves (16-B rows)
+  float am[4][kChunk][36];         // A of the value head each half-wave solves (16-B rows)
 };
 
 __global__ void __launch_bounds__(kThreads, 4) gdn_chunk_prep_kernel(GdnArgs a) {
@@ -630,8 +630,12 @@ __global__ void __launch_bounds__(kThreads, 4) gdn_chunk_prep_kernel(GdnArgs a) 
   }
   __syncthreads();
 
-  for (int v = w; v < a.vpk; v += kThreads / kWave) {
-    const int h = hk * a.vpk + v;
+  // Each half-wave of waves 0 and 1 takes one value head (lanes n of half g);
+  // four heads per pass.
+  for (int v0 = 2 * w; w < 2 && v0 < a.vpk; v0 += 4) {
+    const int v = v0 + g;
+    const bool act = v < a.vpk;
+    const int h = hk * a.vpk + min(v, a.vpk - 1);
     float* rec = a.wrec + ((int64_t)slot * a.hv + h) * kRec;
     const float2 gbv = *reinterpret_cast<const float2*>(a.wg + ((int64_t)min(tb + n, last) * a.hv + h) * 2);
     const float gn = n < ntok ? gbv.x : 0.f, bn = n < ntok ? gbv.y : 0.f;
@@ -642,8 +646,8 @@ __global__ void __launch_bounds__(kThreads, 4) gdn_chunk_prep_kernel(GdnArgs a) 
       if (n >= off) x += y;
     }
     const float gc = __shfl(x, kChunk - 1, 32);
-    float (*A)[36] = sm.am[w];
-    if (g == 0) {
+    float (*A)[36] = sm.am[2 * w + g];
+    if (act) {
       rec[kRecC + n] = __expf(x);
       rec[kRecD + n] = __expf(gc - x);
       rec[kRecBeta + n] = bn;
@@ -653,14 +657,14 @@ __global__ void __launch_bounds__(kThreads, 4) gdn_chunk_prep_kernel(GdnArgs a) 
     for (int t = 0; t < kChunk; ++t) {
       const float gt = __shfl(x, t, 32), bt = __shfl(bn, t, 32);
       const float e = __expf(fminf(gt - x, 0.f));
-      if (g == 0) {
+      if (act) {
         A[t][n] = n < t ? bt * e * sm.kk[t][n] : 0.f;
         rec[kRecB + t * kChunk + n] = n <= t ? e * sm.qq[t][n] : 0.f;
       }
     }
     // this wave's writes of A before its reads (one wave: no barrier needed)
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-    if (g == 0) {   // T = (I + A)^-1 by forward substitution, lane n owns column n;
+    if (act) {      // T = (I + A)^-1 by forward substitution, lane n owns column n;
                     // each row's sum in four interleaved partial sums (shorter FMA chains)
       float tc[kChunk];
 #pragma unroll
