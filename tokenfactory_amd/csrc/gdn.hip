@@ -282,8 +282,8 @@ __global__ void __launch_bounds__(kThreads) gdn_recur_kernel(GdnArgs a) {
 // Requests with several new tokens (the reference's per-request loop,
 // linear_attention.py:328-364): the conv runs over the flattened batch in
 // parallel (kConvTokens rows x kConvCh channels per thread, inputs before a
-// request's first row taken from its conv state, which is shifted afterwards
-// by its own kernel); per 32-token chunk the WY quantities are prepared for all
+// request's first row taken from its conv state, which the q / k kernel
+// shifts afterwards); per 32-token chunk the WY quantities are prepared for all
 // chunks at once; then one workgroup per (request, value head) carries the
 // head's state in MFMA accumulators from the first chunk to the last (one state
 // read and one write per request and head) and applies the gated norm to the
@@ -338,9 +338,9 @@ constexpr int kConvCh = 4;   // channels per thread in the extend conv
 // thread (grid: channel blocks x a stride of kConvTokens-row blocks over the
 // flattened batch; the SiLU table is copied to LDS once per workgroup).
 // Each token's window takes the inputs before its request's first token from
-// the request's conv state, which this kernel only reads;
-// gdn_conv_state_kernel shifts it afterwards.  Rows of requests whose slot is
-// outside the pool are skipped.
+// the request's conv state, which this kernel only reads; gdn_qk_ext_kernel
+// (head dims 128) or gdn_conv_state_kernel shifts it afterwards.  Rows of
+// requests whose slot is outside the pool are skipped.
 constexpr int kConvRowWgs = 192;   // workgroups per channel block (row-block stride)
 
 __global__ void __launch_bounds__(kThreads) gdn_conv_ext_kernel(GdnArgs a) {
@@ -417,9 +417,7 @@ __global__ void __launch_bounds__(kThreads) gdn_conv_ext_kernel(GdnArgs a) {
 
 // Conv state <- the last 3 inputs of each request (after gdn_conv_ext_kernel
 // has read the old state).
-__global__ void __launch_bounds__(kThreads) gdn_conv_state_kernel(GdnArgs a) {
-  const int c = blockIdx.x * kThreads + threadIdx.x, bi = blockIdx.y;
-  if (c >= a.conv_dim) return;
+__device__ __forceinline__ void conv_state_shift(const GdnArgs& a, int bi, int c) {
   const int64_t r = a.req[bi];
   if (r < 0 || r >= a.n_slots) return;
   const int t0 = min(max(a.tok[bi], 0), a.rows), t1 = min(max(a.tok[bi + 1], t0), a.rows);
@@ -432,6 +430,19 @@ __global__ void __launch_bounds__(kThreads) gdn_conv_state_kernel(GdnArgs a) {
   }
 #pragma unroll
   for (int i = 0; i < 3; ++i) st[i] = x[i];
+}
+
+__global__ void __launch_bounds__(kThreads) gdn_conv_state_kernel(GdnArgs a) {
+  const int c = blockIdx.x * kThreads + threadIdx.x;
+  if (c < a.conv_dim) conv_state_shift(a, blockIdx.y, c);
+}
+
+// Zeros of token row tok (a row of no request or of an out-of-pool slot).
+__device__ __forceinline__ void zero_row(const GdnArgs& a, int64_t tok, int i0, int step) {
+  for (int d = 4 * i0; d < a.hv * a.dv; d += 4 * step) {
+    *reinterpret_cast<u32x2*>(a.out + tok * a.out_rs + d) = u32x2{0u, 0u};
+    if (a.core) *reinterpret_cast<u32x2*>(a.core + tok * a.core_rs + d) = u32x2{0u, 0u};
+  }
 }
 
 // Per (token, key head): q / k of the head normalised (F.normalize, eps
@@ -497,6 +508,14 @@ __global__ void __launch_bounds__(kThreads) gdn_qk_ext_kernel(GdnArgs a) {
     gt[0] = -expf(a.a_log[h]) * sp;                            // g = log alpha
     gt[1] = 1.f / (1.f + expf(-bf(a.b[tok * a.ab_rs + h])));
   }
+  // Two small jobs that only need the conv's reads of the old conv states to
+  // be done: zero rows of skipped token rows, and shift the conv states
+  // (every request's last 3 inputs), strided over the first blocks.
+  if (a.owner[tok] < 0) zero_row(a, tok, threadIdx.x, kThreads);
+  const int64_t n_shift = (int64_t)a.batch * a.conv_dim;
+  for (int64_t i = (int64_t)tok * kThreads + threadIdx.x; i < n_shift;
+       i += (int64_t)gridDim.x * kThreads)
+    conv_state_shift(a, (int)(i / a.conv_dim), (int)(i % a.conv_dim));
 }
 
 // global_load_lds_dwordx4 with a scalar base and a 32-bit lane offset: lane
@@ -1034,7 +1053,7 @@ __global__ void __launch_bounds__(kChunkThreads) gdn_chunk_ext_kernel(GdnArgs a)
 // (rms_norm_gated.py:26-40) in the same wave.  Conv outputs come from
 // gdn_conv_kernel (decode: row = request) or gdn_conv_ext_kernel (extend).
 // Decode: a request whose slot is outside the pool gets zero rows here;
-// extend: gdn_zero_ext_kernel writes them.
+// extend: gdn_qk_ext_kernel / gdn_zero_ext_kernel write them.
 constexpr int kGenD = 64;
 constexpr int kGenWaves = kThreads / kWave;
 
@@ -1125,11 +1144,7 @@ constexpr int kZeroRows = kThreads / kWave;   // rows per workgroup
 __global__ void __launch_bounds__(kThreads) gdn_zero_ext_kernel(GdnArgs a) {
   const int64_t tok = (int64_t)blockIdx.x * kZeroRows + wave_id();
   if (tok >= a.rows || a.owner[tok] >= 0) return;
-  const int lane = threadIdx.x & (kWave - 1);
-  for (int d = 4 * lane; d < a.hv * a.dv; d += 4 * kWave) {
-    *reinterpret_cast<u32x2*>(a.out + tok * a.out_rs + d) = u32x2{0u, 0u};
-    if (a.core) *reinterpret_cast<u32x2*>(a.core + tok * a.core_rs + d) = u32x2{0u, 0u};
-  }
+  zero_row(a, tok, threadIdx.x & (kWave - 1), kWave);
 }
 
 }  // namespace
@@ -1440,8 +1455,9 @@ int32_t tf_gdn_extend(const void* qkv, int64_t qkv_row_stride, const void* a, co
                      dim3((g.conv_dim / kConvCh + kThreads - 1) / kThreads,
                           std::min<uint32_t>(tblocks, kConvRowWgs)),
                      dim3(kThreads), 0, s, g);
-  hipLaunchKernelGGL(gdn_conv_state_kernel, dim3(cblocks, batch_size), dim3(kThreads), 0, s, g);
   if (g.dk != kDk) {   // other head dims: every request's rows in one wave per value head
+    hipLaunchKernelGGL(gdn_conv_state_kernel, dim3(cblocks, batch_size), dim3(kThreads), 0, s,
+                       g);
     hipLaunchKernelGGL(gdn_generic_kernel,
                        dim3((uint32_t)(((int64_t)batch_size * num_v_heads + kGenWaves - 1) /
                                        kGenWaves)),
@@ -1489,8 +1505,6 @@ int32_t tf_gdn_extend(const void* qkv, int64_t qkv_row_stride, const void* a, co
   }
   hipLaunchKernelGGL(gdn_chunk_ext_kernel, dim3((int64_t)batch_size * num_v_heads),
                      dim3(kChunkThreads), 0, s, g);
-  hipLaunchKernelGGL(gdn_zero_ext_kernel, dim3((uint32_t)((n_tokens + kZeroRows - 1) / kZeroRows)),
-                     dim3(kThreads), 0, s, g);
   if (lane) {
     const hipError_t e = hipStreamWaitEvent(s, lane->join, 0);
     if (e != hipSuccess) return side_failure("join with the side stream", e);
