@@ -474,14 +474,15 @@ int32_t tf_gdn_decode(const void* qkv, int64_t qkv_row_stride, const void* a, co
  * each request's conv runs over [conv_state, its tokens] and its state is
  * carried through its tokens in order.  The state update is the reference's
  * chunk-wise WY form (:194-242) with 32-token chunks (the same recurrence as
- * token by token, equal up to fp32 rounding).  Eight launches: the request
- * of every token row, the conv for every (token, channel) in parallel, the
- * conv-state shift, normalised q / k and the gates for every token in
- * parallel, the state-independent part of every chunk in parallel, the
- * one-token requests' update (as in tf_gdn_decode), the chunked recurrence
+ * token by token, equal up to fp32 rounding).  Six launches: the request
+ * of every token row, the conv for every (token, channel) in parallel,
+ * normalised q / k and the gates for every token in parallel (with the
+ * conv-state shift and zeros for the rows of no request or of an out-of-pool
+ * slot), the state-independent part of every chunk in parallel, the
+ * one-token requests' update (as in tf_gdn_decode) and the chunked recurrence
  * with the gated norm of its rows (one workgroup per request of two or more
- * tokens and value head, its state in registers from first chunk to last),
- * and zeros for the rows of no request or of an out-of-pool slot.  When the
+ * tokens and value head, its state in registers from first chunk to last).
+ * When the
  * batch can hold both kinds of request (batch_size > 1, max_extend_len > 1),
  * the one-token update of a call that is not under graph capture runs on a
  * second stream of the library's (one per device, made on the first such
