@@ -359,6 +359,45 @@ def test_extend_strided_views_and_graph_replay(gpu):
         float(torch.randn(1 << 16, device=gpu).sum())   # eager work between replays
 
 
+def test_decode_graph_replay(gpu):
+    """A decode step captured in a HIP graph (its output and workspace from the
+    graph's pool) and replayed over new inputs three times, with eager work
+    between the replays: every replay equals an eager step over the same
+    inputs and states bit for bit (outputs, conv and ssm states)."""
+    hk, hv, bsz, n_slots = 16, 48, 8, 12
+    conv_dim = 2 * hk * 128 + hv * 128
+    g = torch.Generator().manual_seed(321)
+    cs = torch.randn((n_slots, conv_dim, 3), generator=g).to(torch.bfloat16).to(gpu)
+    ss = (torch.randn((n_slots, hv, 128, 128), generator=g) * 0.2).to(gpu)
+    cs_e, ss_e = cs.clone(), ss.clone()
+    req = torch.randperm(n_slots, generator=g)[:bsz].to(gpu)
+    gp = [p.to(gpu) for p in make_params(hk, hv, 17)]
+    qkv, a, b, z = (x.to(gpu) for x in make_step(bsz, hk, hv, 40))
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):           # warm-up outside the capture
+        gdn_decode_step(qkv, b, a, z, *gp, 1e-6, cs.clone(), ss.clone(), req, hk, hv)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        out_g, core_g = gdn_decode_step(qkv, b, a, z, *gp, 1e-6, cs, ss, req, hk, hv,
+                                        return_core=True)
+    torch.cuda.synchronize()
+    for r in range(3):
+        nq, na, nb, nz = (x.to(gpu) for x in make_step(bsz, hk, hv, 50 + r))
+        for dst, src in ((qkv, nq), (a, na), (b, nb), (z, nz)):
+            dst.copy_(src)
+        graph.replay()
+        want_out, want_core = gdn_decode_step(nq, nb, na, nz, *gp, 1e-6, cs_e, ss_e, req, hk,
+                                              hv, return_core=True)
+        torch.cuda.synchronize()
+        what = f"replay {r}"
+        assert torch.equal(out_g, want_out) and torch.equal(core_g, want_core), what
+        assert torch.equal(cs, cs_e) and torch.equal(ss, ss_e), f"{what}: states"
+        float(torch.randn(1 << 16, device=gpu).sum())   # eager work between replays
+
+
 def test_decode_out_of_pool_rows_are_zero(gpu):
     hk, hv, n_slots = 4, 12, 6
     conv_dim = 2 * hk * 128 + hv * 128
